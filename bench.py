@@ -1,0 +1,278 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused QKV + QK-Norm + RoPE op on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
+
+Headline (``value``): BASELINE config 2, Qwen3-8B prefill B=4 x S=512 (2048
+tokens, hidden 4096, 32 Q heads, 8 KV heads, head_dim 128, bf16), tokens/s of
+mqk.fused_qkv_rope with every input resident in HBM.  One step = one call of the
+op (one kernel launch) on that batch; K steps are timed with HIP events on the
+stream the op launches on, bracketed by device synchronisation.
+
+``roofline`` prices the dominant (only) kernel of a step: 2*T*hidden*N FLOP per
+launch / average launch duration, against the bf16 dense MFMA peak (2.5
+PFLOP/s).  ``traffic`` is filled from the committed rocprofv3 PMC summary in
+profiles/ when present.  ``cpu_baseline`` times the oracle's restatement of the
+reference's unfused composition (3 projections -> per-head RMSNorm -> RoPE,
+fp32, numpy/BLAS) on the host for a bounded sample of the same workload.
+``secondary`` reports the other BASELINE configurations (decode, long prefill,
+W4A16) with their own roofline fractions; the decode step rotates 8 copies of
+the weights (400 MB, more than the 256 MB Infinity Cache) so it reads HBM.
+
+Synthetic data, seeded: x ~ N(0,1), W ~ N(0, 0.02), gammas 1 + N(0, 0.1),
+theta = 1e6 RoPE tables.  One GPU only (--gpus N>1 exits with a message).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "mini-qwen-llm_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+D = 128
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def flops(T, hidden, n_cols):
+    return 2.0 * T * hidden * n_cols
+
+
+def make_inputs(T, hidden, Hq, Hkv, rows, seed, dev, copies=1):
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(1, T, hidden, generator=g, device=dev).bfloat16()
+    ws = []
+    for _ in range(copies):
+        ws.append(tuple((torch.randn(h * D, hidden, generator=g, device=dev) * 0.02).bfloat16()
+                        for h in (Hq, Hkv, Hkv)))
+    gq = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).bfloat16()
+    gk = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).bfloat16()
+    import mqk
+    cos, sin = (t.to(dev).bfloat16() for t in mqk.rope_tables(D, rows))
+    return x, ws, gq, gk, cos, sin
+
+
+def time_steps(fn, steps, warmup):
+    """(ms per step, wall seconds) for `steps` calls after `warmup` untimed ones."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(steps):
+        fn(i)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / steps, wall
+
+
+def bench_prefill(S_total, B, S, hidden, Hq, Hkv, seed, steps, warmup, dev):
+    import mqk
+    x, ws, gq, gk, cos, sin = make_inputs(S_total, hidden, Hq, Hkv, S, seed, dev)
+    x = x.reshape(B, S, hidden)
+    wq, wk, wv = ws[0]
+    ms, wall = time_steps(lambda i: mqk.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin),
+                          steps, warmup)
+    return ms, wall
+
+
+def bench_decode(B, hidden, Hq, Hkv, seed, steps, warmup, dev, copies=8):
+    import torch
+    import mqk
+    x, ws, gq, gk, cos, sin = make_inputs(B, hidden, Hq, Hkv, 8192, seed, dev, copies)
+    g = torch.Generator(device=dev).manual_seed(seed + 1)
+    pos = torch.randint(0, 8192, (B,), generator=g, device=dev).to(torch.int32)
+    x = x.reshape(B, 1, hidden)
+
+    def step(i):
+        wq, wk, wv = ws[i % copies]
+        return mqk.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin, pos)
+    return time_steps(step, steps, warmup)
+
+
+def bench_w4a16(hidden, Hq, Hkv, seed, steps, warmup, dev):
+    """Config 5: 16 packed sequences, lengths U[1,1024], starts U[0,4096), int4
+    weights (group 128, fp16 scales U(0.005, 0.02), zeros U{0..15})."""
+    import torch
+    import mqk
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(1, 1025, (16,), generator=g)
+    starts = torch.randint(0, 4096, (16,), generator=g)
+    pos = torch.cat([s + torch.arange(int(n)) for s, n in zip(starts, lens)]).to(torch.int32)
+    T = int(lens.sum())
+    gd = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(1, T, hidden, generator=gd, device=dev).bfloat16()
+    projs = []
+    for h in (Hq, Hkv, Hkv):
+        N = h * D
+        qw = torch.randint(-2**31, 2**31 - 1, (hidden // 8, N), generator=gd, device=dev,
+                           dtype=torch.int64).to(torch.int32)
+        sc = (0.005 + 0.015 * torch.rand(hidden // 128, N, generator=gd, device=dev)).half()
+        qz = torch.randint(-2**31, 2**31 - 1, (hidden // 128, N // 8), generator=gd, device=dev,
+                           dtype=torch.int64).to(torch.int32)
+        projs.append((qw, sc, qz))
+    gq = (1 + 0.1 * torch.randn(D, generator=gd, device=dev)).bfloat16()
+    gk = (1 + 0.1 * torch.randn(D, generator=gd, device=dev)).bfloat16()
+    cos, sin = (t.to(dev).bfloat16() for t in mqk.rope_tables(D, 8192))
+    pos = pos.to(dev)
+    ms, _ = time_steps(lambda i: mqk.fused_qkv_rope_w4a16(x, *projs, gq, gk, cos, sin, pos),
+                       steps, warmup)
+    return ms, T
+
+
+def cpu_baseline(budget_s=12.0):
+    """Oracle restatement of the reference's unfused composition on the host, fp32.
+
+    Sample: one sequence of the headline workload (B=1, S=512 of the B=4 x S=512
+    batch; hidden 4096, 32/8 heads), repeated until ~budget_s of CPU time."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+    from oracle import qkv_rope_oracle as orc
+    rng = np.random.default_rng(0)
+    S, hidden, Hq, Hkv = 512, 4096, 32, 8
+    x = orc.round_bf16(rng.standard_normal((1, S, hidden), dtype=np.float32))
+    wq = orc.round_bf16(rng.standard_normal((Hq * D, hidden), dtype=np.float32) * 0.02)
+    wk = orc.round_bf16(rng.standard_normal((Hkv * D, hidden), dtype=np.float32) * 0.02)
+    wv = orc.round_bf16(rng.standard_normal((Hkv * D, hidden), dtype=np.float32) * 0.02)
+    gq = orc.round_bf16(1 + 0.1 * rng.standard_normal(D, dtype=np.float32))
+    gk = orc.round_bf16(1 + 0.1 * rng.standard_normal(D, dtype=np.float32))
+    cos, sin = orc.rope_tables(D, S)
+    times = []
+    t_start = time.perf_counter()
+    orc.unfused_composition(x, wq, wk, wv, gq, gk, cos, sin)  # warm-up
+    while True:
+        t0 = time.perf_counter()
+        orc.unfused_composition(x, wq, wk, wv, gq, gk, cos, sin)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s and len(times) >= 5:
+            break
+    med = sorted(times)[len(times) // 2]
+    threads = max([i.get("num_threads", 1) for i in threadpool_info()
+                   if i.get("user_api") == "blas"] or [1])
+    return {"value": round(S / med, 1), "unit": "tokens/s", "cores": int(threads),
+            "kind": "port",
+            "sample": f"oracle unfused fp32 composition (numpy/BLAS), B=1 x S=512 of the "
+                      f"B=4 x S=512 Qwen3-8B prefill, median of {len(times)} reps, "
+                      f"{med * 1e3:.1f} ms/rep"}
+
+
+def load_traffic(name):
+    f = ROOT / "profiles" / f"{name}.json"
+    if f.exists():
+        try:
+            return json.loads(f.read_text()).get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="mqk fused QKV + QK-Norm + RoPE benchmark")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-secondary", action="store_true", help="skip configs 3-5")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the op has no multi-GPU path); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+    import mqk
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    mqk.library()  # fail loudly before any timing if libmqk.so is missing
+
+    # ---- headline: config 2, Qwen3-8B prefill B=4 x S=512 ---------------------
+    B, S, hidden, Hq, Hkv = 4, 512, 4096, 32, 8
+    T = B * S
+    N = (Hq + 2 * Hkv) * D
+    log(f"[bench] config 2 prefill T={T} hidden={hidden} N={N}: {args.warmup} warmup + {args.steps} steps")
+    ms, wall = bench_prefill(T, B, S, hidden, Hq, Hkv, 1, args.steps, args.warmup, dev)
+    fl = flops(T, hidden, N)
+    achieved = fl / (ms * 1e-3) / 1e12
+    result = {
+        "metric": "fused QKV+QKNorm+RoPE tokens/s and % roofline (Qwen3-8B shapes, bf16, 1 GPU)",
+        "value": round(T / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded x~N(0,1), W~N(0,0.02), gamma 1+N(0,0.1), RoPE theta 1e6)",
+        "config": {"workload": "Qwen3-8B fused QKV+QK-Norm+RoPE prefill (BASELINE config 2)",
+                   "global_batch": B, "seq_len": S, "tokens": T, "hidden": hidden,
+                   "heads_q": Hq, "heads_kv": Hkv, "head_dim": D, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": load_traffic("qkv_tile_c2_prefill_traffic")},
+        "wall_s_timed": round(wall, 4),
+    }
+
+    if not args.no_secondary:
+        sec = {}
+        # config 3: decode B=64, weight-read bound
+        dms, _ = bench_decode(64, hidden, Hq, Hkv, 2, max(50, args.steps), 10, dev)
+        dbytes = (N * hidden * 2 + 64 * hidden * 2 + 64 * N * 2 + 64 * D * 2 * 2 + 2 * D * 2 + 64 * 4)
+        dgbs = dbytes / (dms * 1e-3) / 1e9
+        sec["config3_decode_b64"] = {"tokens_per_s": round(64 / (dms * 1e-3), 1),
+                                     "ms_per_step": round(dms, 6), "bound": "hbm",
+                                     "achieved_GBps": round(dgbs, 1),
+                                     "frac": round(dgbs / PEAK_HBM_GBS, 4)}
+        log(f"[bench] config 3 decode: {dms * 1e3:.2f} us, {dgbs:.0f} GB/s")
+        # config 4: 30B-A3B attention shapes, S=8192
+        h4, q4, kv4 = 2048, 32, 4
+        n4 = (q4 + 2 * kv4) * D
+        ms4, _ = bench_prefill(8192, 1, 8192, h4, q4, kv4, 3, 30, 5, dev)
+        a4 = flops(8192, h4, n4) / (ms4 * 1e-3) / 1e12
+        sec["config4_30b_a3b_s8192"] = {"tokens_per_s": round(8192 / (ms4 * 1e-3), 1),
+                                        "ms_per_step": round(ms4, 6), "bound": "mfma",
+                                        "achieved_TFLOPs": round(a4, 2),
+                                        "frac": round(a4 / PEAK_BF16_TFLOPS, 4)}
+        log(f"[bench] config 4: {ms4 * 1e3:.1f} us, {a4:.0f} TFLOP/s")
+        # config 5: W4A16 ragged continuous batch
+        ms5, T5 = bench_w4a16(hidden, Hq, Hkv, 4, 30, 5, dev)
+        a5 = flops(T5, hidden, N) / (ms5 * 1e-3) / 1e12
+        sec["config5_w4a16_ragged"] = {"tokens": T5, "tokens_per_s": round(T5 / (ms5 * 1e-3), 1),
+                                       "ms_per_step": round(ms5, 6), "bound": "mfma",
+                                       "achieved_TFLOPs": round(a5, 2),
+                                       "frac": round(a5 / PEAK_BF16_TFLOPS, 4)}
+        log(f"[bench] config 5 W4A16 T={T5}: {ms5 * 1e3:.1f} us, {a5:.0f} TFLOP/s")
+        result["secondary"] = sec
+
+    if not args.no_cpu:
+        log("[bench] cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline()
+    else:
+        result["cpu_baseline"] = None
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,157 @@
+/*
+ * mqk.h -- C ABI of the MI355X (gfx950) fused QKV projection + QK-Norm + RoPE
+ * library (libmqk.so).
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream passed
+ * as `void*` (a hipStream_t; NULL = the default stream).  bf16 tensors are
+ * passed as `mqk_bf16*` (the raw 16-bit pattern).  All tensors are dense and
+ * row-major ("contiguous" in PyTorch terms).  Calls are asynchronous on the
+ * given stream, never synchronize, never allocate device memory, and may be
+ * made from any host thread.  Return value: MQK_OK (0) or a negative mqk
+ * error code; mqk_error_string() turns it into text and
+ * mqk_last_error_detail() names the argument or HIP error involved (per host
+ * thread).
+ *
+ * Reference interface each entry point replaces (mini-qwen-llm):
+ *   mqk_fused_qkv_rope_bf16   <- fused_qkv_rope()      mini_qwen/kernels/fused_qkv_rope.py:130-195
+ *   mqk_qk_norm_rope_bf16     <- _qk_norm_rope_kernel  mini_qwen/kernels/fused_qkv_rope.py:46-127
+ *   mqk_w4a16_gemm            <- w4a16_gemm()          mini_qwen/kernels/w4a16_gemm.py:194-247
+ *   mqk_fused_qkv_rope_w4a16  <- the W4A16 attention front (3x LinearW4A16 + RMSNorm + RoPE),
+ *                                mini_qwen/model/layers/attention.py:102-109 (prefill), :136-148 (decode)
+ */
+#ifndef MQK_H_
+#define MQK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t mqk_bf16;
+
+enum mqk_status {
+  MQK_OK = 0,
+  MQK_ERR_NULL_POINTER = -1,     /* a required pointer is NULL */
+  MQK_ERR_BAD_SHAPE = -2,        /* a size is negative, zero where it must not be, or inconsistent */
+  MQK_ERR_UNSUPPORTED = -3,      /* a valid shape this library does not implement (e.g. head_dim != 128) */
+  MQK_ERR_MISALIGNED = -4,       /* a pointer is not 16-byte aligned */
+  MQK_ERR_WORKSPACE = -5,        /* workspace NULL or smaller than mqk_*_workspace_size() */
+  MQK_ERR_HIP = -6,              /* a HIP runtime call failed (launch, attribute query) */
+  MQK_ERR_BAD_OPTION = -7        /* unknown option name or value out of range */
+};
+
+/* Scale element type of the W4A16 entry points. */
+enum mqk_scale_type { MQK_SCALE_BF16 = 0, MQK_SCALE_FP16 = 1 };
+
+/* Library version, major*10000 + minor*100 + patch. */
+int mqk_version(void);
+const char* mqk_error_string(int status);
+/* Detail of the last error raised on the calling host thread ("" if none). */
+const char* mqk_last_error_detail(void);
+
+/*
+ * Fused Q/K/V projection + per-head RMSNorm of Q and K + rotate-half RoPE of
+ * Q and K; V is the plain projection.  Replaces fused_qkv_rope()
+ * (mini_qwen/kernels/fused_qkv_rope.py:130-195; frozen signature :24-35).
+ *
+ *   x        [T, hidden]          T = B*S tokens
+ *   w_q      [Hq*D, hidden]       nn.Linear layout (out_features, in_features)
+ *   w_k, w_v [Hkv*D, hidden]
+ *   q_gamma, k_gamma [D]          QK-Norm weights, shared by all heads
+ *   cos, sin [cos_rows, D]        row stride D
+ *   positions [T] int32 or NULL   NULL: prefill mode, token t uses row t % S
+ *                                 (fused_qkv_rope.py:109); otherwise row
+ *                                 positions[t] (:107).  Rows outside
+ *                                 [0, cos_rows) are clamped into range (the
+ *                                 reference reads out of bounds there).
+ *   q [T, Hq, D], k [T, Hkv, D], v [T, Hkv, D]   outputs, bf16
+ *   eps                           RMSNorm epsilon (the reference hard-codes 1e-6, :187)
+ *   workspace/ws_bytes            device scratch of at least
+ *                                 mqk_fused_qkv_rope_workspace_size(T, Hq, Hkv, hidden)
+ *                                 bytes.  It must be zero-filled once when
+ *                                 first allocated (it holds arrival counters
+ *                                 that every call leaves at zero again).  One
+ *                                 workspace must not be used by two calls that
+ *                                 may overlap (same or different streams).
+ *
+ * Supported: D == 128, hidden % 64 == 0, Hq >= 1, Hkv >= 1, T >= 0 (T == 0 is
+ * a no-op), x/w/q/k/v 16-byte aligned.  Numerics: bf16 inputs, fp32
+ * accumulation on MFMA, the norm and RoPE are applied to the fp32 accumulator
+ * (the projection is not rounded to bf16 before the norm), one bf16 rounding
+ * per output.
+ */
+int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
+                            const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                            const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                            int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                            int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                            void* workspace, size_t ws_bytes, void* stream);
+
+/* Workspace bytes needed by mqk_fused_qkv_rope_bf16 / _w4a16 for these sizes
+ * (0 when the chosen kernels need none). */
+size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden);
+
+/*
+ * QK-Norm + RoPE alone on already-projected q/k (bf16), the functional twin
+ * of _qk_norm_rope_kernel (mini_qwen/kernels/fused_qkv_rope.py:46-127):
+ *   q_raw [T, Hq, D] -> q_out, k_raw [T, Hkv, D] -> k_out.
+ * Position rules as above.  Either projection may be skipped by passing Hq or
+ * Hkv == 0.  In-place (q_out == q_raw) is allowed.
+ */
+int mqk_qk_norm_rope_bf16(const mqk_bf16* q_raw, const mqk_bf16* k_raw, const mqk_bf16* q_gamma,
+                          const mqk_bf16* k_gamma, const mqk_bf16* cos, const mqk_bf16* sin,
+                          const int32_t* positions, int64_t T, int64_t S, int Hq, int Hkv, int D,
+                          int64_t cos_rows, float eps, mqk_bf16* q_out, mqk_bf16* k_out,
+                          void* stream);
+
+/*
+ * W4A16 GEMM, out[M, N] = x[M, K] @ dequant(qweight)   (w4a16_gemm.py:194-247)
+ *   qweight [K/8, N] int32   nibble i of qweight[j, n] is W[8j+i, n] (w4a16_gemm.py:11)
+ *   scales  [K/group, N]     bf16 or fp16 (scale_type)
+ *   qzeros  [K/group, N/8]   int32, packed along N, nibble i of qzeros[g, j] is z[g, 8j+i]
+ *   dequant: (q - z) * s computed exactly in fp32, rounded once to bf16 for the MFMA.
+ * Supported: K % 64 == 0, group % 64 == 0, K % group == 0, N % 8 == 0.
+ */
+int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales,
+                   const int32_t* qzeros, int64_t M, int64_t K, int64_t N, int group,
+                   int scale_type, mqk_bf16* out, void* stream);
+
+/*
+ * Fused W4A16 front: three int4 projections (q, k, v; each in the
+ * mqk_w4a16_gemm layout with N = Hq*D, Hkv*D, Hkv*D) + QK-Norm + RoPE,
+ * with the same position rules, outputs and workspace as
+ * mqk_fused_qkv_rope_bf16.  Replaces attention.py:102-109 / :136-148, where
+ * the reference runs w4a16_gemm x3 then an unfused RMSNorm and RoPE.
+ */
+int mqk_fused_qkv_rope_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void* sc_q,
+                             const int32_t* qz_q, const int32_t* qw_k, const void* sc_k,
+                             const int32_t* qz_k, const int32_t* qw_v, const void* sc_v,
+                             const int32_t* qz_v, int group, int scale_type,
+                             const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                             const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                             int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                             int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                             void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Process-wide tuning knobs (used by benchmarks and tests; defaults are
+ * chosen by shape).  Names:
+ *   "prefill_tile"   0 = auto, otherwise a tile variant id (see mqk_tile_variants)
+ *   "decode_max_t"   largest T routed to the split-K decode kernel (0..64, default 64;
+ *                    0 disables it)
+ *   "decode_splits"  0 = auto, otherwise the split-K factor of the decode kernel
+ *   "group_m"        row tiles per tile-ordering group of the tile kernel (default 4)
+ * Returns MQK_OK or MQK_ERR_BAD_OPTION.
+ */
+int mqk_set_option(const char* name, int64_t value);
+int64_t mqk_get_option(const char* name);
+/* Human-readable list of tile variants, "id:BMxBN/waves;...". */
+const char* mqk_tile_variants(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MQK_H_ */

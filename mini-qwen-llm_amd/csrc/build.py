@@ -1,0 +1,91 @@
+"""Build libmqk.so (gfx950) in-tree with hipcc.
+
+    python mini-qwen-llm_amd/csrc/build.py            # build
+    python mini-qwen-llm_amd/csrc/build.py --verbose  # echo the hipcc lines
+
+Every translation unit is compiled in parallel, then linked into
+``mini-qwen-llm_amd/mqk/libmqk.so`` (the location the ``mqk`` package loads).
+The compile flags switch off packed-fp32 instruction selection for the device
+pass (``-target-feature -packed-fp32-ops``); hipcc's host pass prints a
+harmless "not a recognized feature" warning for it.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+CSRC = Path(__file__).resolve().parent
+PKG = CSRC.parent / "mqk"
+OUT = PKG / "libmqk.so"
+BUILD_DIR = CSRC.parent / "_build"
+SOURCES = ["qkv_tile.hip", "qkv_decode.hip", "norm_rope.hip", "mqk_api.hip"]
+ARCH = "gfx950"
+
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def _filter(text: str) -> str:
+    keep = [ln for ln in text.splitlines() if "packed-fp32-ops" not in ln]
+    return "\n".join(keep)
+
+
+def _compile(src: str, verbose: bool) -> Path:
+    obj = BUILD_DIR / (Path(src).stem + ".o")
+    cmd = [_hipcc(), *COMMON_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    msg = _filter(res.stdout + res.stderr).strip()
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src}:\n{msg}")
+    if msg and verbose:
+        print(msg)
+    return obj
+
+
+def build(verbose: bool = False) -> Path:
+    BUILD_DIR.mkdir(exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
+    tmp = OUT.with_suffix(".so.tmp")
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("link failed:\n" + _filter(res.stdout + res.stderr))
+    os.replace(tmp, OUT)
+    return OUT
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--verbose", action="store_true")
+    args = ap.parse_args(argv)
+    out = build(args.verbose)
+    print(f"built {out}")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,323 @@
+// C ABI of libmqk.so: argument validation, kernel selection and launch.
+// Declarations and the contract of every entry point: include/mqk.h.
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/mqk.h"
+#include "mqk_device.h"
+#include "mqk_kernels.h"
+
+using namespace mqk;
+
+namespace {
+
+thread_local char g_detail[256] = "";
+
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_detail, sizeof(g_detail), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int ok() {
+  g_detail[0] = '\0';
+  return MQK_OK;
+}
+
+int hip_status(hipError_t err, const char* what) {
+  if (err == hipSuccess) return ok();
+  return fail(MQK_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+// Process-wide knobs (mqk_set_option).
+std::atomic<int64_t> g_prefill_tile{0};
+std::atomic<int64_t> g_decode_max_t{64};
+std::atomic<int64_t> g_decode_splits{0};
+std::atomic<int64_t> g_group_m{4};
+
+constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace
+
+// Shared validation of the position / table / gamma arguments.
+int check_rope_args(const void* q_gamma, const void* k_gamma, const void* cos, const void* sin,
+                    int64_t S, int64_t cos_rows, const int32_t* positions, float eps) {
+  if (!q_gamma || !k_gamma || !cos || !sin)
+    return fail(MQK_ERR_NULL_POINTER, "q_gamma/k_gamma/cos/sin must be non-NULL");
+  if (cos_rows <= 0) return fail(MQK_ERR_BAD_SHAPE, "cos_rows must be > 0 (got %lld)", (long long)cos_rows);
+  if (!positions && S <= 0)
+    return fail(MQK_ERR_BAD_SHAPE, "prefill mode (positions == NULL) needs S > 0 (got %lld)", (long long)S);
+  if (!(eps >= 0.0f)) return fail(MQK_ERR_BAD_SHAPE, "eps must be >= 0");
+  return MQK_OK;
+}
+
+EpilogueArgs make_qkv_epilogue(const mqk_bf16* q_gamma, const mqk_bf16* k_gamma, const mqk_bf16* cos,
+                               const mqk_bf16* sin, const int32_t* positions, int64_t S,
+                               int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                               int Hq, int Hkv) {
+  EpilogueArgs e{};
+  e.qkv = 1;
+  e.Hq = Hq;
+  e.Hkv = Hkv;
+  e.q_gamma = q_gamma;
+  e.k_gamma = k_gamma;
+  e.cos = cos;
+  e.sin = sin;
+  e.positions = positions;
+  e.S = positions ? 1 : S;
+  e.cos_rows = cos_rows;
+  e.eps = eps;
+  e.q = q;
+  e.k = k;
+  e.v = v;
+  return e;
+}
+
+bool use_decode(int64_t T) { return T >= 1 && T <= g_decode_max_t.load() && T <= 64; }
+
+// Common launcher of the fused op (bf16 or int4 weights).
+int run_fused(int int4, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
+              void* workspace, size_t ws_bytes, hipStream_t stream) {
+  if (p.M == 0) return ok();
+  if (use_decode(p.M)) {
+    const int splits = decode_splits_for(p.M, p.K, p.n_tiles, int(g_decode_splits.load()));
+    const size_t need = decode_workspace_bytes(p.n_tiles, splits);
+    if (!workspace || ws_bytes < need)
+      return fail(MQK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given%s", need, ws_bytes,
+                  workspace ? "" : " (NULL)");
+    return hip_status(launch_decode(int4, p, w, e, splits, workspace, stream), "decode kernel launch");
+  }
+  const TileVariant* v = choose_tile_variant(int(g_prefill_tile.load()), p.M, p.n_tiles, int4);
+  if (!v) return fail(MQK_ERR_BAD_OPTION, "prefill_tile variant %lld cannot tile %d heads",
+                      (long long)g_prefill_tile.load(), p.n_tiles);
+  return hip_status(launch_tile(*v, int4, p, w, e, int(g_group_m.load()), stream), "tile kernel launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mqk_version(void) { return 100; }  // 0.1.0
+
+const char* mqk_error_string(int status) {
+  switch (status) {
+    case MQK_OK: return "ok";
+    case MQK_ERR_NULL_POINTER: return "null pointer argument";
+    case MQK_ERR_BAD_SHAPE: return "invalid shape or size";
+    case MQK_ERR_UNSUPPORTED: return "unsupported shape";
+    case MQK_ERR_MISALIGNED: return "pointer not 16-byte aligned";
+    case MQK_ERR_WORKSPACE: return "workspace missing or too small";
+    case MQK_ERR_HIP: return "HIP runtime error";
+    case MQK_ERR_BAD_OPTION: return "bad option";
+    default: return "unknown mqk status";
+  }
+}
+
+const char* mqk_last_error_detail(void) { return g_detail; }
+
+size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden) {
+  if (T <= 0 || Hq <= 0 || Hkv <= 0 || hidden <= 0 || !use_decode(T)) return 0;
+  const int tiles = Hq + 2 * Hkv;
+  return decode_workspace_bytes(tiles, decode_splits_for(T, hidden, tiles, int(g_decode_splits.load())));
+}
+
+static int validate_fused_common(const mqk_bf16* x, int64_t T, int64_t S, int64_t hidden, int Hq,
+                                 int Hkv, int D, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v) {
+  if (T < 0 || hidden <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0)
+    return fail(MQK_ERR_BAD_SHAPE, "need T >= 0, hidden > 0, Hq > 0, Hkv > 0, D > 0");
+  if (D % 2 != 0) return fail(MQK_ERR_BAD_SHAPE, "head_dim must be even (RoPE rotate_half), got %d", D);
+  if (D != kHeadDim) return fail(MQK_ERR_UNSUPPORTED, "head_dim %d not supported (only 128)", D);
+  if (hidden % kBK != 0)
+    return fail(MQK_ERR_UNSUPPORTED, "hidden %lld must be a multiple of 64", (long long)hidden);
+  if (Hq + 2 * Hkv > kMaxTiles) return fail(MQK_ERR_UNSUPPORTED, "Hq + 2*Hkv must be <= %d", kMaxTiles);
+  if (T > (int64_t(1) << 31) / 2) return fail(MQK_ERR_UNSUPPORTED, "T too large");
+  (void)S;
+  if (T == 0) return MQK_OK;
+  if (!x || !q || !k || !v) return fail(MQK_ERR_NULL_POINTER, "x/q/k/v must be non-NULL");
+  if (!aligned16(x) || !aligned16(q) || !aligned16(k) || !aligned16(v))
+    return fail(MQK_ERR_MISALIGNED, "x/q/k/v must be 16-byte aligned");
+  return MQK_OK;
+}
+
+int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
+                            const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                            const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                            int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                            int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                            void* workspace, size_t ws_bytes, void* stream) {
+  int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v);
+  if (st != MQK_OK) return st;
+  if (T == 0) return ok();
+  if (!w_q || !w_k || !w_v) return fail(MQK_ERR_NULL_POINTER, "w_q/w_k/w_v must be non-NULL");
+  if (!aligned16(w_q) || !aligned16(w_k) || !aligned16(w_v))
+    return fail(MQK_ERR_MISALIGNED, "weights must be 16-byte aligned");
+  st = check_rope_args(q_gamma, k_gamma, cos, sin, S, cos_rows, positions, eps);
+  if (st != MQK_OK) return st;
+
+  ProblemArgs p{x, T, hidden, Hq + 2 * Hkv};
+  WeightArgs w{};
+  w.w[0] = w_q;
+  w.w[1] = w_k;
+  w.w[2] = w_v;
+  w.n_cols[0] = int64_t(Hq) * kHeadDim;
+  w.n_cols[1] = w.n_cols[2] = int64_t(Hkv) * kHeadDim;
+  const EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
+                                           q, k, v, Hq, Hkv);
+  return run_fused(0, p, w, e, workspace, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+int mqk_qk_norm_rope_bf16(const mqk_bf16* q_raw, const mqk_bf16* k_raw, const mqk_bf16* q_gamma,
+                          const mqk_bf16* k_gamma, const mqk_bf16* cos, const mqk_bf16* sin,
+                          const int32_t* positions, int64_t T, int64_t S, int Hq, int Hkv, int D,
+                          int64_t cos_rows, float eps, mqk_bf16* q_out, mqk_bf16* k_out,
+                          void* stream) {
+  if (T < 0 || Hq < 0 || Hkv < 0 || D <= 0) return fail(MQK_ERR_BAD_SHAPE, "negative size");
+  if (D % 2 != 0) return fail(MQK_ERR_BAD_SHAPE, "head_dim must be even (RoPE rotate_half), got %d", D);
+  if (D != kHeadDim) return fail(MQK_ERR_UNSUPPORTED, "head_dim %d not supported (only 128)", D);
+  if (T == 0 || Hq + Hkv == 0) return ok();
+  if ((Hq > 0 && (!q_raw || !q_out)) || (Hkv > 0 && (!k_raw || !k_out)))
+    return fail(MQK_ERR_NULL_POINTER, "q/k input or output is NULL");
+  int st = check_rope_args(Hq ? q_gamma : k_gamma, Hkv ? k_gamma : q_gamma, cos, sin, S, cos_rows,
+                           positions, eps);
+  if (st != MQK_OK) return st;
+  const EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
+                                           q_out, k_out, nullptr, Hq, Hkv);
+  return hip_status(launch_norm_rope(q_raw, k_raw, e, T, static_cast<hipStream_t>(stream)),
+                    "norm_rope kernel launch");
+}
+
+static int validate_int4(const int32_t* qw, const void* sc, const int32_t* qz, int64_t K, int64_t N,
+                         int group, int scale_type, const char* which) {
+  if (!qw || !sc || !qz) return fail(MQK_ERR_NULL_POINTER, "%s: qweight/scales/qzeros NULL", which);
+  if (N <= 0 || N % 8 != 0) return fail(MQK_ERR_BAD_SHAPE, "%s: N=%lld must be a positive multiple of 8", which, (long long)N);
+  if (group <= 0 || K % group != 0)
+    return fail(MQK_ERR_BAD_SHAPE, "%s: K=%lld not divisible by group=%d", which, (long long)K, group);
+  if (group % kBK != 0) return fail(MQK_ERR_UNSUPPORTED, "%s: group %d must be a multiple of 64", which, group);
+  if (scale_type != MQK_SCALE_BF16 && scale_type != MQK_SCALE_FP16)
+    return fail(MQK_ERR_BAD_SHAPE, "%s: scale_type %d unknown", which, scale_type);
+  return MQK_OK;
+}
+
+int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales,
+                   const int32_t* qzeros, int64_t M, int64_t K, int64_t N, int group,
+                   int scale_type, mqk_bf16* out, void* stream) {
+  if (M < 0 || K <= 0) return fail(MQK_ERR_BAD_SHAPE, "need M >= 0, K > 0");
+  if (K % kBK != 0) return fail(MQK_ERR_UNSUPPORTED, "K=%lld must be a multiple of 64", (long long)K);
+  int st = validate_int4(qweight, scales, qzeros, K, N, group, scale_type, "w4a16_gemm");
+  if (st != MQK_OK) return st;
+  if (M == 0) return ok();
+  if (!x || !out) return fail(MQK_ERR_NULL_POINTER, "x/out must be non-NULL");
+  if (!aligned16(x)) return fail(MQK_ERR_MISALIGNED, "x must be 16-byte aligned");
+  const int tiles = int((N + kHeadDim - 1) / kHeadDim);
+  ProblemArgs p{x, M, K, tiles};
+  WeightArgs w{};
+  w.qw[0] = qweight;
+  w.sc[0] = scales;
+  w.qz[0] = qzeros;
+  w.n_cols[0] = N;
+  w.group = group;
+  w.scale_fp16 = scale_type == MQK_SCALE_FP16;
+  EpilogueArgs e{};
+  e.qkv = 0;
+  e.Hq = tiles;
+  e.Hkv = 0;
+  e.out = out;
+  e.N = N;
+  const TileVariant* v = choose_tile_variant(1, M, tiles, 1);
+  return hip_status(launch_tile(*v, 1, p, w, e, int(g_group_m.load()), static_cast<hipStream_t>(stream)),
+                    "w4a16 tile kernel launch");
+}
+
+int mqk_fused_qkv_rope_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void* sc_q,
+                             const int32_t* qz_q, const int32_t* qw_k, const void* sc_k,
+                             const int32_t* qz_k, const int32_t* qw_v, const void* sc_v,
+                             const int32_t* qz_v, int group, int scale_type,
+                             const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                             const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                             int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                             int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                             void* workspace, size_t ws_bytes, void* stream) {
+  int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v);
+  if (st != MQK_OK) return st;
+  if (T == 0) return ok();
+  const int64_t nq = int64_t(Hq) * kHeadDim, nkv = int64_t(Hkv) * kHeadDim;
+  if ((st = validate_int4(qw_q, sc_q, qz_q, hidden, nq, group, scale_type, "q_proj")) != MQK_OK) return st;
+  if ((st = validate_int4(qw_k, sc_k, qz_k, hidden, nkv, group, scale_type, "k_proj")) != MQK_OK) return st;
+  if ((st = validate_int4(qw_v, sc_v, qz_v, hidden, nkv, group, scale_type, "v_proj")) != MQK_OK) return st;
+  st = check_rope_args(q_gamma, k_gamma, cos, sin, S, cos_rows, positions, eps);
+  if (st != MQK_OK) return st;
+
+  ProblemArgs p{x, T, hidden, Hq + 2 * Hkv};
+  WeightArgs w{};
+  const int32_t* qws[3] = {qw_q, qw_k, qw_v};
+  const void* scs[3] = {sc_q, sc_k, sc_v};
+  const int32_t* qzs[3] = {qz_q, qz_k, qz_v};
+  for (int i = 0; i < 3; ++i) {
+    w.qw[i] = qws[i];
+    w.sc[i] = scs[i];
+    w.qz[i] = qzs[i];
+  }
+  w.n_cols[0] = nq;
+  w.n_cols[1] = w.n_cols[2] = nkv;
+  w.group = group;
+  w.scale_fp16 = scale_type == MQK_SCALE_FP16;
+  const EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
+                                           q, k, v, Hq, Hkv);
+  return run_fused(1, p, w, e, workspace, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+int mqk_set_option(const char* name, int64_t value) {
+  if (!name) return fail(MQK_ERR_BAD_OPTION, "option name is NULL");
+  if (!strcmp(name, "prefill_tile")) {
+    if (value < 0) return fail(MQK_ERR_BAD_OPTION, "prefill_tile must be >= 0");
+    if (value > 0) {
+      bool found = false;
+      for (int i = 0; i < tile_variant_count(); ++i) found |= tile_variant(i)->id == value;
+      if (!found) return fail(MQK_ERR_BAD_OPTION, "unknown prefill_tile %lld", (long long)value);
+    }
+    g_prefill_tile = value;
+  } else if (!strcmp(name, "decode_max_t")) {
+    if (value < 0 || value > 64) return fail(MQK_ERR_BAD_OPTION, "decode_max_t must be in [0, 64]");
+    g_decode_max_t = value;
+  } else if (!strcmp(name, "decode_splits")) {
+    if (value < 0 || value > 4096) return fail(MQK_ERR_BAD_OPTION, "decode_splits must be in [0, 4096]");
+    g_decode_splits = value;
+  } else if (!strcmp(name, "group_m")) {
+    if (value < 1 || value > 1024) return fail(MQK_ERR_BAD_OPTION, "group_m must be in [1, 1024]");
+    g_group_m = value;
+  } else {
+    return fail(MQK_ERR_BAD_OPTION, "unknown option '%s'", name);
+  }
+  return ok();
+}
+
+int64_t mqk_get_option(const char* name) {
+  if (!name) return -1;
+  if (!strcmp(name, "prefill_tile")) return g_prefill_tile.load();
+  if (!strcmp(name, "decode_max_t")) return g_decode_max_t.load();
+  if (!strcmp(name, "decode_splits")) return g_decode_splits.load();
+  if (!strcmp(name, "group_m")) return g_group_m.load();
+  return -1;
+}
+
+const char* mqk_tile_variants(void) {
+  static const char* const text = [] {
+    static char buf[512];
+    size_t n = 0;
+    buf[0] = '\0';
+    for (int i = 0; i < tile_variant_count(); ++i) {
+      const TileVariant* v = tile_variant(i);
+      n += snprintf(buf + n, sizeof(buf) - n, "%s%d:%dx%d/%dw", i ? ";" : "", v->id, v->bm,
+                    v->hpt * kHeadDim, v->threads / 64);
+    }
+    return buf;
+  }();
+  return text;
+}
+
+}  // extern "C"

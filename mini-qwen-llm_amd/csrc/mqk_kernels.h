@@ -1,0 +1,79 @@
+// Host-side launch interface between the C ABI (mqk_api.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mqk {
+
+// Weight source of the projection.  A 128-column tile h (one head) belongs to
+// projection 0 (Q) for h < Hq, 1 (K) for h < Hq + Hkv, else 2 (V); for a plain
+// GEMM (w4a16_gemm) every tile belongs to projection 0 and Hq is the tile count.
+struct WeightArgs {
+  // bf16: w[p] is [n_cols[p], K] row-major (nn.Linear layout).
+  const uint16_t* w[3];
+  // int4: qw[p] [K/8, n_cols[p]] int32, sc[p] [K/group, n_cols[p]] (bf16 or fp16),
+  //       qz[p] [K/group, n_cols[p]/8] int32.
+  const int32_t* qw[3];
+  const void* sc[3];
+  const int32_t* qz[3];
+  int64_t n_cols[3];
+  int group;
+  int scale_fp16;
+};
+
+// Output side.  qkv == 1: per-head norm + RoPE for Q/K tiles, plain store for V,
+// outputs q [T, Hq, 128], k/v [T, Hkv, 128].  qkv == 0: plain [M, N] store into out.
+struct EpilogueArgs {
+  int qkv;
+  int Hq, Hkv;
+  const uint16_t* q_gamma;
+  const uint16_t* k_gamma;
+  const uint16_t* cos;
+  const uint16_t* sin;
+  const int32_t* positions;
+  int64_t S;
+  int64_t cos_rows;
+  float eps;
+  uint16_t* q;
+  uint16_t* k;
+  uint16_t* v;
+  uint16_t* out;   // plain GEMM output
+  int64_t N;       // plain GEMM width
+};
+
+struct ProblemArgs {
+  const uint16_t* x;   // [M, K] bf16
+  int64_t M;
+  int64_t K;
+  int n_tiles;         // number of 128-column tiles (heads)
+};
+
+// One tile-kernel variant: BM rows x (HPT*128) columns per workgroup, with KZ
+// waves splitting each staged K tile.
+struct TileVariant {
+  int id;
+  int bm;
+  int hpt;
+  int kz;
+  int threads;
+};
+
+int tile_variant_count();
+const TileVariant* tile_variant(int index);
+// Picks a variant for the problem (id 0 = automatic).
+const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles, int int4);
+hipError_t launch_tile(const TileVariant& v, int int4, const ProblemArgs& p, const WeightArgs& w,
+                       const EpilogueArgs& e, int group_m, hipStream_t stream);
+
+// Split-K decode kernel for T <= 64.
+int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested);
+size_t decode_workspace_bytes(int n_tiles, int splits);
+hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
+                         int splits, void* workspace, hipStream_t stream);
+
+// Standalone QK-norm + RoPE.
+hipError_t launch_norm_rope(const uint16_t* q_raw, const uint16_t* k_raw, const EpilogueArgs& e,
+                            int64_t T, hipStream_t stream);
+
+}  // namespace mqk

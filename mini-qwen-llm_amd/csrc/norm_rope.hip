@@ -1,0 +1,61 @@
+// Standalone QK-Norm + RoPE on already-projected q/k (bf16 in, bf16 out): the
+// functional twin of the reference's _qk_norm_rope_kernel
+// (mini_qwen/kernels/fused_qkv_rope.py:46-127).  One wave per (token, head);
+// lane l owns the RoPE pair (d, d+64) = (l, l+64), so the rotation is
+// lane-local and the sum of squares is one 64-lane butterfly.  Used by the
+// unfused paths (already-projected activations); the fused kernels carry their
+// own register epilogue.
+#include "mqk_device.h"
+#include "mqk_kernels.h"
+
+namespace mqk {
+namespace {
+
+constexpr int kNrWaves = 4;
+
+__global__ void __launch_bounds__(kNrWaves * 64)
+norm_rope_kernel(const uint16_t* __restrict__ q_raw, const uint16_t* __restrict__ k_raw,
+                 EpilogueArgs e, int64_t T) {
+  const int lane = threadIdx.x & 63;
+  const int heads = e.Hq + e.Hkv;
+  const int64_t item = int64_t(blockIdx.x) * kNrWaves + (threadIdx.x >> 6);
+  if (item >= T * heads) return;
+  const int64_t t = item / heads;
+  const int h = int(item - t * heads);
+  const bool is_q = h < e.Hq;
+  const int hh = is_q ? h : h - e.Hq;
+  const int H = is_q ? e.Hq : e.Hkv;
+  const uint16_t* src = (is_q ? q_raw : k_raw) + (t * H + hh) * kHeadDim;
+  uint16_t* dst = (is_q ? e.q : e.k) + (t * H + hh) * kHeadDim;
+  const uint16_t* gamma = is_q ? e.q_gamma : e.k_gamma;
+
+  const float x1 = bf16_to_f32(src[lane]);
+  const float x2 = bf16_to_f32(src[lane + kHalfDim]);
+  float ss = x1 * x1 + x2 * x2;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+  const float rms = rsqrtf(ss * (1.0f / float(kHeadDim)) + e.eps);
+  const float x1n = x1 * rms * bf16_to_f32(gamma[lane]);
+  const float x2n = x2 * rms * bf16_to_f32(gamma[lane + kHalfDim]);
+  const int64_t prow = rope_row(e.positions, t, e.S, e.cos_rows) * kHeadDim;
+  const float c1 = bf16_to_f32(e.cos[prow + lane]);
+  const float c2 = bf16_to_f32(e.cos[prow + lane + kHalfDim]);
+  const float s1 = bf16_to_f32(e.sin[prow + lane]);
+  const float s2 = bf16_to_f32(e.sin[prow + lane + kHalfDim]);
+  // in-place safe: every lane has read its inputs before the butterfly completes
+  dst[lane] = f32_to_bf16(x1n * c1 - x2n * s1);
+  dst[lane + kHalfDim] = f32_to_bf16(x2n * c2 + x1n * s2);
+}
+
+}  // namespace
+
+hipError_t launch_norm_rope(const uint16_t* q_raw, const uint16_t* k_raw, const EpilogueArgs& e,
+                            int64_t T, hipStream_t stream) {
+  const int64_t items = T * (e.Hq + e.Hkv);
+  const int64_t blocks = (items + kNrWaves - 1) / kNrWaves;
+  hipLaunchKernelGGL(norm_rope_kernel, dim3(unsigned(blocks)), dim3(kNrWaves * 64), 0, stream,
+                     q_raw, k_raw, e, T);
+  return hipGetLastError();
+}
+
+}  // namespace mqk

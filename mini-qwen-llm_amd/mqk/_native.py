@@ -1,0 +1,147 @@
+"""ctypes binding of libmqk.so (the C ABI declared in include/mqk.h).
+
+The library is loaded after ``torch`` so that it binds to the HIP runtime torch
+already mapped (same soname), which keeps one runtime per process and lets
+torch-allocated device pointers and torch streams be passed straight through.
+A missing or unloadable library raises :class:`MqkNativeError`; nothing in
+this package falls back to another implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must be imported before the HIP library is mapped)
+
+LIB_PATH = Path(os.environ.get("MQK_LIBRARY", Path(__file__).with_name("libmqk.so")))
+
+MQK_OK = 0
+MQK_SCALE_BF16 = 0
+MQK_SCALE_FP16 = 1
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/mqk.h.
+SIGNATURES = {
+    "mqk_version": (_I, []),
+    "mqk_error_string": (ctypes.c_char_p, [_I]),
+    "mqk_last_error_detail": (ctypes.c_char_p, []),
+    "mqk_fused_qkv_rope_bf16": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P,     # x w_q w_k w_v q_gamma k_gamma cos sin positions
+         _I64, _I64, _I64, _I, _I, _I,           # T S hidden Hq Hkv D
+         _I64, _F, _P, _P, _P, _P, _SZ, _P],     # cos_rows eps q k v workspace ws_bytes stream
+    ),
+    "mqk_fused_qkv_rope_workspace_size": (_SZ, [_I64, _I, _I, _I64]),
+    "mqk_qk_norm_rope_bf16": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P,             # q_raw k_raw q_gamma k_gamma cos sin positions
+         _I64, _I64, _I, _I, _I,                 # T S Hq Hkv D
+         _I64, _F, _P, _P, _P],                  # cos_rows eps q_out k_out stream
+    ),
+    "mqk_w4a16_gemm": (
+        _I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P],
+    ),
+    "mqk_fused_qkv_rope_w4a16": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P,  # x, (qw, sc, qz) x 3
+         _I, _I,                                  # group scale_type
+         _P, _P, _P, _P, _P,                      # q_gamma k_gamma cos sin positions
+         _I64, _I64, _I64, _I, _I, _I,            # T S hidden Hq Hkv D
+         _I64, _F, _P, _P, _P, _P, _SZ, _P],      # cos_rows eps q k v workspace ws_bytes stream
+    ),
+    "mqk_set_option": (_I, [ctypes.c_char_p, _I64]),
+    "mqk_get_option": (_I64, [ctypes.c_char_p]),
+    "mqk_tile_variants": (ctypes.c_char_p, []),
+}
+
+
+class MqkNativeError(RuntimeError):
+    """libmqk.so is missing, failed to load, or returned an error status."""
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def library() -> ctypes.CDLL:
+    """The loaded libmqk.so (loaded on first use)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise MqkNativeError(
+                    f"libmqk.so not found at {LIB_PATH}; build it with "
+                    "`python mini-qwen-llm_amd/csrc/build.py` (the mqk ops have no fallback path)")
+            try:
+                lib = ctypes.CDLL(str(LIB_PATH))
+            except OSError as exc:
+                raise MqkNativeError(f"cannot load {LIB_PATH}: {exc}") from exc
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    """Raise :class:`MqkNativeError` for a non-zero mqk status."""
+    if status == MQK_OK:
+        return
+    lib = library()
+    msg = lib.mqk_error_string(status).decode()
+    detail = lib.mqk_last_error_detail().decode()
+    raise MqkNativeError(f"{what} failed: {msg} ({status}){': ' + detail if detail else ''}")
+
+
+def set_option(name: str, value: int) -> None:
+    check(library().mqk_set_option(name.encode(), int(value)), f"mqk_set_option({name})")
+
+
+def get_option(name: str) -> int:
+    return int(library().mqk_get_option(name.encode()))
+
+
+def tile_variants() -> str:
+    return library().mqk_tile_variants().decode()
+
+
+def version() -> int:
+    return int(library().mqk_version())
+
+
+# ---------------------------------------------------------------------------
+# Workspace: one zero-initialised device buffer per (device, stream).  The
+# kernels leave its arrival counters at zero after each call, so it is zeroed
+# only when (re)allocated.  Keyed by stream because calls that may overlap must
+# not share a workspace.
+# ---------------------------------------------------------------------------
+_ws_lock = threading.Lock()
+_workspaces: dict = {}
+
+
+def workspace(device: torch.device, stream, nbytes: int):
+    if nbytes <= 0:
+        return None
+    key = (device.index, int(stream.cuda_stream))
+    with _ws_lock:
+        buf = _workspaces.get(key)
+        if buf is None or buf.numel() < nbytes:
+            size = max(nbytes, 1 << 20)
+            with torch.cuda.stream(stream):
+                buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            _workspaces[key] = buf
+        return buf
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,169 @@
+"""Fused QKV projection + QK-Norm + RoPE on MI355X (drop-in for the reference op).
+
+Mirror of ``mini_qwen.kernels.fused_qkv_rope.fused_qkv_rope``
+(mini_qwen/kernels/fused_qkv_rope.py:130-195, frozen signature :24-35):
+
+    fused_qkv_rope(x, w_q, w_k, w_v, q_norm_w, k_norm_w, cos, sin, positions=None)
+        x         [B, S, hidden]           bf16
+        w_q       [H_Q * D, hidden]        bf16 (nn.Linear layout)
+        w_k, w_v  [H_KV * D, hidden]       bf16
+        q_norm_w, k_norm_w [D]             bf16
+        cos, sin  [S or rows, D]           bf16
+        positions [B*S] int32 or None      None: prefill, token t uses row t % S;
+                                           else row positions[t]
+        -> q [B, S, H_Q, D], k [B, S, H_KV, D], v [B, S, H_KV, D]   bf16, contiguous
+
+Shapes are inferred as the reference does (:155-158): ``D = q_norm_w.shape[0]``,
+``H_Q = w_q.shape[0] // D``, ``H_KV = w_k.shape[0] // D``, and ``D`` must be even
+(:160).  The whole op is one HIP kernel launch (libmqk.so): bf16 MFMA projection,
+fp32 norm + RoPE applied to the accumulators, one bf16 store per output.
+
+Differences from the reference, all deliberate:
+  * the norm reads the fp32 accumulator, not a bf16-rounded GEMM output;
+  * ``v`` is our own MFMA projection (fp32 accumulate, one rounding), so it is
+    not bit-identical to a vendor GEMM (test_fused_qkv_rope.py:165 demands
+    bit-equality with torch's own GEMM, which no independent kernel can give);
+  * positions outside ``[0, cos.shape[0])`` are clamped instead of read out of
+    bounds; int64 positions are accepted and converted;
+  * inputs must be bf16 CUDA/HIP tensors (TypeError / ValueError otherwise);
+    non-contiguous inputs are made contiguous.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _native
+
+EPS = 1e-6  # the reference hard-codes EPS=1e-6 (fused_qkv_rope.py:187)
+
+
+def _require(t: torch.Tensor, name: str, device: torch.device, dtype=torch.bfloat16) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a GPU device, got {t.device}")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    return t.contiguous()
+
+
+def _positions(positions: Optional[torch.Tensor], T: int, device) -> Optional[torch.Tensor]:
+    if positions is None:
+        return None
+    if positions.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"positions must be int32 (or int64), got {positions.dtype}")
+    positions = _require(positions, "positions", device, dtype=None).reshape(-1)
+    if positions.numel() != T:
+        raise ValueError(f"positions has {positions.numel()} entries, expected B*S = {T}")
+    return positions.to(torch.int32)
+
+
+def _rope_tables(cos, sin, D, device):
+    cos = _require(cos, "cos", device)
+    sin = _require(sin, "sin", device)
+    if cos.dim() != 2 or cos.shape[1] != D or sin.shape != cos.shape:
+        raise ValueError(f"cos/sin must both be [rows, {D}], got {tuple(cos.shape)} / {tuple(sin.shape)}")
+    if cos.shape[0] < 1:
+        raise ValueError("cos/sin need at least one row")
+    return cos, sin
+
+
+def fused_qkv_rope(
+    x: torch.Tensor,
+    w_q: torch.Tensor,
+    w_k: torch.Tensor,
+    w_v: torch.Tensor,
+    q_norm_w: torch.Tensor,
+    k_norm_w: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    positions: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Fused QKV projection + QK-Norm + RoPE; see the module docstring."""
+    B, S, H = x.shape
+    D = q_norm_w.shape[0]
+    H_Q = w_q.shape[0] // D
+    H_KV = w_k.shape[0] // D
+    assert D % 2 == 0, "head_dim must be even (RoPE rotate_half)"
+    device = x.device
+    x = _require(x, "x", device)
+    w_q = _require(w_q, "w_q", device)
+    w_k = _require(w_k, "w_k", device)
+    w_v = _require(w_v, "w_v", device)
+    q_norm_w = _require(q_norm_w, "q_norm_w", device)
+    k_norm_w = _require(k_norm_w, "k_norm_w", device)
+    if w_q.shape != (H_Q * D, H) or w_k.shape != (H_KV * D, H) or w_v.shape != (H_KV * D, H):
+        raise ValueError(
+            f"weight shapes {tuple(w_q.shape)}, {tuple(w_k.shape)}, {tuple(w_v.shape)} do not match "
+            f"H_Q={H_Q}, H_KV={H_KV}, D={D}, hidden={H}")
+    if k_norm_w.shape != (D,):
+        raise ValueError(f"k_norm_w must be [{D}], got {tuple(k_norm_w.shape)}")
+    cos, sin = _rope_tables(cos, sin, D, device)
+    T = B * S
+    pos = _positions(positions, T, device)
+
+    q = torch.empty(B, S, H_Q, D, dtype=torch.bfloat16, device=device)
+    k = torch.empty(B, S, H_KV, D, dtype=torch.bfloat16, device=device)
+    v = torch.empty(B, S, H_KV, D, dtype=torch.bfloat16, device=device)
+    if T == 0:
+        return q, k, v
+
+    lib = _native.library()
+    stream = torch.cuda.current_stream(device)
+    nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, H_Q, H_KV, H))
+    ws = _native.workspace(device, stream, nbytes)
+    status = lib.mqk_fused_qkv_rope_bf16(
+        x.data_ptr(), w_q.data_ptr(), w_k.data_ptr(), w_v.data_ptr(),
+        q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), _native.ptr(pos),
+        T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
+        q.data_ptr(), k.data_ptr(), v.data_ptr(),
+        _native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
+    _native.check(status, "mqk_fused_qkv_rope_bf16")
+    return q, k, v
+
+
+def qk_norm_rope(
+    q_raw: torch.Tensor,
+    k_raw: torch.Tensor,
+    q_norm_w: torch.Tensor,
+    k_norm_w: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    positions: Optional[torch.Tensor] = None,
+    eps: float = EPS,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """QK-Norm + RoPE on already-projected ``q_raw [B, S, H_Q, D]`` / ``k_raw [B, S, H_KV, D]``.
+
+    The standalone twin of ``_qk_norm_rope_kernel`` (fused_qkv_rope.py:46-127),
+    with the same position rules (prefill: row ``t % S``; else ``positions[t]``).
+    """
+    if q_raw.dim() != 4 or k_raw.dim() != 4:
+        raise ValueError("q_raw/k_raw must be [B, S, H, D]")
+    B, S, H_Q, D = q_raw.shape
+    H_KV = k_raw.shape[2]
+    assert D % 2 == 0, "head_dim must be even (RoPE rotate_half)"
+    if k_raw.shape[:2] != (B, S) or k_raw.shape[3] != D:
+        raise ValueError(f"k_raw shape {tuple(k_raw.shape)} does not match q_raw {tuple(q_raw.shape)}")
+    device = q_raw.device
+    q_raw = _require(q_raw, "q_raw", device)
+    k_raw = _require(k_raw, "k_raw", device)
+    q_norm_w = _require(q_norm_w, "q_norm_w", device)
+    k_norm_w = _require(k_norm_w, "k_norm_w", device)
+    cos, sin = _rope_tables(cos, sin, D, device)
+    T = B * S
+    pos = _positions(positions, T, device)
+    q_out = torch.empty_like(q_raw)
+    k_out = torch.empty_like(k_raw)
+    if T == 0:
+        return q_out, k_out
+    stream = torch.cuda.current_stream(device)
+    status = _native.library().mqk_qk_norm_rope_bf16(
+        q_raw.data_ptr(), k_raw.data_ptr(), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
+        cos.data_ptr(), sin.data_ptr(), _native.ptr(pos), T, S, H_Q, H_KV, D, cos.shape[0],
+        float(eps), q_out.data_ptr(), k_out.data_ptr(), stream.cuda_stream)
+    _native.check(status, "mqk_qk_norm_rope_bf16")
+    return q_out, k_out

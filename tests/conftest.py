@@ -1,0 +1,88 @@
+"""Shared test setup: import paths, the ``gpu`` marker, seeded input builders."""
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+for p in (ROOT, ROOT / "mini-qwen-llm_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+HEAD_DIM = 128
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and libmqk.so")
+
+
+def pytest_collection_modifyitems(config, items):
+    if torch.cuda.is_available():
+        return
+    skip = pytest.mark.skip(reason="no GPU in this environment")
+    for item in items:
+        if "gpu" in item.keywords:
+            item.add_marker(skip)
+
+
+def f32(t: torch.Tensor) -> np.ndarray:
+    """Exact float32 values of a (bf16) tensor, on the host."""
+    return t.detach().float().cpu().numpy()
+
+
+class Case:
+    """Seeded inputs of one fused_qkv_rope call (host copies; .to(dev) moves them)."""
+
+    def __init__(self, B, S, hidden, Hq, Hkv, seed, *, rows=None, theta=1e6, gamma_ones=False,
+                 positions=None, w_std=0.02, x_std=1.0):
+        g = torch.Generator().manual_seed(seed)
+        D = HEAD_DIM
+        self.B, self.S, self.hidden, self.Hq, self.Hkv = B, S, hidden, Hq, Hkv
+        self.x = (torch.randn(B, S, hidden, generator=g) * x_std).bfloat16()
+        self.w_q = (torch.randn(Hq * D, hidden, generator=g) * w_std).bfloat16()
+        self.w_k = (torch.randn(Hkv * D, hidden, generator=g) * w_std).bfloat16()
+        self.w_v = (torch.randn(Hkv * D, hidden, generator=g) * w_std).bfloat16()
+        if gamma_ones:
+            self.q_norm_w = torch.ones(D).bfloat16()
+            self.k_norm_w = torch.ones(D).bfloat16()
+        else:
+            self.q_norm_w = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+            self.k_norm_w = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+        from mqk.rope import rope_tables
+        n_rows = rows if rows is not None else S
+        cos, sin = rope_tables(D, n_rows, theta)
+        self.cos, self.sin = cos.bfloat16(), sin.bfloat16()
+        self.positions = positions
+
+    def args(self, device):
+        pos = None if self.positions is None else self.positions.to(device)
+        return (self.x.to(device), self.w_q.to(device), self.w_k.to(device), self.w_v.to(device),
+                self.q_norm_w.to(device), self.k_norm_w.to(device), self.cos.to(device),
+                self.sin.to(device), pos)
+
+    def oracle(self, token_idx=None, round_projection=False):
+        """Oracle outputs (float64) for all tokens or the given flat token indices."""
+        from oracle import qkv_rope_oracle as orc
+        T = self.B * self.S
+        x2 = f32(self.x).reshape(T, self.hidden)
+        if self.positions is None:
+            rows = np.arange(T) % self.S
+        else:
+            rows = self.positions.cpu().numpy().astype(np.int64)
+        if token_idx is not None:
+            x2 = x2[token_idx]
+            rows = rows[token_idx]
+        n = x2.shape[0]
+        return orc.fused_qkv_rope(x2.reshape(1, n, self.hidden), f32(self.w_q), f32(self.w_k),
+                                  f32(self.w_v), f32(self.q_norm_w), f32(self.k_norm_w),
+                                  f32(self.cos), f32(self.sin), positions=rows,
+                                  round_projection=round_projection)
+
+
+@pytest.fixture(scope="session")
+def device():
+    return torch.device("cuda:0")
