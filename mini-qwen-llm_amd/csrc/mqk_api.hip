@@ -42,7 +42,7 @@ std::atomic<int64_t> g_decode_max_t{64};
 std::atomic<int64_t> g_decode_splits{0};
 std::atomic<int64_t> g_group_m{4};
 
-constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace
+constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace (per head)
 
 // Shared validation of the position / table / gamma arguments.
 int check_rope_args(const void* q_gamma, const void* k_gamma, const void* cos, const void* sin,
@@ -84,8 +84,8 @@ bool use_decode(int64_t T) { return T >= 1 && T <= g_decode_max_t.load() && T <=
 int run_fused(int int4, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
               void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (p.M == 0) return ok();
-  if (use_decode(p.M)) {
-    const int splits = decode_splits_for(p.M, p.K, p.n_tiles, int(g_decode_splits.load()));
+  const int splits = use_decode(p.M) ? decode_splits_for(p.M, p.K, p.n_tiles, int(g_decode_splits.load())) : 0;
+  if (splits > 0) {
     const size_t need = decode_workspace_bytes(p.n_tiles, splits);
     if (!workspace || ws_bytes < need)
       return fail(MQK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given%s", need, ws_bytes,
@@ -121,9 +121,10 @@ const char* mqk_error_string(int status) {
 const char* mqk_last_error_detail(void) { return g_detail; }
 
 size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden) {
-  if (T <= 0 || Hq <= 0 || Hkv <= 0 || hidden <= 0 || !use_decode(T)) return 0;
+  if (T <= 0 || Hq <= 0 || Hkv <= 0 || hidden <= 0 || hidden % kBK != 0 || !use_decode(T)) return 0;
   const int tiles = Hq + 2 * Hkv;
-  return decode_workspace_bytes(tiles, decode_splits_for(T, hidden, tiles, int(g_decode_splits.load())));
+  const int splits = decode_splits_for(T, hidden, tiles, int(g_decode_splits.load()));
+  return splits > 0 ? decode_workspace_bytes(tiles, splits) : 0;
 }
 
 static int validate_fused_common(const mqk_bf16* x, int64_t T, int64_t S, int64_t hidden, int Hq,
@@ -287,6 +288,9 @@ int mqk_set_option(const char* name, int64_t value) {
   } else if (!strcmp(name, "decode_splits")) {
     if (value < 0 || value > 4096) return fail(MQK_ERR_BAD_OPTION, "decode_splits must be in [0, 4096]");
     g_decode_splits = value;
+  } else if (!strcmp(name, "decode_force_recompute")) {
+    if (value != 0 && value != 1) return fail(MQK_ERR_BAD_OPTION, "decode_force_recompute must be 0 or 1");
+    g_decode_force_recompute = int(value);
   } else if (!strcmp(name, "group_m")) {
     if (value < 1 || value > 1024) return fail(MQK_ERR_BAD_OPTION, "group_m must be in [1, 1024]");
     g_group_m = value;
@@ -302,6 +306,7 @@ int64_t mqk_get_option(const char* name) {
   if (!strcmp(name, "decode_max_t")) return g_decode_max_t.load();
   if (!strcmp(name, "decode_splits")) return g_decode_splits.load();
   if (!strcmp(name, "group_m")) return g_group_m.load();
+  if (!strcmp(name, "decode_force_recompute")) return g_decode_force_recompute;
   return -1;
 }
 

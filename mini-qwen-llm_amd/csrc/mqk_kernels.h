@@ -66,11 +66,17 @@ const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles,
 hipError_t launch_tile(const TileVariant& v, int int4, const ProblemArgs& p, const WeightArgs& w,
                        const EpilogueArgs& e, int group_m, hipStream_t stream);
 
-// Split-K decode kernel for T <= 64.
+// Split-K decode kernel for T <= 64.  decode_splits_for returns 0 when no
+// valid split count exists (each split covers at most 16 64-wide k tiles);
+// the caller then uses the tile kernel.
 int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested);
 size_t decode_workspace_bytes(int n_tiles, int splits);
 hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                          int splits, void* workspace, hipStream_t stream);
+
+// 1: the last workgroup of every head recomputes all splits itself (the path
+// taken when a split ran on an unexpected XCD); for tests.
+extern int g_decode_force_recompute;
 
 // Standalone QK-norm + RoPE.
 hipError_t launch_norm_rope(const uint16_t* q_raw, const uint16_t* k_raw, const EpilogueArgs& e,

@@ -1,235 +1,291 @@
-// Split-K projection for small token counts (decode steps, T <= 64), with the
-// per-head norm + RoPE done by the last workgroup that finishes each head.
+// Split-K projection for small token counts (decode steps, T <= 64) with the
+// per-head norm + RoPE applied once the split partial sums are combined.
 //
 // At decode the op is weight-read bound: Qwen3-8B's 50 MB of projection
-// weights against 64 tokens.  48 heads alone cannot keep 256 CUs streaming, so
-// each head is split along K into `splits` workgroups (XCD-aware: all splits of
-// one head are dispatched to the same XCD and so share an L2).  Inside a
-// workgroup, wave w owns columns [32w, 32w+32) of the head for all 64 token
-// rows (v_mfma_f32_16x16x32_bf16, 4 x 2 blocks); its weight rows are streamed
-// HBM -> VGPR with a PREFETCH-deep ring of 64-wide k tiles, each lane loading
-// 16 contiguous bytes so that one load instruction covers 16 rows x 64 bytes.
-// The activation slice x[:, k-range] is staged once in LDS.
+// weights against 64 tokens.  Measured on MI355X: one CU sustains only a few
+// tens of GB/s of reads, so every CU must stream its share of the weights;
+// splitting a head's columns (instead of K) would re-read the activations from
+// L2 per workgroup, which measured 3-4x slower than the weight stream itself;
+// and two workgroups sharing a CU finish twice as late as one alone.  Hence:
+//   * one 1024-thread workgroup per CU (its activation slice in LDS is larger
+//     than half the LDS, so the hardware cannot co-schedule two);
+//   * each head is split along K into S = floor(CUs per XCD / heads per XCD)
+//     k-ranges, and the grid maps all splits of head h to XCD h % 8
+//     (workgroup b runs on XCD b % 8), so every XCD gets the same number of
+//     workgroups, at most one per CU;
+//   * inside a workgroup, wave (cg, kh) owns columns [16cg, 16cg+16) of the
+//     head and half of the split's k-range, for all 64 token rows
+//     (v_mfma_f32_16x16x32_bf16, 4 row blocks).  Its weight slice is loaded
+//     HBM -> VGPR before the first MFMA; the activation slice is staged once
+//     in LDS.  The two k-halves are added through LDS.
+// Combining the splits: each workgroup writes its fp32 partial tile [64 x 128]
+// with plain stores, which stay in (or are written back from) the L2 of its
+// XCD, and bumps the head's arrival counter; the workgroup that arrives last
+// reads the other partials with plain loads -- all of them were written
+// through the same L2 -- adds them in split order, applies RMSNorm over the
+// head (fused_qkv_rope.py:98-100) and rotate-half RoPE (:102-118), writes
+// bf16 q/k (or v unchanged) and resets the counter for the next call.
+// Device-coherent (sc1) accesses measured ~0.5 TB/s and an agent-scope fence
+// pair (L2 writeback + invalidate) ~2x the whole op, so neither is used.
 //
-// Every workgroup writes its fp32 partial tile [64 x 128] to the workspace,
-// fences, and bumps the head's arrival counter; the workgroup that arrives last
-// sums the partials, applies RMSNorm over the head (fused_qkv_rope.py:98-100)
-// and rotate-half RoPE (:102-118), writes bf16 q/k (or v unchanged), and resets
-// the counter to zero for the next call.  No workgroup ever waits on another.
+// Each workgroup checks the XCD it actually runs on (hardware register
+// XCC_ID).  If any split of a head ran elsewhere, its partial may sit in a
+// different L2, so the last workgroup instead recomputes every split of the
+// head itself, with the same per-split arithmetic and summation order: slower,
+// bit-identical, and correct whatever the dispatch order.
 #include "mqk_device.h"
 #include "mqk_kernels.h"
 
 namespace mqk {
 namespace {
 
-constexpr int kDecRows = 64;          // token rows per call (T <= 64)
-constexpr int kDecThreads = 256;      // 4 waves x 32 columns = one head
-constexpr int kDecMaxKc = 512;        // largest k-range of one split (LDS: 64 x 512 bf16 = 64 KB)
-constexpr int kPrefetch = 4;          // k tiles in flight per wave
-constexpr int kCounterBytes = 4096;   // arrival counters at the head of the workspace
+constexpr int kDecRows = 64;            // token rows per call (T <= 64)
+constexpr int kDecThreads = 1024;       // 16 waves: 8 column groups x 2 k-halves
+constexpr int kDecMaxNK = 16;           // largest k-range of one split, in 64-wide tiles
+constexpr int kDecHalfNK = kDecMaxNK / 2;
+constexpr int kDecKc = kDecMaxNK * kBK;     // LDS row length of the x slice (bf16), 2 KB
+constexpr int kMaxHeads = 1024;
+constexpr int kCounterBytes = kMaxHeads * 4;
+constexpr int kTileFloats = kDecRows * kHeadDim;
+constexpr int kPitch = kHeadDim + 4;    // LDS pitch (floats) of the partial tile
+constexpr int kXcds = 8;                // MI355X: 8 XCDs, workgroup b dispatched to XCD b % 8
+constexpr uint32_t kForeignUnit = 1u << 16;  // arrival-counter increment of a misplaced split
+
+static_assert(kDecRows * kDecKc * 2 > 160 * 1024 / 2, "x slice must keep one workgroup per CU");
+static_assert(kDecRows * kPitch * 4 <= kDecRows * kDecKc * 2, "partial tile aliases the x slice");
 
 __device__ __forceinline__ int dec_lds_off(int row, int chunk) {
-  // row stride kDecMaxKc bf16; 16-byte chunk index swizzled in its low 3 bits
-  return row * kDecMaxKc + ((chunk ^ (row & 7)) << 3);
+  // row stride kDecKc bf16; 16-byte chunk index swizzled in its low 3 bits
+  return row * kDecKc + ((chunk ^ (row & 7)) << 3);
 }
 
-template <bool INT4>
-__global__ void __launch_bounds__(kDecThreads)
-decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __restrict__ part,
-              int* __restrict__ counters) {
-  __shared__ __attribute__((aligned(16))) uint16_t xs[kDecRows * kDecMaxKc];
-  __shared__ int last_flag;
+__device__ __forceinline__ int xcc_id() {
+  return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11));  // hwreg(HW_REG_XCC_ID, 0, 4)
+}
 
+// k-tile range [kt0, kt0 + nk) of split s of S over nkt tiles (balanced).
+__device__ __forceinline__ void split_range(int s, int S, int nkt, int& kt0, int& nk) {
+  kt0 = int((int64_t(s) * nkt) / S);
+  nk = int((int64_t(s + 1) * nkt) / S) - kt0;
+}
+
+// Computes the partial tile of k-tiles [kt0, kt0 + nk) of one head into LDS
+// `tile` (fp32 [64][kPitch], row-major), using `xs` as staging.  All threads of
+// the workgroup call it; it ends with a barrier.
+template <bool INT4>
+__device__ void compute_partial(const ProblemArgs& p, const WeightArgs& w, int proj, int hh, int kt0,
+                                int nk, uint16_t* xs, float* tile) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int n_tiles = p.n_tiles;
-
-  // ---- which (head, split): all splits of a head on one XCD -----------------
-  int head, split;
-  const int bid = blockIdx.x;
-  if ((n_tiles & 7) == 0) {
-    const int xcd = bid & 7, q = bid >> 3;
-    split = q % splits;
-    head = (q / splits) * 8 + xcd;
-  } else {
-    head = bid / splits;
-    split = bid % splits;
-  }
-  const int nkt = int(p.K / kBK);
-  const int kt0 = int((int64_t(split) * nkt) / splits);
-  const int kt1 = int((int64_t(split + 1) * nkt) / splits);
-  const int nk = kt1 - kt0;
-  const int64_t kbeg = int64_t(kt0) * kBK;
+  const int cg = wave & 7;            // 16-column group of the head
+  const int kh = wave >> 3;           // k-half of the split
+  const int c16 = lane & 15;
+  const int g4 = lane >> 4;
   const int M = int(p.M);
+  const int64_t kbeg = int64_t(kt0) * kBK;
+  const int n_lo = (nk + 1) / 2;      // tiles of k-half 0
+  const int my_t0 = kh ? n_lo : 0;
+  const int my_nt = kh ? nk - n_lo : n_lo;
 
+  // 1. activation slice x[0:M, kbeg : kbeg + nk*64] -> LDS with direct
+  // global->LDS loads (no VGPR staging).  One wave instruction fills half an
+  // LDS row (64 chunks of 16 B); lane L writes LDS chunk slot half*64 + L, which
+  // holds global chunk slot ^ (row & 7) (the swizzle of dec_lds_off).
+#pragma unroll
+  for (int i = 0; i < 2 * kDecRows / 16; ++i) {
+    const int u = wave + 16 * i;          // (row, half) unit, wave-uniform
+    const int row = u >> 1, half = u & 1;
+    const int gq = (half * 64 + lane) ^ (row & 7);
+    if (row < M && gq < nk * 8)
+      __builtin_amdgcn_global_load_lds(p.x + int64_t(row) * p.K + kbeg + gq * 8,
+                                       xs + row * kDecKc + half * 64 * 8, 16, 0, 0);
+  }
+
+  // 2. this wave's weight slice, straight to registers.  16x16x32 operand
+  // layout: lane (c, g) holds column c (B) / row c (A) and 8 k values; k order
+  // inside a 64-wide tile: block kk (0,1) of 32, lane group g -> kk*32 + g*8.
+  const int64_t col = int64_t(hh) * kHeadDim + cg * 16 + c16;  // column inside the projection
+  const int64_t qstride = w.n_cols[proj];
+  u32x4_t wb[INT4 ? 1 : kDecHalfNK][2];
+  uint32_t wq[INT4 ? kDecHalfNK : 1][2];
+#pragma unroll
+  for (int t = 0; t < kDecHalfNK; ++t) {
+    if (t < my_nt) {
+      const int64_t k0 = kbeg + int64_t(my_t0 + t) * kBK;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        if constexpr (!INT4)
+          wb[t][kk] = *reinterpret_cast<const u32x4_t*>(w.w[proj] + col * p.K + k0 + kk * 32 + g4 * 8);
+        else
+          wq[t][kk] = uint32_t(w.qw[proj][(k0 / 8 + kk * 4 + g4) * qstride + col]);
+      }
+    }
+  }
+
+  // 3. wait for every load (the x slice must be in LDS before the barrier)
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // 4. MFMAs.  Rows >= M of xs hold stale data; output row r depends only on
+  // row r of x and rows >= M are never stored.
+  f32x4_t acc[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4_t{};
+#pragma unroll
+  for (int t = 0; t < kDecHalfNK; ++t) {
+    if (t < my_nt) {
+      u32x4_t b[2];
+      if constexpr (!INT4) {
+        b[0] = wb[t][0];
+        b[1] = wb[t][1];
+      } else {
+        const int64_t k0 = kbeg + int64_t(my_t0 + t) * kBK;
+        const int grp = int(k0 / w.group);
+        const uint32_t sraw = static_cast<const uint16_t*>(w.sc[proj])[grp * qstride + col];
+        const float scale = w.scale_fp16 ? f16_to_f32(sraw) : bf16_to_f32(sraw);
+        const uint32_t zw = uint32_t(w.qz[proj][grp * (qstride / 8) + col / 8]);
+        const float zero = float((zw >> ((col % 8) * 4)) & 0xFu);
+        b[0] = dequant_int4x8(wq[t][0], zero, scale);
+        b[1] = dequant_int4x8(wq[t][1], zero, scale);
+      }
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int chunk = (my_t0 + t) * 8 + kk * 4 + g4;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xs + dec_lds_off(mb * 16 + c16, chunk));
+          acc[mb] = mfma_16x16x32(a, b[kk], acc[mb]);
+        }
+      }
+    }
+  }
+  __syncthreads();  // xs no longer read; tile may alias it
+
+  // 5. k-half 1 writes its sums, k-half 0 adds its own: tile = full partial.
+  // acc[mb][j] = C[mb*16 + 4g + j][cg*16 + c].
+  if (kh == 1) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tile[(mb * 16 + g4 * 4 + j) * kPitch + cg * 16 + c16] = acc[mb][j];
+  }
+  __syncthreads();
+  if (kh == 0) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float* t = tile + (mb * 16 + g4 * 4 + j) * kPitch + cg * 16 + c16;
+        *t = acc[mb][j] + *t;
+      }
+  }
+  __syncthreads();
+}
+
+template <bool INT4>
+__global__ void __launch_bounds__(kDecThreads, 1)
+decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __restrict__ part,
+              uint32_t* __restrict__ counters, int force_recompute) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[kDecRows * kDecKc];
+  __shared__ uint32_t arrival;
+  float* tile = reinterpret_cast<float*>(xs);  // partial tile aliases the x staging area
+
+  const int tid = threadIdx.x;
+  const int n_tiles = p.n_tiles;
+  const int bid = blockIdx.x;
+  const int q = bid / kXcds;
+  const int split = q % splits;
+  const int head = (q / splits) * kXcds + bid % kXcds;
+  if (head >= n_tiles) return;  // padding workgroup
+  const int M = int(p.M);
+  const int nkt = int(p.K / kBK);
   int proj, hh;
   split_head(head, e.Hq, e.Hkv, proj, hh);
 
-  // ---- weight stream setup ---------------------------------------------------
-  // 16x16x32 operand layout: lane (c = lane & 15, g = lane >> 4) holds column c
-  // (B) / row c (A) and 8 k values.  Chosen k order inside a 64-wide tile:
-  // block kk (0,1) of 32, lane group g -> k = kk*32 + g*8 .. +8, so one load
-  // instruction reads 64 contiguous bytes from each of 16 weight rows.
-  const int c16 = lane & 15;
-  const int g4 = lane >> 4;
-  const int64_t col_base = int64_t(hh) * kHeadDim + wave * 32;  // column inside the projection
-  const uint16_t* wrow[2];
-  const int32_t* qrow[2];
-  float wscale[2] = {0.f, 0.f}, wzero[2] = {0.f, 0.f};
-  int64_t qstride = 0;
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int64_t col = col_base + nb * 16 + c16;
-    if constexpr (!INT4) {
-      wrow[nb] = w.w[proj] + col * p.K + kbeg + g4 * 8;
-    } else {
-      qstride = w.n_cols[proj];
-      qrow[nb] = w.qw[proj] + (kbeg / 8 + g4) * qstride + col;
-    }
-  }
+  int kt0, nk;
+  split_range(split, splits, nkt, kt0, nk);
+  compute_partial<INT4>(p, w, proj, hh, kt0, nk, xs, tile);
 
-  // Stage x[0:M, kbeg : kbeg + nk*64] into LDS (rows >= M are never read back
-  // into a stored result: MFMA row r of the output depends only on row r of x).
+  // ---- publish the partial: part[split][head] = [64][128] fp32 row-major -------
   {
-    const int chunks_per_row = nk * 8;
-    const int total = M * chunks_per_row;
-    for (int ci = tid; ci < total; ci += kDecThreads) {
-      const int row = ci / chunks_per_row, q = ci - row * chunks_per_row;
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(p.x + int64_t(row) * p.K + kbeg + q * 8);
-      *reinterpret_cast<u32x4_t*>(xs + dec_lds_off(row, q)) = v;
+    const int r = tid >> 4, c8 = (tid & 15) * 8;  // row, 8 consecutive columns
+    if (r < M) {
+      float* dst = part + (int64_t(split) * n_tiles + head) * kTileFloats + r * kHeadDim + c8;
+      *reinterpret_cast<f32x4_t*>(dst) = *reinterpret_cast<const f32x4_t*>(tile + r * kPitch + c8);
+      *reinterpret_cast<f32x4_t*>(dst + 4) = *reinterpret_cast<const f32x4_t*>(tile + r * kPitch + c8 + 4);
     }
   }
-
-  // Weight ring: for bf16, 4 x 16 B per lane per k tile; for int4, 4 words.
-  u32x4_t wb[kPrefetch][4];
-  uint32_t wq[kPrefetch][4];
-  auto wload = [&](int slot, int kt) {  // kt relative to kt0
-    if constexpr (!INT4) {
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-          wb[slot][nb * 2 + kk] =
-              *reinterpret_cast<const u32x4_t*>(wrow[nb] + int64_t(kt) * kBK + kk * 32);
-    } else {
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-          wq[slot][nb * 2 + kk] = uint32_t(qrow[nb][(int64_t(kt) * 8 + kk * 4) * qstride]);
-    }
-  };
-
-#pragma unroll
-  for (int s = 0; s < kPrefetch; ++s)
-    if (s < nk) wload(s, s);
-
-  __syncthreads();  // x slice visible
-
-  f32x4_t acc[4][2];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = f32x4_t{};
-
-  int cur_group = -1;
-  for (int base = 0; base < nk; base += kPrefetch) {
-#pragma unroll
-    for (int s = 0; s < kPrefetch; ++s) {
-      const int kt = base + s;
-      if (kt < nk) {
-        u32x4_t bfrag[2][2];
-        if constexpr (!INT4) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) bfrag[i >> 1][i & 1] = wb[s][i];
-        } else {
-          const int64_t k_abs = kbeg + int64_t(kt) * kBK;
-          const int grp = int(k_abs / w.group);
-          if (grp != cur_group) {
-            cur_group = grp;
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-              const int64_t col = col_base + nb * 16 + c16;
-              const uint32_t sraw = static_cast<const uint16_t*>(w.sc[proj])[grp * qstride + col];
-              wscale[nb] = w.scale_fp16 ? f16_to_f32(sraw) : bf16_to_f32(sraw);
-              const uint32_t zw = uint32_t(w.qz[proj][grp * (qstride / 8) + col / 8]);
-              wzero[nb] = float((zw >> ((col % 8) * 4)) & 0xFu);
-            }
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            bfrag[i >> 1][i & 1] = dequant_int4x8(wq[s][i], wzero[i >> 1], wscale[i >> 1]);
-        }
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const int chunk = kt * 8 + kk * 4 + g4;
-#pragma unroll
-          for (int mb = 0; mb < 4; ++mb) {
-            const int row = mb * 16 + c16;
-            const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xs + dec_lds_off(row, chunk));
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = mfma_16x16x32(a, bfrag[nb][kk], acc[mb][nb]);
-          }
-        }
-        if (kt + kPrefetch < nk) wload(s, kt + kPrefetch);
-      }
-    }
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have reached the L2
+  __syncthreads();                // ... and every thread's
+  if (tid == 0) {
+    const bool foreign = force_recompute || xcc_id() != bid % kXcds;
+    const uint32_t inc = 1u + (foreign ? kForeignUnit : 0u);
+    arrival = __hip_atomic_fetch_add(counters + head, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
   }
+  __syncthreads();
+  const uint32_t seen = arrival;
+  if ((seen & (kForeignUnit - 1)) != uint32_t(splits)) return;  // not the last split to arrive
+  const bool recompute = (seen >> 16) != 0;
 
-  // ---- publish the partial tile ------------------------------------------------
-  // part layout: [splits][n_tiles][64 rows][128 cols] fp32
-  float* mypart = part + (int64_t(split) * n_tiles + head) * (kDecRows * kHeadDim);
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
+  // ---- last arrival: sum the partials in split order -------------------------------
+  // thread -> row r = tid / 16, c = tid % 16: columns [4c, 4c+4) and
+  // [64+4c, 64+4c+4), so every RoPE pair (d, d+64) is thread-local.
+  const int r = tid >> 4;
+  const int c = tid & 15;
+  float lo[4] = {0.f, 0.f, 0.f, 0.f}, hi[4] = {0.f, 0.f, 0.f, 0.f};
+  if (!recompute) {
+    for (int s0 = 0; s0 < splits; s0 += 4) {
+      f32x4_t pa[4], pb[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int row = mb * 16 + g4 * 4 + j;
-        if (row < M) mypart[row * kHeadDim + wave * 32 + nb * 16 + c16] = acc[mb][nb][j];
+        const int s = s0 + j;
+        if (s < splits && r < M) {
+          const float* src = s == split ? tile + r * kPitch
+                                        : part + (int64_t(s) * n_tiles + head) * kTileFloats + r * kHeadDim;
+          pa[j] = *reinterpret_cast<const f32x4_t*>(src + 4 * c);
+          pb[j] = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + 4 * c);
+        }
       }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) last_flag = (atomicAdd(counters + head, 1) == splits - 1);
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-
-  // ---- last arrival: reduce partials, norm, RoPE, store --------------------------
-  // thread -> row r = tid / 4, quarter q = tid % 4 -> columns [16q, 16q+16) and
-  // [64+16q, 64+16q+16): every RoPE pair (d, d+64) is thread-local.
-  const int r = tid >> 2;
-  const int qq = tid & 3;
-  float lo[16], hi[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) lo[i] = hi[i] = 0.f;
-  if (r < M) {
+      for (int j = 0; j < 4; ++j) {
+        if (s0 + j < splits && r < M) {
+          lo[0] += pa[j].x; lo[1] += pa[j].y; lo[2] += pa[j].z; lo[3] += pa[j].w;
+          hi[0] += pb[j].x; hi[1] += pb[j].y; hi[2] += pb[j].z; hi[3] += pb[j].w;
+        }
+      }
+    }
+  } else {
+    // Some split ran on another XCD: its partial may not be visible through this
+    // L2.  Recompute every split here (same arithmetic, same order).
     for (int s = 0; s < splits; ++s) {
-      const float* src = part + (int64_t(s) * n_tiles + head) * (kDecRows * kHeadDim) + r * kHeadDim;
-#pragma unroll
-      for (int v4 = 0; v4 < 4; ++v4) {
-        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src + qq * 16 + v4 * 4);
-        const f32x4_t b = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + qq * 16 + v4 * 4);
-        lo[v4 * 4 + 0] += a.x; lo[v4 * 4 + 1] += a.y; lo[v4 * 4 + 2] += a.z; lo[v4 * 4 + 3] += a.w;
-        hi[v4 * 4 + 0] += b.x; hi[v4 * 4 + 1] += b.y; hi[v4 * 4 + 2] += b.z; hi[v4 * 4 + 3] += b.w;
+      int s_kt0, s_nk;
+      split_range(s, splits, nkt, s_kt0, s_nk);
+      compute_partial<INT4>(p, w, proj, hh, s_kt0, s_nk, xs, tile);
+      if (r < M) {
+        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(tile + r * kPitch + 4 * c);
+        const f32x4_t b = *reinterpret_cast<const f32x4_t*>(tile + r * kPitch + kHalfDim + 4 * c);
+        lo[0] += a.x; lo[1] += a.y; lo[2] += a.z; lo[3] += a.w;
+        hi[0] += b.x; hi[1] += b.y; hi[2] += b.z; hi[3] += b.w;
       }
+      __syncthreads();  // tile is rewritten by the next split
     }
   }
 
   if (proj != 2) {
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) ss += lo[i] * lo[i] + hi[i] * hi[i];
+    float ss = lo[0] * lo[0] + lo[1] * lo[1] + lo[2] * lo[2] + lo[3] * lo[3] + hi[0] * hi[0] +
+               hi[1] * hi[1] + hi[2] * hi[2] + hi[3] * hi[3];
     ss += __shfl_xor(ss, 1);
     ss += __shfl_xor(ss, 2);
+    ss += __shfl_xor(ss, 4);
+    ss += __shfl_xor(ss, 8);
     const float rms = rsqrtf(ss * (1.0f / float(kHeadDim)) + e.eps);
     if (r < M) {
       const uint16_t* gamma = proj == 0 ? e.q_gamma : e.k_gamma;
       const int64_t prow = rope_row(e.positions, r, e.S, e.cos_rows) * kHeadDim;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = qq * 16 + i;
+      for (int i = 0; i < 4; ++i) {
+        const int d = 4 * c + i;
         const float x1n = lo[i] * rms * bf16_to_f32(gamma[d]);
         const float x2n = hi[i] * rms * bf16_to_f32(gamma[d + kHalfDim]);
         const float c1 = bf16_to_f32(e.cos[prow + d]);
@@ -244,59 +300,72 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   if (r < M) {
     const int H = proj == 0 ? e.Hq : e.Hkv;
     uint16_t* dst = (proj == 0 ? e.q : (proj == 1 ? e.k : e.v)) + (int64_t(r) * H + hh) * kHeadDim;
-    u32x4_t o;
-#pragma unroll
-    for (int h8 = 0; h8 < 2; ++h8) {
-      o.x = pack_bf16x2(lo[h8 * 8 + 0], lo[h8 * 8 + 1]);
-      o.y = pack_bf16x2(lo[h8 * 8 + 2], lo[h8 * 8 + 3]);
-      o.z = pack_bf16x2(lo[h8 * 8 + 4], lo[h8 * 8 + 5]);
-      o.w = pack_bf16x2(lo[h8 * 8 + 6], lo[h8 * 8 + 7]);
-      *reinterpret_cast<u32x4_t*>(dst + qq * 16 + h8 * 8) = o;
-      o.x = pack_bf16x2(hi[h8 * 8 + 0], hi[h8 * 8 + 1]);
-      o.y = pack_bf16x2(hi[h8 * 8 + 2], hi[h8 * 8 + 3]);
-      o.z = pack_bf16x2(hi[h8 * 8 + 4], hi[h8 * 8 + 5]);
-      o.w = pack_bf16x2(hi[h8 * 8 + 6], hi[h8 * 8 + 7]);
-      *reinterpret_cast<u32x4_t*>(dst + kHalfDim + qq * 16 + h8 * 8) = o;
-    }
+    u32x2_t o;
+    o.x = pack_bf16x2(lo[0], lo[1]);
+    o.y = pack_bf16x2(lo[2], lo[3]);
+    *reinterpret_cast<u32x2_t*>(dst + 4 * c) = o;
+    o.x = pack_bf16x2(hi[0], hi[1]);
+    o.y = pack_bf16x2(hi[2], hi[3]);
+    *reinterpret_cast<u32x2_t*>(dst + kHalfDim + 4 * c) = o;
   }
-  if (tid == 0) atomicExch(counters + head, 0);
+  if (tid == 0) __hip_atomic_store(counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+int g_cus_per_xcd = 0;  // queried once (single-device processes)
+
+int cus_per_xcd() {
+  if (g_cus_per_xcd <= 0) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus >= kXcds)
+      g_cus_per_xcd = cus / kXcds;
+    else
+      g_cus_per_xcd = 32;  // MI355X: 256 CUs / 8 XCDs
+    (void)hipGetLastError();
+  }
+  return g_cus_per_xcd;
 }
 
 }  // namespace
 
+int g_decode_force_recompute = 0;
+
 int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested) {
+  (void)M;
   const int nkt = int(K / kBK);
-  const int min_splits = (int(K) + kDecMaxKc - 1) / kDecMaxKc;  // LDS bound on the k-range
+  if (nkt < 1) return 0;
+  const int min_splits = (nkt + kDecMaxNK - 1) / kDecMaxNK;  // LDS bound on a split's k-range
   int s = requested;
   if (s <= 0) {
-    // Keep each workgroup's weight slice >= 4x its fp32 partial tile
-    // (128*kc*2 bytes vs M*128*4) and aim for ~1.5 workgroups per CU.
-    const int64_t kc_min = ((8 * M + kBK - 1) / kBK) * kBK;
-    int by_traffic = int(K / (kc_min > 0 ? kc_min : kBK));
-    int by_fill = (384 + n_tiles - 1) / n_tiles;
-    s = by_fill < by_traffic ? by_fill : by_traffic;
+    // one workgroup per CU: (heads per XCD) x splits <= CUs per XCD
+    const int heads_per_xcd = (n_tiles + kXcds - 1) / kXcds;
+    s = cus_per_xcd() / heads_per_xcd;
+    if (s < min_splits) s = min_splits;
   }
-  if (s < min_splits) s = min_splits;
-  if (s > nkt) s = nkt;
-  if (s < 1) s = 1;
+  if (s < min_splits || s > nkt || s > kDecMaxNK) return 0;
   return s;
 }
 
 size_t decode_workspace_bytes(int n_tiles, int splits) {
-  return size_t(kCounterBytes) + size_t(splits) * n_tiles * kDecRows * kHeadDim * sizeof(float);
+  return size_t(kCounterBytes) + size_t(splits) * n_tiles * kTileFloats * sizeof(float);
 }
 
 hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                          int splits, void* workspace, hipStream_t stream) {
-  int* counters = static_cast<int*>(workspace);
+  const int nkt = int(p.K / kBK);
+  if (splits < 1 || splits > kDecMaxNK || splits > nkt || (nkt + splits - 1) / splits > kDecMaxNK ||
+      p.n_tiles > kMaxHeads)
+    return hipErrorInvalidValue;
+  uint32_t* counters = static_cast<uint32_t*>(workspace);
   float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-  const int blocks = p.n_tiles * splits;
+  const dim3 grid(((p.n_tiles + kXcds - 1) / kXcds) * kXcds * splits);
+  const int fr = g_decode_force_recompute;
   if (int4)
-    hipLaunchKernelGGL(decode_kernel<true>, dim3(blocks), dim3(kDecThreads), 0, stream, p, w, e,
-                       splits, part, counters);
+    hipLaunchKernelGGL(decode_kernel<true>, grid, dim3(kDecThreads), 0, stream, p, w, e, splits, part, counters,
+                       fr);
   else
-    hipLaunchKernelGGL(decode_kernel<false>, dim3(blocks), dim3(kDecThreads), 0, stream, p, w, e,
-                       splits, part, counters);
+    hipLaunchKernelGGL(decode_kernel<false>, grid, dim3(kDecThreads), 0, stream, p, w, e, splits, part,
+                       counters, fr);
   return hipGetLastError();
 }
 

@@ -151,6 +151,31 @@ def test_decode_and_tile_paths_agree(device):
     _check(b, case.oracle(), "tile path")
 
 
+@pytest.mark.parametrize("splits,recompute", [(0, 0), (0, 1), (4, 0), (8, 0), (16, 0), (16, 1), (7, 0)])
+def test_decode_variants(splits, recompute, device):
+    """Split counts of the decode kernel, and its recompute path (taken when a
+    split runs on an unexpected XCD), which must give bit-identical results."""
+    import mqk
+    g = torch.Generator().manual_seed(600 + splits)
+    pos = torch.randint(0, 8192, (64,), generator=g).to(torch.int32)
+    case = Case(64, 1, 4096, 32, 8, seed=600 + splits, rows=8192, positions=pos)
+    names = ("decode_splits", "decode_force_recompute")
+    old = [mqk.get_option(n) for n in names]
+    try:
+        mqk.set_option("decode_splits", splits)
+        ref_path = _run(case, device)
+        mqk.set_option("decode_force_recompute", recompute)
+        out = _run(case, device)
+        again = _run(case, device)
+    finally:
+        for n, val in zip(names, old):
+            mqk.set_option(n, val)
+    for a, b, c in zip(out, again, ref_path):
+        assert torch.equal(a, b)
+        assert torch.equal(a, c)
+    _check(out, case.oracle(), f"decode splits={splits} recompute={recompute}")
+
+
 def test_decode_repeatable(device):
     """Arrival counters are reset by each call: repeated calls give identical bits."""
     case = Case(32, 1, 4096, 32, 8, seed=12, rows=8192,
