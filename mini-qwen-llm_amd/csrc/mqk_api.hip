@@ -291,6 +291,10 @@ int mqk_set_option(const char* name, int64_t value) {
   } else if (!strcmp(name, "decode_force_recompute")) {
     if (value != 0 && value != 1) return fail(MQK_ERR_BAD_OPTION, "decode_force_recompute must be 0 or 1");
     g_decode_force_recompute = int(value);
+#ifdef MQK_DECODE_TRACE
+  } else if (!strcmp(name, "decode_trace")) {  // diagnostic builds only
+    set_decode_trace(reinterpret_cast<void*>(value));
+#endif
   } else if (!strcmp(name, "group_m")) {
     if (value < 1 || value > 1024) return fail(MQK_ERR_BAD_OPTION, "group_m must be in [1, 1024]");
     g_group_m = value;
