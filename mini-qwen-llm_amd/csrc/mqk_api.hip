@@ -93,8 +93,11 @@ int run_fused(int int4, const ProblemArgs& p, const WeightArgs& w, const Epilogu
     return hip_status(launch_decode(int4, p, w, e, splits, workspace, stream), "decode kernel launch");
   }
   const TileVariant* v = choose_tile_variant(int(g_prefill_tile.load()), p.M, p.n_tiles, int4);
-  if (!v) return fail(MQK_ERR_BAD_OPTION, "prefill_tile variant %lld cannot tile %d heads",
-                      (long long)g_prefill_tile.load(), p.n_tiles);
+  if (!v) return fail(MQK_ERR_BAD_OPTION, "prefill_tile variant %lld cannot run this problem (%d heads%s)",
+                      (long long)g_prefill_tile.load(), p.n_tiles, int4 ? ", int4 weights" : "");
+  // The pipelined variants read gamma/cos/sin rows with 16-byte loads.
+  if (v->id >= 10 && !(aligned16(e.q_gamma) && aligned16(e.k_gamma) && aligned16(e.cos) && aligned16(e.sin)))
+    v = choose_tile_variant(p.n_tiles % 2 == 0 ? 4 : 1, p.M, p.n_tiles, int4);
   return hip_status(launch_tile(*v, int4, p, w, e, int(g_group_m.load()), stream), "tile kernel launch");
 }
 
@@ -322,7 +325,7 @@ const char* mqk_tile_variants(void) {
     for (int i = 0; i < tile_variant_count(); ++i) {
       const TileVariant* v = tile_variant(i);
       n += snprintf(buf + n, sizeof(buf) - n, "%s%d:%dx%d/%dw", i ? ";" : "", v->id, v->bm,
-                    v->hpt * kHeadDim, v->threads / 64);
+                                    v->hpt * kHeadDim, v->threads / 64);
     }
     return buf;
   }();

@@ -65,6 +65,9 @@ const TileVariant* tile_variant(int index);
 const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles, int int4);
 hipError_t launch_tile(const TileVariant& v, int int4, const ProblemArgs& p, const WeightArgs& w,
                        const EpilogueArgs& e, int group_m, hipStream_t stream);
+// Direct-to-LDS pipelined tile kernel (variant ids >= 10, bf16 weights).
+hipError_t launch_tile_dma(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e, int group_m,
+                           hipStream_t stream);
 
 // Split-K decode kernel for T <= 64.  decode_splits_for returns 0 when no
 // valid split count exists (each split covers at most 16 64-wide k tiles);

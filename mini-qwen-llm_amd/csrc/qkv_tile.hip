@@ -350,12 +350,20 @@ hipError_t launch_dispatch(int int4, const ProblemArgs& p, const WeightArgs& w,
               : launch_impl<BM, HPT, KZ, false>(p, w, e, group_m, stream);
 }
 
+// ids 1-5: register-staged kernel above (bf16 and int4 weights);
+// ids 10-14: direct-to-LDS pipelined kernel (qkv_tile_dma.hip, bf16 weights only).
 const TileVariant kVariants[] = {
     {1, 128, 1, 2, 256},
     {2, 256, 1, 1, 256},
     {3, 128, 2, 1, 256},
     {4, 256, 2, 1, 512},
     {5, 128, 2, 2, 512},
+    {10, 256, 2, 0, 512},
+    {11, 128, 3, 0, 512},
+    {12, 256, 1, 0, 256},
+    {13, 128, 2, 0, 256},
+    {14, 256, 2, 0, 512},
+    {15, 128, 3, 0, 512},
 };
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 
@@ -367,21 +375,48 @@ const TileVariant* tile_variant(int index) {
   return (index >= 0 && index < kNumVariants) ? &kVariants[index] : nullptr;
 }
 
+const TileVariant* find_variant(int id) {
+  for (const auto& v : kVariants)
+    if (v.id == id) return &v;
+  return nullptr;
+}
+
 const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles, int int4) {
   if (requested_id > 0) {
-    for (const auto& v : kVariants)
-      if (v.id == requested_id) return (n_tiles % v.hpt == 0) ? &v : nullptr;
-    return nullptr;
+    const TileVariant* v = find_variant(requested_id);
+    if (!v || n_tiles % v->hpt != 0 || (int4 && v->id >= 10)) return nullptr;
+    return v;
   }
-  (void)int4;
-  // 256x256 (8 waves, two heads per tile) measured fastest on the Qwen3-8B and
-  // 30B-A3B prefill shapes; it needs an even head count and enough row tiles.
-  if (n_tiles % 2 == 0 && M >= 512) return &kVariants[3];
-  return &kVariants[0];  // 128x128, 4 waves: valid for every head count
+  // Score = relative per-tile speed (measured on MI355X) x fraction of the last
+  // round of workgroups that is busy, assuming one workgroup per CU at a time.
+  struct Cand { int id; float speed; };
+  static const Cand bf16_cands[] = {{11, 1.00f}, {10, 1.03f}, {13, 0.85f}, {12, 0.85f}, {1, 0.55f}};
+  static const Cand int4_cands[] = {{4, 1.00f}, {2, 0.90f}, {3, 0.90f}, {1, 0.80f}};
+  const Cand* cands = int4 ? int4_cands : bf16_cands;
+  const int ncand = int4 ? 4 : 5;
+  const int64_t cus = 256;
+  const TileVariant* best = find_variant(1);
+  float best_score = -1.f;
+  for (int i = 0; i < ncand; ++i) {
+    const TileVariant* v = find_variant(cands[i].id);
+    if (!v || n_tiles % v->hpt != 0) continue;
+    const int64_t tiles = ((M + v->bm - 1) / v->bm) * (n_tiles / v->hpt);
+    const int64_t rounds = (tiles + cus - 1) / cus;
+    const float util = float(tiles) / float(rounds * cus);
+    // rows past M in the last row tile are wasted work
+    const float fill = float(M) / float(((M + v->bm - 1) / v->bm) * v->bm);
+    const float score = cands[i].speed * util * fill;
+    if (score > best_score) {
+      best_score = score;
+      best = v;
+    }
+  }
+  return best;
 }
 
 hipError_t launch_tile(const TileVariant& v, int int4, const ProblemArgs& p, const WeightArgs& w,
                        const EpilogueArgs& e, int group_m, hipStream_t stream) {
+  if (v.id >= 10) return int4 ? hipErrorInvalidValue : launch_tile_dma(v.id, p, w, e, group_m, stream);
   switch (v.id) {
     case 1: return launch_dispatch<128, 1, 2>(int4, p, w, e, group_m, stream);
     case 2: return launch_dispatch<256, 1, 1>(int4, p, w, e, group_m, stream);

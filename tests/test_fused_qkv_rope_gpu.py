@@ -187,6 +187,21 @@ def test_decode_repeatable(device):
             assert torch.equal(x, y)
 
 
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5, 10, 11, 12, 13, 14])
+def test_tile_variants(variant, device):
+    """Every prefill tile variant, on a shape with a row tail (M = 600) and a
+    head count (24) that all of them can tile."""
+    import mqk
+    case = Case(2, 300, 2048, 16, 4, seed=700 + variant)
+    old = mqk.get_option("prefill_tile")
+    try:
+        mqk.set_option("prefill_tile", variant)
+        out = _run(case, device)
+    finally:
+        mqk.set_option("prefill_tile", old)
+    _check(out, case.oracle(), f"tile variant {variant}")
+
+
 @pytest.mark.parametrize("Hq,Hkv", [(8, 8), (32, 4), (40, 8), (12, 2)])
 def test_gqa_ratios(Hq, Hkv, device):
     case = Case(2, 96, 1024, Hq, Hkv, seed=500 + Hq)
