@@ -402,6 +402,7 @@ int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested) {
     // one workgroup per CU: (heads per XCD) x splits <= CUs per XCD
     const int heads_per_xcd = (n_tiles + kXcds - 1) / kXcds;
     s = cus_per_xcd() / heads_per_xcd;
+    if (s > nkt) s = nkt;  // small hidden: at most one k tile per split
     if (s < min_splits) s = min_splits;
   }
   if (s < min_splits || s > nkt || s > kDecMaxNK) return 0;

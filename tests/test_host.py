@@ -1,0 +1,246 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every
+entry point include/mqk.h declares, argument validation returns the documented
+error codes before anything is launched, the option knobs, the no-fallback
+rule, and the torch-side format utilities against the oracle.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import qkv_rope_oracle as orc
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "mqk.h"
+LIB = ROOT / "mini-qwen-llm_amd" / "mqk" / "libmqk.so"
+
+needs_lib = pytest.mark.skipif(not LIB.exists(), reason="libmqk.so not built (run __graft_entry__.build())")
+
+
+def header_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(mqk_[a-z0-9_]+)\s*\(", text)))
+
+
+# ── symbols ───────────────────────────────────────────────────────────────────
+
+def test_header_lists_expected_entry_points():
+    names = header_functions()
+    for n in ("mqk_fused_qkv_rope_bf16", "mqk_qk_norm_rope_bf16", "mqk_w4a16_gemm",
+              "mqk_fused_qkv_rope_w4a16", "mqk_fused_qkv_rope_workspace_size"):
+        assert n in names
+
+
+@needs_lib
+def test_library_exports_every_header_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(LIB)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    missing = [n for n in header_functions() if n not in exported]
+    assert not missing, f"libmqk.so lacks {missing}"
+
+
+@needs_lib
+def test_ctypes_signatures_cover_header():
+    from mqk import _native
+    assert sorted(_native.SIGNATURES) == header_functions()
+
+
+# ── calls that never reach a kernel ──────────────────────────────────────────
+
+@pytest.fixture(scope="module")
+def lib():
+    if not LIB.exists():
+        pytest.skip("libmqk.so not built")
+    from mqk import _native
+    return _native.library()
+
+
+def test_version_and_error_strings(lib):
+    assert lib.mqk_version() >= 100
+    for code, text in ((0, "ok"), (-1, "null"), (-2, "shape"), (-3, "unsupported"), (-4, "aligned"),
+                       (-5, "workspace"), (-6, "HIP"), (-7, "option")):
+        assert text in lib.mqk_error_string(code).decode()
+    assert "unknown" in lib.mqk_error_string(-99).decode()
+
+
+def _fused(lib, **kw):
+    """Call mqk_fused_qkv_rope_bf16 with fake (never dereferenced) pointers."""
+    fake = 1 << 20  # 16-byte aligned, never touched: every case fails validation first
+    a = dict(x=fake, w_q=fake, w_k=fake, w_v=fake, q_gamma=fake, k_gamma=fake, cos=fake, sin=fake,
+             positions=None, T=4, S=4, hidden=256, Hq=2, Hkv=1, D=128, cos_rows=4, eps=1e-6,
+             q=fake, k=fake, v=fake, ws=None, ws_bytes=0, stream=None)
+    a.update(kw)
+    return lib.mqk_fused_qkv_rope_bf16(a["x"], a["w_q"], a["w_k"], a["w_v"], a["q_gamma"], a["k_gamma"],
+                                       a["cos"], a["sin"], a["positions"], a["T"], a["S"], a["hidden"],
+                                       a["Hq"], a["Hkv"], a["D"], a["cos_rows"], a["eps"], a["q"], a["k"],
+                                       a["v"], a["ws"], a["ws_bytes"], a["stream"])
+
+
+@pytest.mark.parametrize("kw,code,detail", [
+    (dict(D=64), -3, "head_dim 64"),
+    (dict(D=127), -2, "even"),
+    (dict(hidden=96), -3, "multiple of 64"),
+    (dict(T=-1), -2, "T >= 0"),
+    (dict(Hkv=0), -2, "Hkv > 0"),
+    (dict(x=None), -1, "x/q/k/v"),
+    (dict(w_v=None), -1, "w_q/w_k/w_v"),
+    (dict(cos=None), -1, "cos"),
+    (dict(q=(1 << 20) + 2), -4, "aligned"),
+    (dict(cos_rows=0), -2, "cos_rows"),
+    (dict(S=0), -2, "S > 0"),
+    (dict(eps=-1.0), -2, "eps"),
+    (dict(Hq=1100), -3, "<= 1024"),
+])
+def test_fused_validation(lib, kw, code, detail):
+    assert _fused(lib, **kw) == code
+    assert detail in lib.mqk_last_error_detail().decode()
+
+
+def test_fused_empty_is_noop(lib):
+    assert _fused(lib, T=0, x=None, q=None, k=None, v=None) == 0
+    assert lib.mqk_last_error_detail().decode() == ""
+
+
+def test_decode_needs_workspace(lib):
+    """T <= 64 routes to the split-K kernel, which needs its workspace."""
+    assert _fused(lib, T=8, ws=None) == -5
+    assert "workspace" in lib.mqk_last_error_detail().decode()
+
+
+def test_workspace_size(lib):
+    assert lib.mqk_fused_qkv_rope_workspace_size(512, 32, 8, 4096) == 0      # tile kernel
+    assert lib.mqk_fused_qkv_rope_workspace_size(0, 32, 8, 4096) == 0
+    n = lib.mqk_fused_qkv_rope_workspace_size(64, 32, 8, 4096)
+    assert n >= 4096 + 48 * 64 * 128 * 4  # counters + at least one fp32 partial per head
+
+
+def test_w4a16_validation(lib):
+    fake = 1 << 20
+    call = lambda M=4, K=256, N=64, g=128, st=0, qw=fake: lib.mqk_w4a16_gemm(
+        fake, qw, fake, fake, M, K, N, g, st, fake, None)
+    assert call(N=12) == -2
+    assert call(g=96) == -2         # K % group
+    assert call(st=5) == -2
+    assert call(qw=None) == -1
+    assert call(K=96, g=32) == -3
+    assert call(M=0) == 0
+
+
+def test_qk_norm_rope_validation(lib):
+    fake = 1 << 20
+    f = lambda T=4, Hq=2, Hkv=1, D=128, qr=fake: lib.mqk_qk_norm_rope_bf16(
+        qr, fake, fake, fake, fake, fake, None, T, 4, Hq, Hkv, D, 4, 1e-6, fake, fake, None)
+    assert f(D=96) == -3
+    assert f(qr=None) == -1
+    assert f(T=0) == 0
+    assert f(Hq=0, Hkv=0) == 0
+
+
+def test_options_roundtrip(lib):
+    from mqk import _native
+    assert _native.get_option("decode_max_t") == 64
+    for name, val in (("prefill_tile", 11), ("decode_max_t", 16), ("decode_splits", 4), ("group_m", 8),
+                      ("decode_force_recompute", 1)):
+        old = _native.get_option(name)
+        _native.set_option(name, val)
+        assert _native.get_option(name) == val
+        _native.set_option(name, old)
+    with pytest.raises(_native.MqkNativeError, match="unknown prefill_tile"):
+        _native.set_option("prefill_tile", 999)
+    with pytest.raises(_native.MqkNativeError, match="unknown option"):
+        _native.set_option("no_such_knob", 1)
+    assert _native.get_option("no_such_knob") == -1
+    assert re.fullmatch(r"(\d+:\d+x\d+/\d+w;?)+", _native.tile_variants())
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    """No fallback: pointing the loader at a missing library raises on use."""
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "import torch, mqk\n"
+            "x = torch.zeros(1, 2, 128, dtype=torch.bfloat16)\n"
+            "try:\n"
+            "    mqk.version()\n"
+            "except mqk.MqkNativeError as e:\n"
+            "    print('RAISED', e)\n") % str(ROOT / "mini-qwen-llm_amd")
+    env = {"MQK_LIBRARY": str(tmp_path / "nope.so"), "PATH": "/usr/bin:/bin",
+           "HOME": str(tmp_path)}
+    import os
+    env = {**os.environ, **env}
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300)
+    assert "RAISED" in r.stdout and "not found" in r.stdout, r.stdout + r.stderr
+
+
+def test_fused_op_rejects_cpu_tensors():
+    """The Python drop-in never computes on the host."""
+    import mqk
+    from mqk import _native
+    x = torch.zeros(1, 4, 256, dtype=torch.bfloat16)
+    w = torch.zeros(256, 256, dtype=torch.bfloat16)
+    wk = torch.zeros(128, 256, dtype=torch.bfloat16)
+    g = torch.ones(128, dtype=torch.bfloat16)
+    c = torch.ones(4, 128, dtype=torch.bfloat16)
+    with pytest.raises((ValueError, RuntimeError, _native.MqkNativeError)):
+        mqk.fused_qkv_rope(x, w, wk, wk, g, g, c, c)
+
+
+# ── torch host utilities vs the oracle ────────────────────────────────────────
+
+def test_torch_rope_tables_match_oracle():
+    import mqk
+    for theta in (1e6, 1e4):
+        c, s = mqk.rope_tables(128, 4096, theta)
+        oc, os_ = orc.rope_tables(128, 4096, theta)
+        # same fp32 operation sequence; torch's and numpy's pow/cos/sin may differ
+        # by an ulp, i.e. an angle error of ~|angle| * 2^-23
+        tol = np.arange(4096, dtype=np.float64)[:, None] * 2.0 ** -22 + 2e-6
+        assert np.all(np.abs(c.numpy() - oc) <= tol) and np.all(np.abs(s.numpy() - os_) <= tol)
+
+
+def test_torch_rotary_rows_and_apply():
+    import mqk
+    rope = mqk.RotaryEmbedding(128, 64)
+    pos = torch.tensor([5, 0, 63])
+    c, s = rope.rows(pos, torch.float32)
+    assert torch.equal(c, rope.cos_cached[pos])
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((1, 64, 2, 128)).astype(np.float32)
+    cc, ss = rope(64)
+    qo, _ = mqk.apply_rotary_emb(torch.from_numpy(q), torch.from_numpy(q), cc, ss)
+    ref = orc.rope(q.reshape(64, 2, 128), cc.numpy(), ss.numpy()).reshape(1, 64, 2, 128)
+    np.testing.assert_allclose(qo.numpy(), ref, atol=1e-5)
+
+
+def test_torch_pack_matches_oracle():
+    import mqk
+    rng = np.random.default_rng(1)
+    v = rng.integers(0, 16, (64, 256))
+    t = mqk.pack_int4(torch.from_numpy(v))
+    assert np.array_equal(t.numpy(), orc.pack_int4(v))
+    assert np.array_equal(mqk.unpack_int4(t).numpy(), v)
+
+
+def test_torch_quantizer_matches_oracle():
+    import mqk
+    rng = np.random.default_rng(2)
+    w = rng.standard_normal((512, 64)).astype(np.float32)
+    qw, sc, qz = mqk.per_group_minmax_quantize(torch.from_numpy(w), 128)
+    oqw, osc, oqz = orc.minmax_quantize(w, 128)
+    assert np.array_equal(qw.numpy(), oqw) and np.array_equal(qz.numpy(), oqz)
+    assert np.array_equal(sc.view(torch.int16).numpy().view(np.uint16), osc)
+    deq = mqk.dequantize(qw, sc, qz, 128).numpy()
+    np.testing.assert_array_equal(deq, orc.dequant(oqw, orc.bf16_to_f32(osc), oqz, 128))
+
+
+def test_torch_gptq_fix_matches_oracle():
+    import mqk
+    z = np.random.default_rng(3).integers(0, 16, (4, 32))
+    pz = orc.pack_int4(z)
+    assert np.array_equal(mqk.gptq_zero_fix(torch.from_numpy(pz)).numpy(), orc.gptq_zero_fix(pz))
