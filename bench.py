@@ -2,6 +2,7 @@
 """Benchmark of the fused QKV + QK-Norm + RoPE op on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
+    python bench.py --only {c2,c3,c4,c5,copy} --steps K   # one workload, for profiler runs
 
 Headline (``value``): BASELINE config 2, Qwen3-8B prefill B=4 x S=512 (2048
 tokens, hidden 4096, 32 Q heads, 8 KV heads, head_dim 128, bf16), tokens/s of
@@ -65,21 +66,32 @@ def make_inputs(T, hidden, Hq, Hkv, rows, seed, dev, copies=1):
 
 
 def time_steps(fn, steps, warmup):
-    """(ms per step, wall seconds) for `steps` calls after `warmup` untimed ones."""
+    """(ms per step, wall seconds, ms per launch) for `steps` calls after `warmup` untimed ones.
+
+    Step time: one HIP event pair around all `steps` calls.  Launch time: an
+    event pair around every call, averaged -- the duration of the op's kernel
+    alone, used for the roofline.  All events are recorded on the current
+    stream, the one the mqk ops launch on.
+    """
     import torch
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record()
     for i in range(steps):
+        ev[i][0].record()
         fn(i)
+        ev[i][1].record()
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return e0.elapsed_time(e1) / steps, wall
+    per_launch = sum(a.elapsed_time(b) for a, b in ev) / steps
+    return e0.elapsed_time(e1) / steps, wall, per_launch
 
 
 def bench_prefill(S_total, B, S, hidden, Hq, Hkv, seed, steps, warmup, dev):
@@ -87,9 +99,7 @@ def bench_prefill(S_total, B, S, hidden, Hq, Hkv, seed, steps, warmup, dev):
     x, ws, gq, gk, cos, sin = make_inputs(S_total, hidden, Hq, Hkv, S, seed, dev)
     x = x.reshape(B, S, hidden)
     wq, wk, wv = ws[0]
-    ms, wall = time_steps(lambda i: mqk.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin),
-                          steps, warmup)
-    return ms, wall
+    return time_steps(lambda i: mqk.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin), steps, warmup)
 
 
 def bench_decode(B, hidden, Hq, Hkv, seed, steps, warmup, dev, copies=8):
@@ -131,9 +141,9 @@ def bench_w4a16(hidden, Hq, Hkv, seed, steps, warmup, dev):
     gk = (1 + 0.1 * torch.randn(D, generator=gd, device=dev)).bfloat16()
     cos, sin = (t.to(dev).bfloat16() for t in mqk.rope_tables(D, 8192))
     pos = pos.to(dev)
-    ms, _ = time_steps(lambda i: mqk.fused_qkv_rope_w4a16(x, *projs, gq, gk, cos, sin, pos),
-                       steps, warmup)
-    return ms, T
+    ms, _, launch = time_steps(lambda i: mqk.fused_qkv_rope_w4a16(x, *projs, gq, gk, cos, sin, pos),
+                               steps, warmup)
+    return ms, launch, T
 
 
 def cpu_baseline(budget_s=12.0):
@@ -182,6 +192,44 @@ def load_traffic(name):
     return None
 
 
+def decode_bytes(B, hidden, N):
+    """Algorithmic HBM bytes of one decode launch: weights + x + q/k/v outputs +
+    the B cos/sin rows + gammas + positions (each read or written once)."""
+    return N * hidden * 2 + B * hidden * 2 + B * N * 2 + B * D * 2 * 2 + 2 * D * 2 + B * 4
+
+
+def copy_kernel(nbytes, steps, dev):
+    """A plain device-to-device copy of known size: the calibration kernel of the
+    FETCH_SIZE / WRITE_SIZE counters (reads and writes nbytes per launch)."""
+    import torch
+    a = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).normal_()
+    b = torch.empty_like(a)
+    for _ in range(steps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+
+
+WORKLOADS = ("c2", "c3", "c4", "c5", "copy")
+
+
+def run_only(name, steps, warmup, dev):
+    """One workload alone (for profiler runs); prints one JSON line of timings."""
+    B, S, hidden, Hq, Hkv = 4, 512, 4096, 32, 8
+    if name == "c2":
+        ms, _, launch = bench_prefill(B * S, B, S, hidden, Hq, Hkv, 1, steps, warmup, dev)
+    elif name == "c3":
+        ms, _, launch = bench_decode(64, hidden, Hq, Hkv, 2, steps, warmup, dev)
+    elif name == "c4":
+        ms, _, launch = bench_prefill(8192, 1, 8192, 2048, 32, 4, 3, steps, warmup, dev)
+    elif name == "c5":
+        ms, launch, _ = bench_w4a16(hidden, Hq, Hkv, 4, steps, warmup, dev)
+    else:
+        copy_kernel(256 << 20, steps, dev)
+        ms = launch = float("nan")
+    print(json.dumps({"workload": name, "steps": steps, "ms_per_step": ms, "ms_per_launch": launch}),
+          flush=True)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="mqk fused QKV + QK-Norm + RoPE benchmark")
     ap.add_argument("--gpus", type=int, default=1)
@@ -189,6 +237,8 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip configs 3-5")
+    ap.add_argument("--only", choices=WORKLOADS,
+                    help="run one workload alone (profiler runs; 'copy' = 256 MiB calibration copy)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the op has no multi-GPU path); "
@@ -202,15 +252,19 @@ def main(argv=None) -> int:
         return 2
     dev = torch.device("cuda:0")
     mqk.library()  # fail loudly before any timing if libmqk.so is missing
+    if args.only:
+        run_only(args.only, args.steps, args.warmup, dev)
+        return 0
 
     # ---- headline: config 2, Qwen3-8B prefill B=4 x S=512 ---------------------
     B, S, hidden, Hq, Hkv = 4, 512, 4096, 32, 8
     T = B * S
     N = (Hq + 2 * Hkv) * D
     log(f"[bench] config 2 prefill T={T} hidden={hidden} N={N}: {args.warmup} warmup + {args.steps} steps")
-    ms, wall = bench_prefill(T, B, S, hidden, Hq, Hkv, 1, args.steps, args.warmup, dev)
+    ms, wall, launch = bench_prefill(T, B, S, hidden, Hq, Hkv, 1, args.steps, args.warmup, dev)
     fl = flops(T, hidden, N)
-    achieved = fl / (ms * 1e-3) / 1e12
+    achieved = fl / (launch * 1e-3) / 1e12
+    log(f"[bench] config 2: {ms * 1e3:.1f} us/step, {launch * 1e3:.1f} us/launch, {achieved:.0f} TFLOP/s")
     result = {
         "metric": "fused QKV+QKNorm+RoPE tokens/s and % roofline (Qwen3-8B shapes, bf16, 1 GPU)",
         "value": round(T / (ms * 1e-3), 1),
@@ -229,39 +283,40 @@ def main(argv=None) -> int:
                    "heads_q": Hq, "heads_kv": Hkv, "head_dim": D, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": load_traffic("qkv_tile_c2_prefill_traffic")},
+                     "traffic": load_traffic("qkv_tile_dma_c2_traffic"),
+                     "ms_per_launch": round(launch, 6), "flop_per_launch": fl},
         "wall_s_timed": round(wall, 4),
     }
 
     if not args.no_secondary:
         sec = {}
         # config 3: decode B=64, weight-read bound
-        dms, _ = bench_decode(64, hidden, Hq, Hkv, 2, max(50, args.steps), 10, dev)
-        dbytes = (N * hidden * 2 + 64 * hidden * 2 + 64 * N * 2 + 64 * D * 2 * 2 + 2 * D * 2 + 64 * 4)
-        dgbs = dbytes / (dms * 1e-3) / 1e9
+        dms, _, dl = bench_decode(64, hidden, Hq, Hkv, 2, max(50, args.steps), 10, dev)
+        dgbs = decode_bytes(64, hidden, N) / (dl * 1e-3) / 1e9
         sec["config3_decode_b64"] = {"tokens_per_s": round(64 / (dms * 1e-3), 1),
-                                     "ms_per_step": round(dms, 6), "bound": "hbm",
-                                     "achieved_GBps": round(dgbs, 1),
-                                     "frac": round(dgbs / PEAK_HBM_GBS, 4)}
-        log(f"[bench] config 3 decode: {dms * 1e3:.2f} us, {dgbs:.0f} GB/s")
+                                     "ms_per_step": round(dms, 6), "ms_per_launch": round(dl, 6),
+                                     "bound": "hbm", "achieved_GBps": round(dgbs, 1),
+                                     "frac": round(dgbs / PEAK_HBM_GBS, 4),
+                                     "traffic": load_traffic("qkv_decode_c3_traffic")}
+        log(f"[bench] config 3 decode: {dms * 1e3:.2f} us/step, {dl * 1e3:.2f} us/launch, {dgbs:.0f} GB/s")
         # config 4: 30B-A3B attention shapes, S=8192
         h4, q4, kv4 = 2048, 32, 4
         n4 = (q4 + 2 * kv4) * D
-        ms4, _ = bench_prefill(8192, 1, 8192, h4, q4, kv4, 3, 30, 5, dev)
-        a4 = flops(8192, h4, n4) / (ms4 * 1e-3) / 1e12
+        ms4, _, l4 = bench_prefill(8192, 1, 8192, h4, q4, kv4, 3, 30, 5, dev)
+        a4 = flops(8192, h4, n4) / (l4 * 1e-3) / 1e12
         sec["config4_30b_a3b_s8192"] = {"tokens_per_s": round(8192 / (ms4 * 1e-3), 1),
-                                        "ms_per_step": round(ms4, 6), "bound": "mfma",
-                                        "achieved_TFLOPs": round(a4, 2),
+                                        "ms_per_step": round(ms4, 6), "ms_per_launch": round(l4, 6),
+                                        "bound": "mfma", "achieved_TFLOPs": round(a4, 2),
                                         "frac": round(a4 / PEAK_BF16_TFLOPS, 4)}
-        log(f"[bench] config 4: {ms4 * 1e3:.1f} us, {a4:.0f} TFLOP/s")
+        log(f"[bench] config 4: {ms4 * 1e3:.1f} us/step, {a4:.0f} TFLOP/s")
         # config 5: W4A16 ragged continuous batch
-        ms5, T5 = bench_w4a16(hidden, Hq, Hkv, 4, 30, 5, dev)
-        a5 = flops(T5, hidden, N) / (ms5 * 1e-3) / 1e12
+        ms5, l5, T5 = bench_w4a16(hidden, Hq, Hkv, 4, 30, 5, dev)
+        a5 = flops(T5, hidden, N) / (l5 * 1e-3) / 1e12
         sec["config5_w4a16_ragged"] = {"tokens": T5, "tokens_per_s": round(T5 / (ms5 * 1e-3), 1),
-                                       "ms_per_step": round(ms5, 6), "bound": "mfma",
-                                       "achieved_TFLOPs": round(a5, 2),
+                                       "ms_per_step": round(ms5, 6), "ms_per_launch": round(l5, 6),
+                                       "bound": "mfma", "achieved_TFLOPs": round(a5, 2),
                                        "frac": round(a5 / PEAK_BF16_TFLOPS, 4)}
-        log(f"[bench] config 5 W4A16 T={T5}: {ms5 * 1e3:.1f} us, {a5:.0f} TFLOP/s")
+        log(f"[bench] config 5 W4A16 T={T5}: {ms5 * 1e3:.1f} us/step, {a5:.0f} TFLOP/s")
         result["secondary"] = sec
 
     if not args.no_cpu:
