@@ -66,32 +66,26 @@ def make_inputs(T, hidden, Hq, Hkv, rows, seed, dev, copies=1):
 
 
 def time_steps(fn, steps, warmup):
-    """(ms per step, wall seconds, ms per launch) for `steps` calls after `warmup` untimed ones.
-
-    Step time: one HIP event pair around all `steps` calls.  Launch time: an
-    event pair around every call, averaged -- the duration of the op's kernel
-    alone, used for the roofline.  All events are recorded on the current
-    stream, the one the mqk ops launch on.
+    """(ms per step, wall seconds) for `steps` back-to-back calls after `warmup`
+    untimed ones, timed with one HIP event pair on the current stream (the one
+    the mqk ops launch on).  Each step is one kernel launch, so the step time is
+    also the kernel's average launch duration (per-launch event pairs were
+    measured to add ~2 us to a 20 us kernel and are not used).
     """
     import torch
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record()
     for i in range(steps):
-        ev[i][0].record()
         fn(i)
-        ev[i][1].record()
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per_launch = sum(a.elapsed_time(b) for a, b in ev) / steps
-    return e0.elapsed_time(e1) / steps, wall, per_launch
+    return e0.elapsed_time(e1) / steps, wall
 
 
 def bench_prefill(S_total, B, S, hidden, Hq, Hkv, seed, steps, warmup, dev):
@@ -141,9 +135,8 @@ def bench_w4a16(hidden, Hq, Hkv, seed, steps, warmup, dev):
     gk = (1 + 0.1 * torch.randn(D, generator=gd, device=dev)).bfloat16()
     cos, sin = (t.to(dev).bfloat16() for t in mqk.rope_tables(D, 8192))
     pos = pos.to(dev)
-    ms, _, launch = time_steps(lambda i: mqk.fused_qkv_rope_w4a16(x, *projs, gq, gk, cos, sin, pos),
-                               steps, warmup)
-    return ms, launch, T
+    ms, _ = time_steps(lambda i: mqk.fused_qkv_rope_w4a16(x, *projs, gq, gk, cos, sin, pos), steps, warmup)
+    return ms, T
 
 
 def cpu_baseline(budget_s=12.0):
@@ -216,18 +209,17 @@ def run_only(name, steps, warmup, dev):
     """One workload alone (for profiler runs); prints one JSON line of timings."""
     B, S, hidden, Hq, Hkv = 4, 512, 4096, 32, 8
     if name == "c2":
-        ms, _, launch = bench_prefill(B * S, B, S, hidden, Hq, Hkv, 1, steps, warmup, dev)
+        ms, _ = bench_prefill(B * S, B, S, hidden, Hq, Hkv, 1, steps, warmup, dev)
     elif name == "c3":
-        ms, _, launch = bench_decode(64, hidden, Hq, Hkv, 2, steps, warmup, dev)
+        ms, _ = bench_decode(64, hidden, Hq, Hkv, 2, steps, warmup, dev)
     elif name == "c4":
-        ms, _, launch = bench_prefill(8192, 1, 8192, 2048, 32, 4, 3, steps, warmup, dev)
+        ms, _ = bench_prefill(8192, 1, 8192, 2048, 32, 4, 3, steps, warmup, dev)
     elif name == "c5":
-        ms, launch, _ = bench_w4a16(hidden, Hq, Hkv, 4, steps, warmup, dev)
+        ms, _ = bench_w4a16(hidden, Hq, Hkv, 4, steps, warmup, dev)
     else:
         copy_kernel(256 << 20, steps, dev)
-        ms = launch = float("nan")
-    print(json.dumps({"workload": name, "steps": steps, "ms_per_step": ms, "ms_per_launch": launch}),
-          flush=True)
+        ms = float("nan")
+    print(json.dumps({"workload": name, "steps": steps, "ms_per_step": ms}), flush=True)
 
 
 def main(argv=None) -> int:
@@ -261,10 +253,10 @@ def main(argv=None) -> int:
     T = B * S
     N = (Hq + 2 * Hkv) * D
     log(f"[bench] config 2 prefill T={T} hidden={hidden} N={N}: {args.warmup} warmup + {args.steps} steps")
-    ms, wall, launch = bench_prefill(T, B, S, hidden, Hq, Hkv, 1, args.steps, args.warmup, dev)
+    ms, wall = bench_prefill(T, B, S, hidden, Hq, Hkv, 1, args.steps, args.warmup, dev)
     fl = flops(T, hidden, N)
-    achieved = fl / (launch * 1e-3) / 1e12
-    log(f"[bench] config 2: {ms * 1e3:.1f} us/step, {launch * 1e3:.1f} us/launch, {achieved:.0f} TFLOP/s")
+    achieved = fl / (ms * 1e-3) / 1e12
+    log(f"[bench] config 2: {ms * 1e3:.1f} us per launch, {achieved:.0f} TFLOP/s")
     result = {
         "metric": "fused QKV+QKNorm+RoPE tokens/s and % roofline (Qwen3-8B shapes, bf16, 1 GPU)",
         "value": round(T / (ms * 1e-3), 1),
@@ -284,37 +276,34 @@ def main(argv=None) -> int:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": load_traffic("qkv_tile_dma_c2_traffic"),
-                     "ms_per_launch": round(launch, 6), "flop_per_launch": fl},
+                     "flop_per_launch": fl},
         "wall_s_timed": round(wall, 4),
     }
 
     if not args.no_secondary:
         sec = {}
         # config 3: decode B=64, weight-read bound
-        dms, _, dl = bench_decode(64, hidden, Hq, Hkv, 2, max(50, args.steps), 10, dev)
-        dgbs = decode_bytes(64, hidden, N) / (dl * 1e-3) / 1e9
+        dms, _ = bench_decode(64, hidden, Hq, Hkv, 2, max(50, args.steps), 10, dev)
+        dgbs = decode_bytes(64, hidden, N) / (dms * 1e-3) / 1e9
         sec["config3_decode_b64"] = {"tokens_per_s": round(64 / (dms * 1e-3), 1),
-                                     "ms_per_step": round(dms, 6), "ms_per_launch": round(dl, 6),
-                                     "bound": "hbm", "achieved_GBps": round(dgbs, 1),
+                                     "ms_per_step": round(dms, 6), "bound": "hbm", "achieved_GBps": round(dgbs, 1),
                                      "frac": round(dgbs / PEAK_HBM_GBS, 4),
                                      "traffic": load_traffic("qkv_decode_c3_traffic")}
-        log(f"[bench] config 3 decode: {dms * 1e3:.2f} us/step, {dl * 1e3:.2f} us/launch, {dgbs:.0f} GB/s")
+        log(f"[bench] config 3 decode: {dms * 1e3:.2f} us per launch, {dgbs:.0f} GB/s")
         # config 4: 30B-A3B attention shapes, S=8192
         h4, q4, kv4 = 2048, 32, 4
         n4 = (q4 + 2 * kv4) * D
-        ms4, _, l4 = bench_prefill(8192, 1, 8192, h4, q4, kv4, 3, 30, 5, dev)
-        a4 = flops(8192, h4, n4) / (l4 * 1e-3) / 1e12
+        ms4, _ = bench_prefill(8192, 1, 8192, h4, q4, kv4, 3, 30, 5, dev)
+        a4 = flops(8192, h4, n4) / (ms4 * 1e-3) / 1e12
         sec["config4_30b_a3b_s8192"] = {"tokens_per_s": round(8192 / (ms4 * 1e-3), 1),
-                                        "ms_per_step": round(ms4, 6), "ms_per_launch": round(l4, 6),
-                                        "bound": "mfma", "achieved_TFLOPs": round(a4, 2),
+                                        "ms_per_step": round(ms4, 6), "bound": "mfma", "achieved_TFLOPs": round(a4, 2),
                                         "frac": round(a4 / PEAK_BF16_TFLOPS, 4)}
         log(f"[bench] config 4: {ms4 * 1e3:.1f} us/step, {a4:.0f} TFLOP/s")
         # config 5: W4A16 ragged continuous batch
-        ms5, l5, T5 = bench_w4a16(hidden, Hq, Hkv, 4, 30, 5, dev)
-        a5 = flops(T5, hidden, N) / (l5 * 1e-3) / 1e12
+        ms5, T5 = bench_w4a16(hidden, Hq, Hkv, 4, 30, 5, dev)
+        a5 = flops(T5, hidden, N) / (ms5 * 1e-3) / 1e12
         sec["config5_w4a16_ragged"] = {"tokens": T5, "tokens_per_s": round(T5 / (ms5 * 1e-3), 1),
-                                       "ms_per_step": round(ms5, 6), "ms_per_launch": round(l5, 6),
-                                       "bound": "mfma", "achieved_TFLOPs": round(a5, 2),
+                                       "ms_per_step": round(ms5, 6), "bound": "mfma", "achieved_TFLOPs": round(a5, 2),
                                        "frac": round(a5 / PEAK_BF16_TFLOPS, 4)}
         log(f"[bench] config 5 W4A16 T={T5}: {ms5 * 1e3:.1f} us/step, {a5:.0f} TFLOP/s")
         result["secondary"] = sec

@@ -99,4 +99,103 @@ __device__ __forceinline__ int xcd_tile_id(int bid, int nblocks) {
   return (bid & 7) * (nblocks >> 3) + (bid >> 3);
 }
 
+// ---------------------------------------------------------------------------
+// Direct L2 -> LDS loads and explicit waits (inline asm; see the kernels that use them)
+// ---------------------------------------------------------------------------
+
+// L2 -> LDS: this lane's 16 bytes at gptr go to LDS byte lds_base + 16 * lane
+// (lds_base wave-uniform).  M0 carries the LDS base; it is saved and restored
+// around the load because the compiler reserves it.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(gptr)
+      : "memory");
+}
+
+// Wait until at most n of this wave's vector-memory operations are pending.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// wait_vm with a count known only after unrolling (folds to one s_waitcnt when
+// n is a constant; counts above 62 wait for nothing older than 63 operations).
+__device__ __forceinline__ void wait_vm_n(int n) {
+  switch (n) {
+    case 0: wait_vm<0>(); break;
+    case 1: wait_vm<1>(); break;
+    case 2: wait_vm<2>(); break;
+    case 3: wait_vm<3>(); break;
+    case 4: wait_vm<4>(); break;
+    case 5: wait_vm<5>(); break;
+    case 6: wait_vm<6>(); break;
+    case 7: wait_vm<7>(); break;
+    case 8: wait_vm<8>(); break;
+    case 9: wait_vm<9>(); break;
+    case 10: wait_vm<10>(); break;
+    case 11: wait_vm<11>(); break;
+    case 12: wait_vm<12>(); break;
+    case 13: wait_vm<13>(); break;
+    case 14: wait_vm<14>(); break;
+    case 15: wait_vm<15>(); break;
+    case 16: wait_vm<16>(); break;
+    case 17: wait_vm<17>(); break;
+    case 18: wait_vm<18>(); break;
+    case 19: wait_vm<19>(); break;
+    case 20: wait_vm<20>(); break;
+    case 21: wait_vm<21>(); break;
+    case 22: wait_vm<22>(); break;
+    case 23: wait_vm<23>(); break;
+    case 24: wait_vm<24>(); break;
+    case 25: wait_vm<25>(); break;
+    case 26: wait_vm<26>(); break;
+    case 27: wait_vm<27>(); break;
+    case 28: wait_vm<28>(); break;
+    case 29: wait_vm<29>(); break;
+    case 30: wait_vm<30>(); break;
+    case 31: wait_vm<31>(); break;
+    case 32: wait_vm<32>(); break;
+    case 33: wait_vm<33>(); break;
+    case 34: wait_vm<34>(); break;
+    case 35: wait_vm<35>(); break;
+    case 36: wait_vm<36>(); break;
+    case 37: wait_vm<37>(); break;
+    case 38: wait_vm<38>(); break;
+    case 39: wait_vm<39>(); break;
+    case 40: wait_vm<40>(); break;
+    case 41: wait_vm<41>(); break;
+    case 42: wait_vm<42>(); break;
+    case 43: wait_vm<43>(); break;
+    case 44: wait_vm<44>(); break;
+    case 45: wait_vm<45>(); break;
+    case 46: wait_vm<46>(); break;
+    case 47: wait_vm<47>(); break;
+    case 48: wait_vm<48>(); break;
+    case 49: wait_vm<49>(); break;
+    case 50: wait_vm<50>(); break;
+    case 51: wait_vm<51>(); break;
+    case 52: wait_vm<52>(); break;
+    case 53: wait_vm<53>(); break;
+    case 54: wait_vm<54>(); break;
+    case 55: wait_vm<55>(); break;
+    case 56: wait_vm<56>(); break;
+    case 57: wait_vm<57>(); break;
+    case 58: wait_vm<58>(); break;
+    case 59: wait_vm<59>(); break;
+    case 60: wait_vm<60>(); break;
+    case 61: wait_vm<61>(); break;
+    case 62: wait_vm<62>(); break;
+    default: wait_vm<63>(); break;
+  }
+}
+
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 }  // namespace mqk

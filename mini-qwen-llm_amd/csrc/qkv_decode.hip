@@ -13,14 +13,15 @@
 //     k-ranges, and the grid maps all splits of head h to XCD h % 8
 //     (workgroup b runs on XCD b % 8), so every XCD gets the same number of
 //     workgroups, at most one per CU;
-//   * inside a workgroup, wave (cg, kq) owns columns [64cg, 64cg+64) of the
-//     head and a quarter of the split's k-range, for all 64 token rows
-//     (v_mfma_f32_16x16x32_bf16, 4 x 4 blocks, so each activation fragment read
-//     from LDS feeds 4 MFMAs).  Its weight slice is loaded HBM -> VGPR before
-//     the first MFMA; the activation slice is staged once in LDS with direct
-//     global->LDS loads.  The four k-quarters are added through LDS.
+//   * inside a workgroup, wave w owns columns [16w, 16w+16) of the head over
+//     the split's whole k-range, for all 64 token rows (v_mfma_f32_16x16x32_bf16,
+//     4 row blocks, so each weight fragment feeds 4 MFMAs and no reduction
+//     between waves is needed).  The activation slice is staged once in LDS
+//     with direct L2 -> LDS loads; the wave's weight slice streams HBM -> VGPR,
+//     all of it issued up front, and each 64-wide k tile is multiplied as soon
+//     as its fragments land.
 // Combining the splits: each workgroup writes its fp32 partial tile [64 x 128]
-// with plain stores, which stay in (or are written back from) the L2 of its
+// (in MFMA fragment order, 16-byte stores) with plain stores, which stay in (or are written back from) the L2 of its
 // XCD, and bumps the head's arrival counter; the workgroup that arrives last
 // reads the other partials with plain loads -- all of them were written
 // through the same L2 -- adds them in split order, applies RMSNorm over the
@@ -42,7 +43,9 @@ namespace mqk {
 #ifdef MQK_DECODE_TRACE
 // Diagnostic build only: per-workgroup phase timestamps (100 MHz s_memrealtime)
 // written to a device buffer set with mqk_set_option("decode_trace", ptr).
-__device__ int64_t* g_decode_trace = nullptr;
+// (a __constant__ pointer: read with a scalar load, so a trace point never waits
+// for the kernel's outstanding vector loads)
+__constant__ int64_t* g_decode_trace = nullptr;
 void set_decode_trace(void* ptr) {
   (void)hipMemcpyToSymbol(HIP_SYMBOL(g_decode_trace), &ptr, sizeof(ptr));
 }
@@ -56,24 +59,32 @@ void set_decode_trace(void* ptr) {
 namespace {
 
 constexpr int kDecRows = 64;            // token rows per call (T <= 64)
-constexpr int kDecThreads = 512;        // 8 waves: 2 column halves x 4 k-quarters
+constexpr int kDecThreads = 512;        // 8 waves; wave w owns columns [16w, 16w+16) of the head
+constexpr int kDecWaves = kDecThreads / 64;
 constexpr int kDecMaxNK = 16;           // largest k-range of one split, in 64-wide tiles
-constexpr int kDecQuarterNK = kDecMaxNK / 4;
+#ifndef MQK_DEC_LOOK
+#define MQK_DEC_LOOK 6
+#endif
+constexpr int kDecLookahead = MQK_DEC_LOOK;  // weight tiles in flight per wave
 constexpr int kDecKc = kDecMaxNK * kBK;     // LDS row length of the x slice (bf16), 2 KB
 constexpr int kMaxHeads = 1024;
 constexpr int kCounterBytes = kMaxHeads * 4;
 constexpr int kTileFloats = kDecRows * kHeadDim;
-constexpr int kPitch = kHeadDim;        // LDS pitch (floats) of a partial tile
+constexpr int kPitch = kHeadDim + 4;    // fp32 pitch of the finisher's LDS head tile
 constexpr int kXcds = 8;                // MI355X: 8 XCDs, workgroup b dispatched to XCD b % 8
 constexpr uint32_t kForeignUnit = 1u << 16;  // arrival-counter increment of a misplaced split
 
 static_assert(kDecRows * kDecKc * 2 > 160 * 1024 / 2, "x slice must keep one workgroup per CU");
-static_assert(4 * kDecRows * kPitch * 4 <= kDecRows * kDecKc * 2, "4 partial tiles alias the x slice");
+static_assert(kDecRows * 8 == kDecThreads, "one 16-byte x chunk per thread per k tile");
+static_assert(kDecRows * kPitch * 4 <= kDecRows * kDecKc * 2, "the head tile aliases the x slice");
+static_assert(kDecWaves * 16 == kHeadDim, "one 16-column group per wave");
 
-__device__ __forceinline__ int dec_lds_off(int row, int chunk) {
-  // row stride kDecKc bf16 (2 KB); 16-byte chunk index XOR-swizzled in its low
-  // 4 bits so the 16 rows read by one quarter-wave hit 16 different bank groups
-  return row * kDecKc + ((chunk ^ (row & 15)) << 3);
+// x slice layout in LDS: tile-major, [k tile t][row 0..63][8 chunks of 16 B]
+// (8 KB per 64-wide k tile); chunk c of row r is stored in slot c ^ ((r >> 1) & 7),
+// so the 16 rows one quarter-wave reads (8 even rows in one half of the banks, 8
+// odd rows in the other) hit 16 different bank groups.
+__device__ __forceinline__ int dec_lds_off(int t, int row, int chunk) {
+  return t * (kDecRows * 64) + row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3);  // in bf16 elements
 }
 
 __device__ __forceinline__ int xcc_id() {
@@ -86,152 +97,224 @@ __device__ __forceinline__ void split_range(int s, int S, int nkt, int& kt0, int
   nk = int((int64_t(s + 1) * nkt) / S) - kt0;
 }
 
-// Computes the partial tile of k-tiles [kt0, kt0 + nk) of one head into LDS
-// `tile` (fp32 [64][kPitch], row-major), using `xs` as staging.  All threads of
-// the workgroup call it; it ends with a barrier.
-template <bool INT4>
-__device__ void compute_partial(const ProblemArgs& p, const WeightArgs& w, int proj, int hh, int kt0,
-                                int nk, uint16_t* xs, float* tile) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int cg = wave & 1;            // 64-column half of the head
-  const int kq = wave >> 1;           // k-quarter of the split
-  const int c16 = lane & 15;
-  const int g4 = lane >> 4;
-  const int M = int(p.M);
+// One direct L2 -> LDS load per wave stages k tile t of the x slice: wave w
+// fills rows [8w, 8w+8) (1 KB, contiguous in LDS); lane L takes row 8w + L/8 and
+// LDS slot L % 8, i.e. global chunk (L % 8) ^ ((row >> 1) & 7).  Rows >= M
+// re-read row M-1; those LDS rows only feed output rows that are never stored.
+__device__ __forceinline__ void stage_x_tile(const ProblemArgs& p, int64_t kbeg, int t, uint32_t xs_lds) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row = wave * 8 + (lane >> 3);
+  const int gq = (lane & 7) ^ ((row >> 1) & 7);
+  const int grow = row < int(p.M) ? row : int(p.M) - 1;
+  dma16(p.x + int64_t(grow) * p.K + kbeg + t * kBK + gq * 8,
+        xs_lds + uint32_t(t * kDecRows * 128 + wave * 1024));
+}
+
+// 16x16x32 operand layout: lane (c, g) = (lane & 15, lane >> 4) holds column c
+// of the wave's 16 (B) / row c of a 16-row block (A) and 8 k values; inside a
+// 64-wide k tile, block kk (0, 1) of 32 and lane group g give k = kk*32 + g*8.
+// acc[mb][j] = C[mb*16 + 4g + j][16*wave + c].
+__device__ __forceinline__ void mma_tile(const uint16_t* xs, int t, const u32x4_t (&b)[2], f32x4_t (&acc)[4]) {
+  const int lane = threadIdx.x & 63;
+  const int c16 = lane & 15, g4 = lane >> 4;
+  u32x4_t a[2][4];  // all 8 activation fragments of the tile in flight before the first MFMA
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+      a[kk][mb] = *reinterpret_cast<const u32x4_t*>(xs + dec_lds_off(t, mb * 16 + c16, kk * 4 + g4));
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) acc[mb] = mfma_16x16x32(a[kk][mb], b[kk], acc[mb]);
+}
+
+// 8 consecutive bf16 (16 bytes; one vector load when 16-byte aligned).
+__device__ __forceinline__ u32x4_t load8_bf16(const uint16_t* ptr, bool vec) {
+  if (vec) return *reinterpret_cast<const u32x4_t*>(ptr);
+  u32x4_t v;
+  v.x = uint32_t(ptr[0]) | (uint32_t(ptr[1]) << 16);
+  v.y = uint32_t(ptr[2]) | (uint32_t(ptr[3]) << 16);
+  v.z = uint32_t(ptr[4]) | (uint32_t(ptr[5]) << 16);
+  v.w = uint32_t(ptr[6]) | (uint32_t(ptr[7]) << 16);
+  return v;
+}
+
+// Element i (0..7) of 8 packed bf16, as float.
+__device__ __forceinline__ float bf16_lane(const u32x4_t& v, int i) {
+  const uint32_t wd = i < 2 ? v.x : (i < 4 ? v.y : (i < 6 ? v.z : v.w));
+  return __uint_as_float((i & 1) ? (wd & 0xFFFF0000u) : (wd << 16));
+}
+
+// Weight fragment load: non-temporal, so the weight stream does not evict the
+// split partials and the x slice from the L2.
+__device__ __forceinline__ u32x4_t wload(const uint16_t* ptr) {
+#ifdef MQK_DEC_TEMPORAL
+  return *reinterpret_cast<const u32x4_t*>(ptr);
+#else
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(ptr));
+#endif
+}
+
+struct Int4Col {  // this lane's column of an int4 projection
+  const int32_t* qw;
+  const uint16_t* sc;
+  const int32_t* qz;
+  int64_t n;      // columns of the projection
+  int64_t col;
+  int group;
+  bool fp16;
+};
+
+__device__ __forceinline__ Int4Col int4_col(const WeightArgs& w, int proj, int64_t col) {
+  return Int4Col{w.qw[proj], static_cast<const uint16_t*>(w.sc[proj]), w.qz[proj], w.n_cols[proj], col,
+                 w.group, w.scale_fp16 != 0};
+}
+
+__device__ __forceinline__ void dequant_tile(const Int4Col& ic, const uint32_t (&q)[2], uint32_t sraw, uint32_t zw,
+                                             u32x4_t (&b)[2]) {
+  const float scale = ic.fp16 ? f16_to_f32(sraw) : bf16_to_f32(sraw);
+  const float zero = float((zw >> ((ic.col % 8) * 4)) & 0xFu);
+  b[0] = dequant_int4x8(q[0], zero, scale);
+  b[1] = dequant_int4x8(q[1], zero, scale);
+}
+
+// The split partial of one wave over k tiles [kt0, kt0 + NK).
+// bf16: per tile, the wave issues the x tile's direct load, then its two weight
+// fragments (HBM -> VGPR, non-temporal so the weight stream does not evict the
+// split partials from the L2).  Tile t is multiplied once the x tile has landed
+// in every wave (own wait: the 3*(NK-1-t)+2 later loads may still be pending;
+// then a barrier) and its weight fragments have arrived (the compiler's per-use
+// waits), so the MFMAs run under the rest of the stream.
+template <bool INT4, int NK>
+__device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const WeightArgs& w, int proj, int hh,
+                                              int kt0, const uint16_t* xs, uint32_t xs_lds, f32x4_t (&acc)[4]) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c16 = lane & 15, g4 = lane >> 4;
   const int64_t kbeg = int64_t(kt0) * kBK;
-  // k-quarter kq covers tiles [kq*nk/4, (kq+1)*nk/4) of the split
-  const int my_t0 = (kq * nk) >> 2;
-  const int my_nt = (((kq + 1) * nk) >> 2) - my_t0;
-
-  // 1. activation slice x[0:M, kbeg : kbeg + nk*64] -> LDS with direct
-  // global->LDS loads (no VGPR staging).  One wave instruction fills half an
-  // LDS row (64 chunks of 16 B); lane L writes LDS chunk slot half*64 + L, which
-  // holds global chunk slot ^ (row & 15) (the swizzle of dec_lds_off).
-  constexpr int kWaves = kDecThreads / 64;
+  const int64_t col = int64_t(hh) * kHeadDim + wave * 16 + c16;
 #pragma unroll
-  for (int i = 0; i < 2 * kDecRows / kWaves; ++i) {
-    const int u = wave + kWaves * i;      // (row, half) unit, wave-uniform
-    const int row = u >> 1, half = u & 1;
-    const int gq = (half * 64 + lane) ^ (row & 15);
-    if (row < M && gq < nk * 8)
-      __builtin_amdgcn_global_load_lds(p.x + int64_t(row) * p.K + kbeg + gq * 8,
-                                       xs + row * kDecKc + half * 64 * 8, 16, 0, 0);
-  }
-
-  // 2. this wave's weight slice, straight to registers.  16x16x32 operand
-  // layout: lane (c, g) holds column c (B) / row c (A) and 8 k values; k order
-  // inside a 64-wide tile: block kk (0,1) of 32, lane group g -> kk*32 + g*8.
-  const int64_t col0 = int64_t(hh) * kHeadDim + cg * 64 + c16;  // column (nb = 0) inside the projection
-  const int64_t qstride = w.n_cols[proj];
-  u32x4_t wb[INT4 ? 1 : kDecQuarterNK][4][2];
-  uint32_t wq[INT4 ? kDecQuarterNK : 1][4][2];
+  for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4_t{};
+  if constexpr (!INT4) {
+    // The x slice (L2-resident) is requested first, then the first kLook weight
+    // tiles; each later tile is requested one tile before the MFMAs that free
+    // the lookahead slot, so about kLook tiles (16 KB per tile per CU) stay in
+    // flight and early tiles land early instead of the whole stream landing at
+    // once.
+    constexpr int kLook = NK < kDecLookahead ? NK : kDecLookahead;
+    const uint16_t* wp = w.w[proj] + col * p.K + kbeg + g4 * 8;
+    u32x4_t b[NK][2];
 #pragma unroll
-  for (int t = 0; t < kDecQuarterNK; ++t) {
-    if (t < my_nt) {
-      const int64_t k0 = kbeg + int64_t(my_t0 + t) * kBK;
+    for (int t = 0; t < NK; ++t) stage_x_tile(p, kbeg, t, xs_lds);
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
+    for (int t = 0; t < kLook; ++t)
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const int64_t col = col0 + nb * 16;
-          if constexpr (!INT4)
-            wb[t][nb][kk] = *reinterpret_cast<const u32x4_t*>(w.w[proj] + col * p.K + k0 + kk * 32 + g4 * 8);
-          else
-            wq[t][nb][kk] = uint32_t(w.qw[proj][(k0 / 8 + kk * 4 + g4) * qstride + col]);
-        }
-    }
-  }
-
-  // 3. wait for every load (the x slice must be in LDS before the barrier; the
-  // compiler drains all loads before a barrier that follows LDS-DMA loads anyway)
-  __builtin_amdgcn_s_waitcnt(0);
-  DECODE_TRACE(1)
-  __syncthreads();
-  DECODE_TRACE(5)
-
-  // 4. MFMAs.  Rows >= M of xs hold stale data; output row r depends only on
-  // row r of x and rows >= M are never stored.
-  f32x4_t acc[4][4];
+      for (int kk = 0; kk < 2; ++kk)
+        b[t][kk] = wload(wp + t * kBK + kk * 32);
+    wait_vm<2 * kLook>();  // the x slice has landed (older than the weight loads) ...
+    barrier();             // ... in every wave
+    DECODE_TRACE(5)
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+    for (int t = 0; t < NK; ++t) {
+      if (t + kLook < NK) {
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x4_t{};
-#pragma unroll
-  for (int t = 0; t < kDecQuarterNK; ++t) {
-    if (t < my_nt) {
-      u32x4_t b[4][2];
-      if constexpr (!INT4) {
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          b[nb][0] = wb[t][nb][0];
-          b[nb][1] = wb[t][nb][1];
-        }
-      } else {
-        const int64_t k0 = kbeg + int64_t(my_t0 + t) * kBK;
-        const int grp = int(k0 / w.group);
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          const int64_t col = col0 + nb * 16;
-          const uint32_t sraw = static_cast<const uint16_t*>(w.sc[proj])[grp * qstride + col];
-          const float scale = w.scale_fp16 ? f16_to_f32(sraw) : bf16_to_f32(sraw);
-          const uint32_t zw = uint32_t(w.qz[proj][grp * (qstride / 8) + col / 8]);
-          const float zero = float((zw >> ((col % 8) * 4)) & 0xFu);
-          b[nb][0] = dequant_int4x8(wq[t][nb][0], zero, scale);
-          b[nb][1] = dequant_int4x8(wq[t][nb][1], zero, scale);
-        }
+        for (int kk = 0; kk < 2; ++kk)
+          b[t + kLook][kk] =
+              wload(wp + (t + kLook) * kBK + kk * 32);
       }
+      mma_tile(xs, t, b[t], acc);
+    }
+  } else {
+    // int4 weights are 4x smaller: load them with their scales and zeros, then
+    // the x slice, and wait for everything
+    const Int4Col ic = int4_col(w, proj, col);
+    uint32_t q[NK][2], sraw[NK], zw[NK];
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const int chunk = (my_t0 + t) * 8 + kk * 4 + g4;
+    for (int t = 0; t < NK; ++t) {
+      const int64_t k0 = kbeg + int64_t(t) * kBK;
+      const int64_t grp = k0 / ic.group;
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xs + dec_lds_off(mb * 16 + c16, chunk));
+      for (int kk = 0; kk < 2; ++kk) q[t][kk] = uint32_t(ic.qw[(k0 / 8 + kk * 4 + g4) * ic.n + col]);
+      sraw[t] = ic.sc[grp * ic.n + col];
+      zw[t] = uint32_t(ic.qz[grp * (ic.n / 8) + col / 8]);
+    }
 #pragma unroll
-          for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mfma_16x16x32(a, b[nb][kk], acc[mb][nb]);
-        }
-      }
+    for (int t = 0; t < NK; ++t) stage_x_tile(p, kbeg, t, xs_lds);
+    wait_vm<0>();
+    barrier();
+#pragma unroll
+    for (int t = 0; t < NK; ++t) {
+      u32x4_t b[2];
+      dequant_tile(ic, q[t], sraw[t], zw[t], b);
+      mma_tile(xs, t, b, acc);
     }
   }
-  __syncthreads();  // xs no longer read; the quarter tiles alias it
-  DECODE_TRACE(6)
+}
 
-  // 5. add the four k-quarters: wave (cg, kq) writes its block into quarter tile
-  // kq, then every thread sums one 16-column strip of one row into tile 0.
-  // acc[mb][nb][j] = C[mb*16 + 4g + j][cg*64 + nb*16 + c].
-  float* qt = tile + kq * (kDecRows * kPitch);
+// The same partial with a run-time k-range and one tile's loads at a time: the
+// arithmetic (per-tile dequant, MFMA order) is identical to partial_fixed, so
+// its result is bit-identical.  Used by the recompute path only.
+template <bool INT4>
+__device__ void partial_any(const ProblemArgs& p, const WeightArgs& w, int proj, int hh, int kt0, int nk,
+                            const uint16_t* xs, uint32_t xs_lds, f32x4_t (&acc)[4]) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c16 = lane & 15, g4 = lane >> 4;
+  const int64_t kbeg = int64_t(kt0) * kBK;
+  const int64_t col = int64_t(hh) * kHeadDim + wave * 16 + c16;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        qt[(mb * 16 + g4 * 4 + j) * kPitch + cg * 64 + nb * 16 + c16] = acc[mb][nb][j];
-  __syncthreads();
-  {
-    const int r = tid >> 3, c0 = (tid & 7) * 16;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      f32x4_t sum = *reinterpret_cast<const f32x4_t*>(tile + r * kPitch + c0 + 4 * v);
-#pragma unroll
-      for (int k = 1; k < 4; ++k)
-        sum += *reinterpret_cast<const f32x4_t*>(tile + k * (kDecRows * kPitch) + r * kPitch + c0 + 4 * v);
-      *reinterpret_cast<f32x4_t*>(tile + r * kPitch + c0 + 4 * v) = sum;
+  for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4_t{};
+  for (int t = 0; t < nk; ++t) stage_x_tile(p, kbeg, t, xs_lds);
+  wait_vm<0>();
+  barrier();
+  for (int t = 0; t < nk; ++t) {
+    const int64_t k0 = kbeg + int64_t(t) * kBK;
+    u32x4_t b[2];
+    if constexpr (!INT4) {
+      const uint16_t* wp = w.w[proj] + col * p.K + k0 + g4 * 8;
+      b[0] = *reinterpret_cast<const u32x4_t*>(wp);
+      b[1] = *reinterpret_cast<const u32x4_t*>(wp + 32);
+    } else {
+      const Int4Col ic = int4_col(w, proj, col);
+      const int64_t grp = k0 / ic.group;
+      const uint32_t q[2] = {uint32_t(ic.qw[(k0 / 8 + g4) * ic.n + col]),
+                             uint32_t(ic.qw[(k0 / 8 + 4 + g4) * ic.n + col])};
+      dequant_tile(ic, q, ic.sc[grp * ic.n + col], uint32_t(ic.qz[grp * (ic.n / 8) + col / 8]), b);
     }
+    mma_tile(xs, t, b, acc);
   }
-  __syncthreads();
+}
+
+template <bool INT4>
+__device__ __forceinline__ void partial_dispatch(const ProblemArgs& p, const WeightArgs& w, int proj, int hh,
+                                                 int kt0, int nk, const uint16_t* xs, uint32_t xs_lds,
+                                                 f32x4_t (&acc)[4]) {
+  switch (nk) {
+#define MQK_DEC_CASE(n) \
+  case n: partial_fixed<INT4, n>(p, w, proj, hh, kt0, xs, xs_lds, acc); break;
+    MQK_DEC_CASE(1) MQK_DEC_CASE(2) MQK_DEC_CASE(3) MQK_DEC_CASE(4)
+    MQK_DEC_CASE(5) MQK_DEC_CASE(6) MQK_DEC_CASE(7) MQK_DEC_CASE(8)
+    MQK_DEC_CASE(9) MQK_DEC_CASE(10) MQK_DEC_CASE(11) MQK_DEC_CASE(12)
+    MQK_DEC_CASE(13) MQK_DEC_CASE(14) MQK_DEC_CASE(15) MQK_DEC_CASE(16)
+#undef MQK_DEC_CASE
+    default: break;  // the launcher guarantees 1 <= nk <= kDecMaxNK
+  }
 }
 
 template <bool INT4>
 __global__ void __launch_bounds__(kDecThreads, 1)
 decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __restrict__ part,
-              uint32_t* __restrict__ counters, int force_recompute) {
+              uint32_t* __restrict__ counters, int force_recompute, bool vec_epi) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[kDecRows * kDecKc];
   __shared__ uint32_t arrival;
-  float* tile = reinterpret_cast<float*>(xs);  // partial tile aliases the x staging area
+  const uint32_t xs_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(xs));
+  float* tile = reinterpret_cast<float*>(xs);  // the finisher's head tile aliases the x slice
 
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int n_tiles = p.n_tiles;
   const int bid = blockIdx.x;
   const int q = bid / kXcds;
@@ -246,19 +329,14 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
 
   int kt0, nk;
   split_range(split, splits, nkt, kt0, nk);
-  compute_partial<INT4>(p, w, proj, hh, kt0, nk, xs, tile);
+  f32x4_t acc[4];
+  partial_dispatch<INT4>(p, w, proj, hh, kt0, nk, xs, xs_lds, acc);
+  DECODE_TRACE(1)
 
-  DECODE_TRACE(2)
-  // ---- publish the partial: part[split][head] = [64][128] fp32 row-major -------
-  {
-    const int r = tid >> 3, c0 = (tid & 7) * 16;  // row, 16 consecutive columns
-    if (r < M) {
-      float* dst = part + (int64_t(split) * n_tiles + head) * kTileFloats + r * kHeadDim + c0;
+  // ---- publish the partial in fragment order: part[split][head][wave][mb][lane] ----
+  f32x4_t* mine = reinterpret_cast<f32x4_t*>(part) + ((int64_t(split) * n_tiles + head) * kDecWaves + wave) * 4 * 64 + lane;
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        *reinterpret_cast<f32x4_t*>(dst + 4 * v) = *reinterpret_cast<const f32x4_t*>(tile + r * kPitch + c0 + 4 * v);
-    }
-  }
+  for (int mb = 0; mb < 4; ++mb) mine[mb * 64] = acc[mb];
   __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have reached the L2
   __syncthreads();                // ... and every thread's
   if (tid == 0) {
@@ -267,52 +345,74 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
     arrival = __hip_atomic_fetch_add(counters + head, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
   }
   __syncthreads();
-  DECODE_TRACE(3)
+  DECODE_TRACE(2)
   const uint32_t seen = arrival;
   if ((seen & (kForeignUnit - 1)) != uint32_t(splits)) return;  // not the last split to arrive
   const bool recompute = (seen >> 16) != 0;
 
-  // ---- last arrival: sum the partials in split order -------------------------------
-  // thread -> row r = tid / 8, c = tid % 8: columns [8c, 8c+8) and
-  // [64+8c, 64+8c+8), so every RoPE pair (d, d+64) is thread-local.
+  // thread -> row r = tid / 8, c = tid % 8 of the head tile: columns [8c, 8c+8)
+  // and [64+8c, 64+8c+8), so every RoPE pair (d, d+64) is thread-local.  Its
+  // gamma / cos / sin operands are loaded now, under the partial reads.
   const int r = tid >> 3;
   const int c = tid & 7;
-  float lo[8], hi[8];
+  u32x4_t g_lo{}, g_hi{}, c_lo{}, c_hi{}, s_lo{}, s_hi{};
+  if (proj != 2 && r < M) {
+    const uint16_t* gamma = proj == 0 ? e.q_gamma : e.k_gamma;
+    const int64_t prow = rope_row(e.positions, r, e.S, e.cos_rows) * kHeadDim;
+    g_lo = load8_bf16(gamma + 8 * c, vec_epi);
+    g_hi = load8_bf16(gamma + kHalfDim + 8 * c, vec_epi);
+    c_lo = load8_bf16(e.cos + prow + 8 * c, vec_epi);
+    c_hi = load8_bf16(e.cos + prow + kHalfDim + 8 * c, vec_epi);
+    s_lo = load8_bf16(e.sin + prow + 8 * c, vec_epi);
+    s_hi = load8_bf16(e.sin + prow + kHalfDim + 8 * c, vec_epi);
+  }
+
+  // ---- last arrival: sum the partials in split order ---------------------------------
+  f32x4_t sum[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) lo[i] = hi[i] = 0.f;
-  auto add8 = [&](const float* src) {
-    const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(src + 8 * c);
-    const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(src + 8 * c + 4);
-    const f32x4_t b0 = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + 8 * c);
-    const f32x4_t b1 = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + 8 * c + 4);
-    lo[0] += a0.x; lo[1] += a0.y; lo[2] += a0.z; lo[3] += a0.w;
-    lo[4] += a1.x; lo[5] += a1.y; lo[6] += a1.z; lo[7] += a1.w;
-    hi[0] += b0.x; hi[1] += b0.y; hi[2] += b0.z; hi[3] += b0.w;
-    hi[4] += b1.x; hi[5] += b1.y; hi[6] += b1.z; hi[7] += b1.w;
-  };
+  for (int mb = 0; mb < 4; ++mb) sum[mb] = f32x4_t{};
   if (!recompute) {
-    if (r < M) {
-      for (int s0 = 0; s0 < splits; s0 += 4) {
-        f32x4_t buf[4][4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int s = s0 + j < splits ? s0 + j : s0;  // padding slots re-read a valid tile
-          const float* src = s == split ? tile + r * kPitch
-                                        : part + (int64_t(s) * n_tiles + head) * kTileFloats + r * kHeadDim;
-          buf[j][0] = *reinterpret_cast<const f32x4_t*>(src + 8 * c);
-          buf[j][1] = *reinterpret_cast<const f32x4_t*>(src + 8 * c + 4);
-          buf[j][2] = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + 8 * c);
-          buf[j][3] = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + 8 * c + 4);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (s0 + j >= splits) break;
-          lo[0] += buf[j][0].x; lo[1] += buf[j][0].y; lo[2] += buf[j][0].z; lo[3] += buf[j][0].w;
-          lo[4] += buf[j][1].x; lo[5] += buf[j][1].y; lo[6] += buf[j][1].z; lo[7] += buf[j][1].w;
-          hi[0] += buf[j][2].x; hi[1] += buf[j][2].y; hi[2] += buf[j][2].z; hi[3] += buf[j][2].w;
-          hi[4] += buf[j][3].x; hi[5] += buf[j][3].y; hi[6] += buf[j][3].z; hi[7] += buf[j][3].w;
-        }
+    // The other splits' fragments of this wave are pulled into LDS with direct
+    // L2 -> LDS loads (a CU fetches faster that way than into VGPRs), up to four
+    // splits per batch in the x slice's space, which no wave reads any more; each
+    // wave reads back only the 4 KB regions it loaded itself, so its own vmcnt
+    // wait is the only synchronisation.  Summation is in split order.
+    const char* frag = reinterpret_cast<const char*>(part) +
+                       ((int64_t(head) * kDecWaves + wave) * 4 * 64) * sizeof(f32x4_t);
+    const int64_t split_stride = int64_t(n_tiles) * kTileFloats * sizeof(float);
+    const uint32_t slot0 = xs_lds + uint32_t(wave * 4096);
+    const char* slot0_ptr = reinterpret_cast<const char*>(xs) + wave * 4096;
+    int s = 0;
+    while (s < splits) {
+      int s_end = s, n_other = 0;
+      while (s_end < splits && (s_end == split || n_other < 4)) {
+        if (s_end != split) ++n_other;
+        ++s_end;
       }
+      int slot = 0;
+      for (int q = s; q < s_end; ++q) {
+        if (q == split) continue;
+        const char* src = frag + q * split_stride + lane * 16;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+          dma16(src + mb * 1024, slot0 + uint32_t(slot * kDecWaves * 4096 + mb * 1024));
+        ++slot;
+      }
+      wait_vm<0>();
+      slot = 0;
+      for (int q = s; q < s_end; ++q) {
+        if (q == split) {
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb) sum[mb] += acc[mb];
+          continue;
+        }
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+          sum[mb] += *reinterpret_cast<const f32x4_t*>(slot0_ptr + slot * kDecWaves * 4096 + mb * 1024 + lane * 16);
+        ++slot;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next batch overwrites
+      s = s_end;
     }
   } else {
     // Some split ran on another XCD: its partial may not be visible through this
@@ -320,10 +420,37 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
     for (int s = 0; s < splits; ++s) {
       int s_kt0, s_nk;
       split_range(s, splits, nkt, s_kt0, s_nk);
-      compute_partial<INT4>(p, w, proj, hh, s_kt0, s_nk, xs, tile);
-      if (r < M) add8(tile + r * kPitch);
-      __syncthreads();  // tile is rewritten by the next split
+      __syncthreads();  // every wave is done with the x slice of the previous split
+      partial_any<INT4>(p, w, proj, hh, s_kt0, s_nk, xs, xs_lds, acc);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) sum[mb] += acc[mb];
     }
+  }
+
+  // ---- head tile to LDS (fp32 [64][kPitch]); the x slice is no longer read ----------
+  DECODE_TRACE(7)
+  __syncthreads();
+  {
+    const int c16 = lane & 15, g4 = lane >> 4;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tile[(mb * 16 + g4 * 4 + j) * kPitch + wave * 16 + c16] = sum[mb][j];
+  }
+  __syncthreads();
+  DECODE_TRACE(3)
+
+  float lo[8], hi[8];
+  {
+    const float* src = tile + r * kPitch;
+    const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(src + 8 * c);
+    const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(src + 8 * c + 4);
+    const f32x4_t b0 = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + 8 * c);
+    const f32x4_t b1 = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + 8 * c + 4);
+    lo[0] = a0.x; lo[1] = a0.y; lo[2] = a0.z; lo[3] = a0.w;
+    lo[4] = a1.x; lo[5] = a1.y; lo[6] = a1.z; lo[7] = a1.w;
+    hi[0] = b0.x; hi[1] = b0.y; hi[2] = b0.z; hi[3] = b0.w;
+    hi[4] = b1.x; hi[5] = b1.y; hi[6] = b1.z; hi[7] = b1.w;
   }
 
   if (proj != 2) {
@@ -334,21 +461,14 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
     ss += __shfl_xor(ss, 2);
     ss += __shfl_xor(ss, 4);
     const float rms = rsqrtf(ss * (1.0f / float(kHeadDim)) + e.eps);
-    if (r < M) {
-      const uint16_t* gamma = proj == 0 ? e.q_gamma : e.k_gamma;
-      const int64_t prow = rope_row(e.positions, r, e.S, e.cos_rows) * kHeadDim;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int d = 8 * c + i;
-        const float x1n = lo[i] * rms * bf16_to_f32(gamma[d]);
-        const float x2n = hi[i] * rms * bf16_to_f32(gamma[d + kHalfDim]);
-        const float c1 = bf16_to_f32(e.cos[prow + d]);
-        const float c2 = bf16_to_f32(e.cos[prow + d + kHalfDim]);
-        const float s1 = bf16_to_f32(e.sin[prow + d]);
-        const float s2 = bf16_to_f32(e.sin[prow + d + kHalfDim]);
-        lo[i] = x1n * c1 - x2n * s1;
-        hi[i] = x2n * c2 + x1n * s2;
-      }
+    for (int i = 0; i < 8; ++i) {
+      const float x1n = lo[i] * rms * bf16_lane(g_lo, i);
+      const float x2n = hi[i] * rms * bf16_lane(g_hi, i);
+      const float t1 = x1n * bf16_lane(c_lo, i) - x2n * bf16_lane(s_lo, i);
+      const float t2 = x2n * bf16_lane(c_hi, i) + x1n * bf16_lane(s_hi, i);
+      lo[i] = t1;
+      hi[i] = t2;
     }
   }
   if (r < M) {
@@ -423,12 +543,14 @@ hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, co
   float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
   const dim3 grid(((p.n_tiles + kXcds - 1) / kXcds) * kXcds * splits);
   const int fr = g_decode_force_recompute;
+  auto a16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; };
+  const bool vec = a16(e.q_gamma) && a16(e.k_gamma) && a16(e.cos) && a16(e.sin);
   if (int4)
     hipLaunchKernelGGL(decode_kernel<true>, grid, dim3(kDecThreads), 0, stream, p, w, e, splits, part, counters,
-                       fr);
+                       fr, vec);
   else
     hipLaunchKernelGGL(decode_kernel<false>, grid, dim3(kDecThreads), 0, stream, p, w, e, splits, part,
-                       counters, fr);
+                       counters, fr, vec);
   return hipGetLastError();
 }
 

@@ -60,30 +60,6 @@ struct DmaShape {
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
 };
 
-// L2 -> LDS: this lane's 16 bytes at gptr go to LDS byte lds_base + 16 * lane
-// (lds_base wave-uniform).  M0 carries the LDS base; it is saved and restored
-// around the load because the compiler reserves it.
-__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "global_load_lds_dwordx4 %2, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(gptr)
-      : "memory");
-}
-
-// Wait until at most n of this wave's vector-memory operations are pending.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
-
 template <int NS, int LPW>
 __device__ __forceinline__ void wait_stage(int remaining_after) {
   // remaining_after = stages issued after the one being waited for (0..NS-2)
