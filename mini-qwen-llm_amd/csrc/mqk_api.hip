@@ -80,11 +80,19 @@ EpilogueArgs make_qkv_epilogue(const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
 
 bool use_decode(int64_t T) { return T >= 1 && T <= g_decode_max_t.load() && T <= 64; }
 
+// The split-K decode kernel and the pipelined tile variants read gamma / cos /
+// sin rows with 16-byte loads.
+bool epilogue_aligned(const EpilogueArgs& e) {
+  return aligned16(e.q_gamma) && aligned16(e.k_gamma) && aligned16(e.cos) && aligned16(e.sin);
+}
+
 // Common launcher of the fused op (bf16 or int4 weights).
 int run_fused(int int4, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
               void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (p.M == 0) return ok();
-  const int splits = use_decode(p.M) ? decode_splits_for(p.M, p.K, p.n_tiles, int(g_decode_splits.load())) : 0;
+  const int splits = use_decode(p.M) && epilogue_aligned(e)
+                         ? decode_splits_for(p.M, p.K, p.n_tiles, int(g_decode_splits.load()))
+                         : 0;
   if (splits > 0) {
     const size_t need = decode_workspace_bytes(p.n_tiles, splits);
     if (!workspace || ws_bytes < need)
@@ -96,7 +104,7 @@ int run_fused(int int4, const ProblemArgs& p, const WeightArgs& w, const Epilogu
   if (!v) return fail(MQK_ERR_BAD_OPTION, "prefill_tile variant %lld cannot run this problem (%d heads%s)",
                       (long long)g_prefill_tile.load(), p.n_tiles, int4 ? ", int4 weights" : "");
   // The pipelined variants read gamma/cos/sin rows with 16-byte loads.
-  if (v->id >= 10 && !(aligned16(e.q_gamma) && aligned16(e.k_gamma) && aligned16(e.cos) && aligned16(e.sin)))
+  if (v->id >= 10 && !epilogue_aligned(e))
     v = choose_tile_variant(p.n_tiles % 2 == 0 ? 4 : 1, p.M, p.n_tiles, int4);
   return hip_status(launch_tile(*v, int4, p, w, e, int(g_group_m.load()), stream), "tile kernel launch");
 }

@@ -51,7 +51,7 @@ void set_decode_trace(void* ptr) {
 }
 #define DECODE_TRACE(i)                                                   \
   if (g_decode_trace && threadIdx.x == 0)                                 \
-    g_decode_trace[blockIdx.x * 8 + (i)] = __builtin_amdgcn_s_memrealtime();
+    g_decode_trace[blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memrealtime();
 #else
 #define DECODE_TRACE(i)
 #endif
@@ -130,16 +130,8 @@ __device__ __forceinline__ void mma_tile(const uint16_t* xs, int t, const u32x4_
     for (int mb = 0; mb < 4; ++mb) acc[mb] = mfma_16x16x32(a[kk][mb], b[kk], acc[mb]);
 }
 
-// 8 consecutive bf16 (16 bytes; one vector load when 16-byte aligned).
-__device__ __forceinline__ u32x4_t load8_bf16(const uint16_t* ptr, bool vec) {
-  if (vec) return *reinterpret_cast<const u32x4_t*>(ptr);
-  u32x4_t v;
-  v.x = uint32_t(ptr[0]) | (uint32_t(ptr[1]) << 16);
-  v.y = uint32_t(ptr[2]) | (uint32_t(ptr[3]) << 16);
-  v.z = uint32_t(ptr[4]) | (uint32_t(ptr[5]) << 16);
-  v.w = uint32_t(ptr[6]) | (uint32_t(ptr[7]) << 16);
-  return v;
-}
+// 8 consecutive bf16 (16 bytes, 16-byte aligned: the launcher checks gamma / cos / sin).
+__device__ __forceinline__ u32x4_t load8_bf16(const uint16_t* ptr) { return *reinterpret_cast<const u32x4_t*>(ptr); }
 
 // Element i (0..7) of 8 packed bf16, as float.
 __device__ __forceinline__ float bf16_lane(const u32x4_t& v, int i) {
@@ -306,7 +298,7 @@ __device__ __forceinline__ void partial_dispatch(const ProblemArgs& p, const Wei
 template <bool INT4>
 __global__ void __launch_bounds__(kDecThreads, 1)
 decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __restrict__ part,
-              uint32_t* __restrict__ counters, int force_recompute, bool vec_epi) {
+              uint32_t* __restrict__ counters, int force_recompute) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[kDecRows * kDecKc];
   __shared__ uint32_t arrival;
   const uint32_t xs_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(xs));
@@ -326,6 +318,10 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   int proj, hh;
   split_head(head, e.Hq, e.Hkv, proj, hh);
   DECODE_TRACE(0)
+
+  // RoPE table row of this thread's finisher row (tid / 8), read now: a
+  // positions[] load here is off every critical path
+  const int64_t prow = (proj != 2 && (tid >> 3) < M) ? rope_row(e.positions, tid >> 3, e.S, e.cos_rows) * kHeadDim : 0;
 
   int kt0, nk;
   split_range(split, splits, nkt, kt0, nk);
@@ -349,23 +345,27 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   const uint32_t seen = arrival;
   if ((seen & (kForeignUnit - 1)) != uint32_t(splits)) return;  // not the last split to arrive
   const bool recompute = (seen >> 16) != 0;
+  DECODE_TRACE(8)
 
   // thread -> row r = tid / 8, c = tid % 8 of the head tile: columns [8c, 8c+8)
   // and [64+8c, 64+8c+8), so every RoPE pair (d, d+64) is thread-local.  Its
-  // gamma / cos / sin operands are loaded now, under the partial reads.
+  // gamma / cos / sin operands are loaded under the partial reads; its RoPE row
+  // (prow, which may need a positions[] load) was read at kernel start so that
+  // no dependent load stalls the finisher.
   const int r = tid >> 3;
   const int c = tid & 7;
   u32x4_t g_lo{}, g_hi{}, c_lo{}, c_hi{}, s_lo{}, s_hi{};
-  if (proj != 2 && r < M) {
-    const uint16_t* gamma = proj == 0 ? e.q_gamma : e.k_gamma;
-    const int64_t prow = rope_row(e.positions, r, e.S, e.cos_rows) * kHeadDim;
-    g_lo = load8_bf16(gamma + 8 * c, vec_epi);
-    g_hi = load8_bf16(gamma + kHalfDim + 8 * c, vec_epi);
-    c_lo = load8_bf16(e.cos + prow + 8 * c, vec_epi);
-    c_hi = load8_bf16(e.cos + prow + kHalfDim + 8 * c, vec_epi);
-    s_lo = load8_bf16(e.sin + prow + 8 * c, vec_epi);
-    s_hi = load8_bf16(e.sin + prow + kHalfDim + 8 * c, vec_epi);
-  }
+  auto load_operands = [&]() {
+    if (proj != 2 && r < M) {
+      const uint16_t* gamma = proj == 0 ? e.q_gamma : e.k_gamma;
+      g_lo = load8_bf16(gamma + 8 * c);
+      g_hi = load8_bf16(gamma + kHalfDim + 8 * c);
+      c_lo = load8_bf16(e.cos + prow + 8 * c);
+      c_hi = load8_bf16(e.cos + prow + kHalfDim + 8 * c);
+      s_lo = load8_bf16(e.sin + prow + 8 * c);
+      s_hi = load8_bf16(e.sin + prow + kHalfDim + 8 * c);
+    }
+  };
 
   // ---- last arrival: sum the partials in split order ---------------------------------
   f32x4_t sum[4];
@@ -382,41 +382,41 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
     const int64_t split_stride = int64_t(n_tiles) * kTileFloats * sizeof(float);
     const uint32_t slot0 = xs_lds + uint32_t(wave * 4096);
     const char* slot0_ptr = reinterpret_cast<const char*>(xs) + wave * 4096;
-    int s = 0;
-    while (s < splits) {
-      int s_end = s, n_other = 0;
-      while (s_end < splits && (s_end == split || n_other < 4)) {
-        if (s_end != split) ++n_other;
-        ++s_end;
-      }
-      int slot = 0;
-      for (int q = s; q < s_end; ++q) {
-        if (q == split) continue;
+    load_operands();
+    int slot = 0, first = 0;
+#pragma unroll 1
+    for (int q = 0; q < splits; ++q) {
+      if (q != split) {
         const char* src = frag + q * split_stride + lane * 16;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
           dma16(src + mb * 1024, slot0 + uint32_t(slot * kDecWaves * 4096 + mb * 1024));
         ++slot;
       }
-      wait_vm<0>();
-      slot = 0;
-      for (int q = s; q < s_end; ++q) {
-        if (q == split) {
+      if (slot == 4 || q == splits - 1) {  // four slots filled, or the last split: add in split order
+        wait_vm<0>();
+        int u_slot = 0;
+#pragma unroll 1
+        for (int u = first; u <= q; ++u) {
+          if (u == split) {
 #pragma unroll
-          for (int mb = 0; mb < 4; ++mb) sum[mb] += acc[mb];
-          continue;
+            for (int mb = 0; mb < 4; ++mb) sum[mb] += acc[mb];
+          } else {
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+              sum[mb] += *reinterpret_cast<const f32x4_t*>(slot0_ptr + u_slot * kDecWaves * 4096 + mb * 1024 + lane * 16);
+            ++u_slot;
+          }
         }
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
-          sum[mb] += *reinterpret_cast<const f32x4_t*>(slot0_ptr + slot * kDecWaves * 4096 + mb * 1024 + lane * 16);
-        ++slot;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next batch overwrites
+        slot = 0;
+        first = q + 1;
       }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next batch overwrites
-      s = s_end;
     }
   } else {
     // Some split ran on another XCD: its partial may not be visible through this
     // L2.  Recompute every split here (same arithmetic, same order).
+    load_operands();
     for (int s = 0; s < splits; ++s) {
       int s_kt0, s_nk;
       split_range(s, splits, nkt, s_kt0, s_nk);
@@ -544,13 +544,13 @@ hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, co
   const dim3 grid(((p.n_tiles + kXcds - 1) / kXcds) * kXcds * splits);
   const int fr = g_decode_force_recompute;
   auto a16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; };
-  const bool vec = a16(e.q_gamma) && a16(e.k_gamma) && a16(e.cos) && a16(e.sin);
+  if (!(a16(e.q_gamma) && a16(e.k_gamma) && a16(e.cos) && a16(e.sin))) return hipErrorInvalidValue;
   if (int4)
     hipLaunchKernelGGL(decode_kernel<true>, grid, dim3(kDecThreads), 0, stream, p, w, e, splits, part, counters,
-                       fr, vec);
+                       fr);
   else
     hipLaunchKernelGGL(decode_kernel<false>, grid, dim3(kDecThreads), 0, stream, p, w, e, splits, part,
-                       counters, fr, vec);
+                       counters, fr);
   return hipGetLastError();
 }
 
