@@ -226,11 +226,12 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="mqk fused QKV + QK-Norm + RoPE benchmark")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip configs 3-5")
     ap.add_argument("--only", choices=WORKLOADS,
                     help="run one workload alone (profiler runs; 'copy' = 256 MiB calibration copy)")
+    ap.add_argument("--tile", type=int, default=0, help="force a prefill tile variant (mqk.tile_variants())")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the op has no multi-GPU path); "
@@ -244,6 +245,8 @@ def main(argv=None) -> int:
         return 2
     dev = torch.device("cuda:0")
     mqk.library()  # fail loudly before any timing if libmqk.so is missing
+    if args.tile:
+        mqk.set_option("prefill_tile", args.tile)
     if args.only:
         run_only(args.only, args.steps, args.warmup, dev)
         return 0

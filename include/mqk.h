@@ -143,7 +143,7 @@ int mqk_fused_qkv_rope_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void*
  *                    0 disables it)
  *   "decode_splits"  0 = auto, otherwise the split-K factor of the decode kernel (1..16,
  *                    at most 16 64-wide k tiles per split; otherwise the tile kernel runs)
- *   "group_m"        row tiles per tile-ordering group of the tile kernel (default 4)
+ *   "group_m"        row tiles per tile-ordering group of the tile kernel (default 8)
  *   "decode_force_recompute"  1: the decode kernel takes its recompute path (used when a
  *                    split ran on an unexpected XCD) for every head; for tests
  * Returns MQK_OK or MQK_ERR_BAD_OPTION.

@@ -40,7 +40,7 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 std::atomic<int64_t> g_prefill_tile{0};
 std::atomic<int64_t> g_decode_max_t{64};
 std::atomic<int64_t> g_decode_splits{0};
-std::atomic<int64_t> g_group_m{4};
+std::atomic<int64_t> g_group_m{8};
 
 constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace (per head)
 
@@ -305,6 +305,10 @@ int mqk_set_option(const char* name, int64_t value) {
 #ifdef MQK_DECODE_TRACE
   } else if (!strcmp(name, "decode_trace")) {  // diagnostic builds only
     set_decode_trace(reinterpret_cast<void*>(value));
+#endif
+#ifdef MQK_TILE_TRACE
+  } else if (!strcmp(name, "tile_trace")) {  // diagnostic builds only
+    set_tile_trace(reinterpret_cast<void*>(value));
 #endif
   } else if (!strcmp(name, "group_m")) {
     if (value < 1 || value > 1024) return fail(MQK_ERR_BAD_OPTION, "group_m must be in [1, 1024]");

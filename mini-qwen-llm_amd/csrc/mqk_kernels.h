@@ -81,6 +81,9 @@ hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, co
 // taken when a split ran on an unexpected XCD); for tests.
 extern int g_decode_force_recompute;
 
+#ifdef MQK_TILE_TRACE
+void set_tile_trace(void* ptr);
+#endif
 #ifdef MQK_DECODE_TRACE
 void set_decode_trace(void* ptr);  // diagnostic builds only
 #endif

@@ -351,7 +351,7 @@ hipError_t launch_dispatch(int int4, const ProblemArgs& p, const WeightArgs& w,
 }
 
 // ids 1-5: register-staged kernel above (bf16 and int4 weights);
-// ids 10-14: direct-to-LDS pipelined kernel (qkv_tile_dma.hip, bf16 weights only).
+// ids 10-18: direct-to-LDS pipelined kernel (qkv_tile_dma.hip, bf16 weights only).
 const TileVariant kVariants[] = {
     {1, 128, 1, 2, 256},
     {2, 256, 1, 1, 256},
@@ -364,6 +364,9 @@ const TileVariant kVariants[] = {
     {13, 128, 2, 0, 256},
     {14, 256, 2, 0, 512},
     {15, 128, 3, 0, 512},
+    {16, 128, 3, 0, 512},
+    {17, 256, 2, 0, 512},
+    {18, 256, 2, 0, 512},
 };
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 
@@ -390,10 +393,13 @@ const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles,
   // Score = relative per-tile speed (measured on MI355X) x fraction of the last
   // round of workgroups that is busy, assuming one workgroup per CU at a time.
   struct Cand { int id; float speed; };
-  static const Cand bf16_cands[] = {{11, 1.00f}, {10, 1.03f}, {13, 0.85f}, {12, 0.85f}, {1, 0.55f}};
+  // (per-tile rates measured on MI355X: 64-wide k stages (16, 17, 18) beat 32-wide
+  // ones; 128x384 wins when its tiles fill the chip, 256x256 otherwise)
+  static const Cand bf16_cands[] = {{16, 1.00f}, {18, 1.27f}, {17, 1.26f}, {11, 0.94f}, {10, 1.19f},
+                                    {13, 0.75f}, {12, 0.75f}, {1, 0.50f}};
   static const Cand int4_cands[] = {{4, 1.00f}, {2, 0.90f}, {3, 0.90f}, {1, 0.80f}};
   const Cand* cands = int4 ? int4_cands : bf16_cands;
-  const int ncand = int4 ? 4 : 5;
+  const int ncand = int4 ? 4 : int(sizeof(bf16_cands) / sizeof(bf16_cands[0]));
   const int64_t cus = 256;
   const TileVariant* best = find_variant(1);
   float best_score = -1.f;

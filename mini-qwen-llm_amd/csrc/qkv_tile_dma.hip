@@ -2,8 +2,8 @@
 // (bf16 weights; the prefill / large-T path).
 //
 // A workgroup computes a BM x (NH*128) tile of  x[M,K] @ W^T  (NH whole heads;
-// the Q/K/V weight matrices are addressed directly).  K is consumed in 32-wide
-// stages held in an NS-deep LDS ring that is filled with global_load_lds_dwordx4
+// the Q/K/V weight matrices are addressed directly).  K is consumed in SBK-wide
+// (32 or 64) stages held in an NS-deep LDS ring that is filled with global_load_lds_dwordx4
 // (L2 -> LDS without VGPRs): while stage k is multiplied, the loads of stages
 // k+1 .. k+NS-1 are in flight, which hides the L2 latency that a single
 // register-staged prefetch could not.  One barrier per stage: after it, every
@@ -32,14 +32,24 @@
 #include "mqk_kernels.h"
 
 namespace mqk {
+
+#ifdef MQK_TILE_TRACE
+__constant__ int64_t* g_tile_trace = nullptr;
+void set_tile_trace(void* ptr) { (void)hipMemcpyToSymbol(HIP_SYMBOL(g_tile_trace), &ptr, sizeof(ptr)); }
+#endif
+
 namespace {
 
-constexpr int kSBK = 32;                    // K extent of one stage
-constexpr int kRowBytes = kSBK * 2;         // 64 B per staged row
 constexpr int kEpiPitch = kHeadDim + 4;     // fp32 pitch of the epilogue head tile
 
-template <int BM, int NH, int WM, int WN, int NS>
+// SBK = K extent of one stage (32 or 64): staged rows of 64 or 128 bytes.  A
+// CU's L2 -> LDS rate depends on the bytes per row: 128-byte rows measured
+// ~1.35x the rate of 64-byte rows (fewer, full-line requests in flight).
+template <int BM, int NH, int WM, int WN, int NS, int SBK>
 struct DmaShape {
+  static constexpr int kRowBytes = SBK * 2;
+  static constexpr int kChunks = kRowBytes / 16;         // 16-byte chunks per staged row
+  static constexpr int kRowsPerLoad = 1024 / kRowBytes;  // rows filled by one 1 KB load instruction
   static constexpr int kBN = NH * kHeadDim;
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = kWaves * 64;
@@ -49,7 +59,7 @@ struct DmaShape {
   static constexpr int kNB = kTN / 32;
   static constexpr int kRows = BM + kBN;                // staged rows per stage
   static constexpr int kStageBytes = kRows * kRowBytes;
-  static constexpr int kLoadsPerStage = kRows / 16;     // 1 KB load instructions
+  static constexpr int kLoadsPerStage = kRows / kRowsPerLoad;  // 1 KB load instructions
   static constexpr int kLoadsPerWave = kLoadsPerStage / kWaves;
   static constexpr int kRingBytes = NS * kStageBytes;
   static constexpr int kEpiBytes = BM * kEpiPitch * 4;
@@ -75,12 +85,19 @@ __device__ __forceinline__ void wait_stage(int remaining_after) {
   (void)NS;
 }
 
-__device__ __forceinline__ int stage_slot(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+// LDS slot of 16-byte chunk `chunk` of staged row `row`: the 16 rows one
+// quarter-wave reads (same chunk) land in 16 different bank groups.
+template <int SBK>
+__device__ __forceinline__ int stage_slot(int row, int chunk) {
+  if constexpr (SBK == 32) return chunk ^ ((row >> 2) & 3);  // 64 B rows: rows r, r+4, r+8, r+12 share banks
+  else return chunk ^ ((row >> 1) & 7);                       // 128 B rows: even / odd rows use bank halves
+}
 
-template <int BM, int NH, int WM, int WN, int NS>
+template <int BM, int NH, int WM, int WN, int NS, int SBK>
 __global__ void __launch_bounds__(WM* WN * 64)
 tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
-  using S = DmaShape<BM, NH, WM, WN, NS>;
+  using S = DmaShape<BM, NH, WM, WN, NS, SBK>;
+  constexpr int kRowBytes = S::kRowBytes;
   constexpr int BN = S::kBN;
   __shared__ __attribute__((aligned(16))) unsigned char smem[S::kLdsBytes];
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
@@ -103,17 +120,32 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   const int mt = first_m + rr % gsz;
   const int ht = rr / gsz;
   const int64_t m0 = int64_t(mt) * BM;
+
+  // Epilogue geometry: thread -> rows (tid / 8) + q * kRowStep and the column pairs
+  // [8c, 8c+8) / [64+8c, +8) of every head.  The RoPE table row of each of its
+  // rows (a positions[] load in positions mode) is read now, under the main loop.
+  constexpr int kRowStep = S::kThreads / 8;
+  constexpr int kPasses = BM / kRowStep;
+  // gamma / cos / sin depend only on the token: with few rows per thread they are
+  // loaded once for all NH heads of the tile (16 VGPRs per row)
+  constexpr bool kPreload = kPasses <= 4;
+  int32_t prow[kPasses];
+#pragma unroll
+  for (int q = 0; q < kPasses; ++q) {
+    const int64_t t = m0 + (tid >> 3) + q * kRowStep;
+    prow[q] = (e.qkv && t < p.M) ? int32_t(rope_row(e.positions, t, e.S, e.cos_rows)) : 0;
+  }
   const int64_t K = p.K;
 
   // ---- this lane's sources: load instruction i of a stage fills staged rows
-  // [16*(wave + i*W), +16); lane -> row +lane/4, slot lane%4 ----------------------
+  // [R*(wave + i*W), +R), R = rows per load; lane -> row +lane/chunks, slot lane%chunks
   const uint16_t* src[S::kLoadsPerWave];
   uint32_t dst_off[S::kLoadsPerWave];
 #pragma unroll
   for (int i = 0; i < S::kLoadsPerWave; ++i) {
-    const int row0 = 16 * (wave + i * S::kWaves);
-    const int row = row0 + (lane >> 2);
-    const int chunk = stage_slot(row, lane & 3);  // global chunk stored in slot lane & 3
+    const int row0 = S::kRowsPerLoad * (wave + i * S::kWaves);
+    const int row = row0 + lane / S::kChunks;
+    const int chunk = stage_slot<SBK>(row, lane % S::kChunks);  // global chunk stored in slot lane % chunks
     if (row < BM) {
       int64_t grow = m0 + row;
       grow = grow < p.M ? grow : p.M - 1;  // rows past M re-read the last row; never stored
@@ -131,7 +163,12 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   auto issue = [&](int kt) {
     const uint32_t base = lds0 + uint32_t((kt % NS) * S::kStageBytes);
 #pragma unroll
-    for (int i = 0; i < S::kLoadsPerWave; ++i) dma16(src[i] + int64_t(kt) * kSBK, base + dst_off[i]);
+    for (int i = 0; i < S::kLoadsPerWave; ++i) {
+#ifdef MQK_DIAG_NOLOAD  // diagnostic build: K loop without global loads (timing only, wrong results)
+      if (kt >= NS) break;
+#endif
+      dma16(src[i] + int64_t(kt) * SBK, base + dst_off[i]);
+    }
   };
 
   // ---- main loop -------------------------------------------------------------------
@@ -143,7 +180,11 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
 
   const int c32 = lane & 31;
   const int khalf = lane >> 5;
-  const int nkt = int(K / kSBK);
+#ifdef MQK_DIAG_NOLOOP  // diagnostic build: epilogue only (timing only, wrong results)
+  const int nkt = 0;
+#else
+  const int nkt = int(K / SBK);
+#endif
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
     if (s < nkt) issue(s);
@@ -151,32 +192,66 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   for (int kt = 0; kt < nkt; ++kt) {
     const int ahead = min(NS - 2, nkt - 1 - kt);  // stages already issued after kt
     wait_stage<NS, S::kLoadsPerWave>(ahead);
+#ifdef MQK_TILE_TRACE  // diagnostic build: per-stage timestamps of wave 0 of each workgroup
+    if (g_tile_trace && tid == 0 && kt < 126) g_tile_trace[blockIdx.x * 256 + 2 * kt] = __builtin_amdgcn_s_memrealtime();
+#endif
     barrier();
+#ifdef MQK_TILE_TRACE
+    if (g_tile_trace && tid == 0 && kt < 126) g_tile_trace[blockIdx.x * 256 + 2 * kt + 1] = __builtin_amdgcn_s_memrealtime();
+#endif
     if (kt + NS - 1 < nkt) issue(kt + NS - 1);
     const unsigned char* st = smem + (kt % NS) * S::kStageBytes;
 #pragma unroll
-    for (int ks = 0; ks < kSBK / 16; ++ks) {
+    for (int ks = 0; ks < SBK / 16; ++ks) {
       const int chunk = 2 * ks + khalf;
       u32x4_t af[S::kMB], bf[S::kNB];
 #pragma unroll
       for (int mb = 0; mb < S::kMB; ++mb) {
         const int row = wm * S::kTM + mb * 32 + c32;
-        af[mb] = *reinterpret_cast<const u32x4_t*>(st + row * kRowBytes + stage_slot(row, chunk) * 16);
+        af[mb] = *reinterpret_cast<const u32x4_t*>(st + row * kRowBytes + stage_slot<SBK>(row, chunk) * 16);
       }
 #pragma unroll
       for (int nb = 0; nb < S::kNB; ++nb) {
         const int row = BM + wn * S::kTN + nb * 32 + c32;
-        bf[nb] = *reinterpret_cast<const u32x4_t*>(st + row * kRowBytes + stage_slot(row, chunk) * 16);
+        bf[nb] = *reinterpret_cast<const u32x4_t*>(st + row * kRowBytes + stage_slot<SBK>(row, chunk) * 16);
       }
 #pragma unroll
       for (int mb = 0; mb < S::kMB; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < S::kNB; ++nb) acc[mb][nb] = mfma_32x32x16(af[mb], bf[nb], acc[mb][nb]);
+        for (int nb = 0; nb < S::kNB; ++nb) {
+#ifdef MQK_DIAG_NOMFMA  // diagnostic build: K loop without MFMAs (timing only, wrong results)
+          acc[mb][nb][0] += __builtin_bit_cast(float, af[mb][0] ^ bf[nb][0]);
+#else
+          acc[mb][nb] = mfma_32x32x16(af[mb], bf[nb], acc[mb][nb]);
+#endif
+        }
     }
   }
   barrier();  // every wave is done with the ring; the epilogue reuses the LDS
+#ifdef MQK_TILE_TRACE
+  if (g_tile_trace && tid == 0) g_tile_trace[blockIdx.x * 256 + 252] = __builtin_amdgcn_s_memrealtime();
+#endif
 
   // ---- epilogue, one head at a time --------------------------------------------------
+  const int c8 = tid & 7;
+  u32x4_t gq[2] = {}, gk[2] = {}, cs[kPreload ? kPasses : 1][2] = {}, sn[kPreload ? kPasses : 1][2] = {};
+  auto load_rows = [&](int q, u32x4_t (&c2)[2], u32x4_t (&s2)[2]) {
+    const int64_t base = int64_t(prow[q]) * kHeadDim;
+    c2[0] = *reinterpret_cast<const u32x4_t*>(e.cos + base + 8 * c8);
+    c2[1] = *reinterpret_cast<const u32x4_t*>(e.cos + base + kHalfDim + 8 * c8);
+    s2[0] = *reinterpret_cast<const u32x4_t*>(e.sin + base + 8 * c8);
+    s2[1] = *reinterpret_cast<const u32x4_t*>(e.sin + base + kHalfDim + 8 * c8);
+  };
+  if (e.qkv) {
+    gq[0] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + 8 * c8);
+    gq[1] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + kHalfDim + 8 * c8);
+    gk[0] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + 8 * c8);
+    gk[1] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + kHalfDim + 8 * c8);
+    if constexpr (kPreload) {
+#pragma unroll
+      for (int q = 0; q < kPasses; ++q) load_rows(q, cs[q], sn[q]);
+    }
+  }
   float* ep = reinterpret_cast<float*>(smem);
   const int half = lane >> 5;
 #pragma unroll
@@ -199,8 +274,9 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
     const int head = ht * NH + j;
     int proj, hh;
     split_head(head, e.Hq, e.Hkv, proj, hh);
-    const int c8 = tid & 7;
-    for (int r0 = tid >> 3; r0 < BM; r0 += S::kThreads / 8) {
+#pragma unroll
+    for (int q = 0; q < kPasses; ++q) {
+      const int r0 = (tid >> 3) + q * kRowStep;
       const int64_t t = m0 + r0;
       const float* rowp = ep + r0 * kEpiPitch;
       float lo[8], hi[8];
@@ -220,27 +296,24 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
         ss += __shfl_xor(ss, 2);
         ss += __shfl_xor(ss, 4);
         const float rms = rsqrtf(ss * (1.0f / float(kHeadDim)) + e.eps);
-        if (t < p.M) {
-          const uint16_t* gamma = proj == 0 ? e.q_gamma : e.k_gamma;
-          const int64_t prow = rope_row(e.positions, t, e.S, e.cos_rows) * kHeadDim;
-          const u32x4_t g1 = *reinterpret_cast<const u32x4_t*>(gamma + 8 * c8);
-          const u32x4_t g2 = *reinterpret_cast<const u32x4_t*>(gamma + kHalfDim + 8 * c8);
-          const u32x4_t cs1 = *reinterpret_cast<const u32x4_t*>(e.cos + prow + 8 * c8);
-          const u32x4_t cs2 = *reinterpret_cast<const u32x4_t*>(e.cos + prow + kHalfDim + 8 * c8);
-          const u32x4_t sn1 = *reinterpret_cast<const u32x4_t*>(e.sin + prow + 8 * c8);
-          const u32x4_t sn2 = *reinterpret_cast<const u32x4_t*>(e.sin + prow + kHalfDim + 8 * c8);
+        u32x4_t c2[2], s2[2];
+        if constexpr (kPreload) {
+          c2[0] = cs[q][0]; c2[1] = cs[q][1]; s2[0] = sn[q][0]; s2[1] = sn[q][1];
+        } else {
+          load_rows(q, c2, s2);
+        }
+        const u32x4_t* g = proj == 0 ? gq : gk;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int wd = i >> 1, sh = (i & 1) * 16;
-            const float x1n = lo[i] * rms * bf16_to_f32((g1[wd] >> sh) & 0xFFFFu);
-            const float x2n = hi[i] * rms * bf16_to_f32((g2[wd] >> sh) & 0xFFFFu);
-            const float c1 = bf16_to_f32((cs1[wd] >> sh) & 0xFFFFu);
-            const float c2 = bf16_to_f32((cs2[wd] >> sh) & 0xFFFFu);
-            const float s1 = bf16_to_f32((sn1[wd] >> sh) & 0xFFFFu);
-            const float s2 = bf16_to_f32((sn2[wd] >> sh) & 0xFFFFu);
-            lo[i] = x1n * c1 - x2n * s1;
-            hi[i] = x2n * c2 + x1n * s2;
-          }
+        for (int i = 0; i < 8; ++i) {
+          const int wd = i >> 1, sh = (i & 1) * 16;
+          const float x1n = lo[i] * rms * bf16_to_f32((g[0][wd] >> sh) & 0xFFFFu);
+          const float x2n = hi[i] * rms * bf16_to_f32((g[1][wd] >> sh) & 0xFFFFu);
+          const float co1 = bf16_to_f32((c2[0][wd] >> sh) & 0xFFFFu);
+          const float co2 = bf16_to_f32((c2[1][wd] >> sh) & 0xFFFFu);
+          const float si1 = bf16_to_f32((s2[0][wd] >> sh) & 0xFFFFu);
+          const float si2 = bf16_to_f32((s2[1][wd] >> sh) & 0xFFFFu);
+          lo[i] = x1n * co1 - x2n * si1;
+          hi[i] = x2n * co2 + x1n * si2;
         }
       }
       if (t < p.M) {
@@ -264,15 +337,18 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
     }
     __syncthreads();  // the next head reuses ep
   }
+#ifdef MQK_TILE_TRACE
+  if (g_tile_trace && tid == 0) g_tile_trace[blockIdx.x * 256 + 253] = __builtin_amdgcn_s_memrealtime();
+#endif
 }
 
-template <int BM, int NH, int WM, int WN, int NS>
+template <int BM, int NH, int WM, int WN, int NS, int SBK = 32>
 hipError_t launch_dma(const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e, int group_m,
                       hipStream_t stream) {
-  using S = DmaShape<BM, NH, WM, WN, NS>;
+  using S = DmaShape<BM, NH, WM, WN, NS, SBK>;
   const int n_mt = int((p.M + BM - 1) / BM);
   const int blocks = n_mt * (p.n_tiles / NH);
-  hipLaunchKernelGGL((tile_dma_kernel<BM, NH, WM, WN, NS>), dim3(blocks), dim3(S::kThreads), 0, stream, p, w, e,
+  hipLaunchKernelGGL((tile_dma_kernel<BM, NH, WM, WN, NS, SBK>), dim3(blocks), dim3(S::kThreads), 0, stream, p, w, e,
                      group_m < 1 ? 1 : group_m);
   return hipGetLastError();
 }
@@ -288,6 +364,9 @@ hipError_t launch_tile_dma(int id, const ProblemArgs& p, const WeightArgs& w, co
     case 13: return launch_dma<128, 2, 2, 2, 4>(p, w, e, group_m, stream);   // 128x256, 4 waves
     case 14: return launch_dma<256, 2, 2, 4, 4>(p, w, e, group_m, stream);   // 256x256, 8 waves (128x64)
     case 15: return launch_dma<128, 3, 2, 4, 5>(p, w, e, group_m, stream);   // 128x384, 5 stages
+    case 16: return launch_dma<128, 3, 2, 4, 2, 64>(p, w, e, group_m, stream);  // 128x384, 2 stages of 64 k
+    case 17: return launch_dma<256, 2, 4, 2, 2, 64>(p, w, e, group_m, stream);  // 256x256, 2 stages of 64 k
+    case 18: return launch_dma<256, 2, 2, 4, 2, 64>(p, w, e, group_m, stream);  // 256x256 (128x64 waves), 64 k
     default: return hipErrorInvalidValue;
   }
 }
