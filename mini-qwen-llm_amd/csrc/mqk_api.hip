@@ -78,6 +78,12 @@ EpilogueArgs make_qkv_epilogue(const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
   return e;
 }
 
+bool int4_aligned(const WeightArgs& w) {
+  for (int i = 0; i < 3; ++i)
+    if (!aligned16(w.qw[i]) || !aligned16(w.sc[i]) || !aligned16(w.qz[i])) return false;
+  return true;
+}
+
 bool use_decode(int64_t T) { return T >= 1 && T <= g_decode_max_t.load() && T <= 64; }
 
 // The split-K decode kernel and the pipelined tile variants read gamma / cos /
@@ -103,8 +109,8 @@ int run_fused(int int4, const ProblemArgs& p, const WeightArgs& w, const Epilogu
   const TileVariant* v = choose_tile_variant(int(g_prefill_tile.load()), p.M, p.n_tiles, int4);
   if (!v) return fail(MQK_ERR_BAD_OPTION, "prefill_tile variant %lld cannot run this problem (%d heads%s)",
                       (long long)g_prefill_tile.load(), p.n_tiles, int4 ? ", int4 weights" : "");
-  // The pipelined variants read gamma/cos/sin rows with 16-byte loads.
-  if (v->id >= 10 && !epilogue_aligned(e))
+  // The pipelined variants (ids >= 10) read every operand with 16-byte direct loads.
+  if (v->id >= 10 && !(epilogue_aligned(e) && (!int4 || int4_aligned(w))))
     v = choose_tile_variant(p.n_tiles % 2 == 0 ? 4 : 1, p.M, p.n_tiles, int4);
   return hip_status(launch_tile(*v, int4, p, w, e, int(g_group_m.load()), stream), "tile kernel launch");
 }
@@ -240,7 +246,12 @@ int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales
   e.Hkv = 0;
   e.out = out;
   e.N = N;
-  const TileVariant* v = choose_tile_variant(1, M, tiles, 1);
+  // Whole 128-column tiles can use any int4 variant; a partial last tile needs the
+  // register-staged kernel (variant 1), which bounds-checks columns.
+  const TileVariant* v = nullptr;
+  if (N % kHeadDim == 0 && aligned16(qweight) && aligned16(scales) && aligned16(qzeros))
+    v = choose_tile_variant(int(g_prefill_tile.load()), M, tiles, 1);
+  if (!v) v = choose_tile_variant(1, M, tiles, 1);
   return hip_status(launch_tile(*v, 1, p, w, e, int(g_group_m.load()), static_cast<hipStream_t>(stream)),
                     "w4a16 tile kernel launch");
 }

@@ -34,8 +34,12 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 }
 
 // Two floats -> packed bf16x2 (low half = a).
+// Two floats -> two bf16 (round to nearest even) in one 32-bit word, low half first;
+// one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return uint32_t(f32_to_bf16(a)) | (uint32_t(f32_to_bf16(b)) << 16);
+  typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+  typedef float f32x2_v __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_v){a, b}, bf16x2_v));
 }
 
 __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
@@ -60,11 +64,18 @@ __device__ __forceinline__ f32x4_t mfma_16x16x32(u32x4_t a, u32x4_t b, f32x4_t c
 // w = (q - z) * s, exact in fp32 (|q - z| <= 15 times an 8/11-bit mantissa),
 // then one rounding to bf16.  Nibble e holds k = 8j + e (little-endian nibbles).
 __device__ __forceinline__ u32x4_t dequant_int4x8(uint32_t packed, float zero, float scale) {
+  // (q - z) * s with q, z in 0..15 and a 16-bit (bf16 / fp16) scale: q*s and z*s
+  // have at most 15 significant bits, so fma(q, s, -z*s) is exact in fp32 and
+  // equals (q - z) * s bit for bit; the nibbles are split into bytes so each
+  // converts with one byte-to-float instruction.
+  const float zs = zero * scale;
+  const uint32_t even = packed & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6
+  const uint32_t odd = (packed >> 4) & 0x0F0F0F0Fu;   // nibbles 1, 3, 5, 7
   float w[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float q = static_cast<float>((packed >> (4 * e)) & 0xFu);
-    w[e] = (q - zero) * scale;
+  for (int b = 0; b < 4; ++b) {
+    w[2 * b] = __builtin_fmaf(static_cast<float>((even >> (8 * b)) & 0xFFu), scale, -zs);
+    w[2 * b + 1] = __builtin_fmaf(static_cast<float>((odd >> (8 * b)) & 0xFFu), scale, -zs);
   }
   u32x4_t r;
   r.x = pack_bf16x2(w[0], w[1]);

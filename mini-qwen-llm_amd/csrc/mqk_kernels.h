@@ -68,6 +68,9 @@ hipError_t launch_tile(const TileVariant& v, int int4, const ProblemArgs& p, con
 // Direct-to-LDS pipelined tile kernel (variant ids >= 10, bf16 weights).
 hipError_t launch_tile_dma(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e, int group_m,
                            hipStream_t stream);
+// int4-weight (W4A16) variant of the pipelined kernel, ids 30-32.
+hipError_t launch_tile_dma_w4(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
+                              int group_m, hipStream_t stream);
 
 // Split-K decode kernel for T <= 64.  decode_splits_for returns 0 when no
 // valid split count exists (each split covers at most 16 64-wide k tiles);

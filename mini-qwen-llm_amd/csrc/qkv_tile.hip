@@ -351,7 +351,8 @@ hipError_t launch_dispatch(int int4, const ProblemArgs& p, const WeightArgs& w,
 }
 
 // ids 1-5: register-staged kernel above (bf16 and int4 weights);
-// ids 10-18: direct-to-LDS pipelined kernel (qkv_tile_dma.hip, bf16 weights only).
+// ids 10-18: direct-to-LDS pipelined kernel (qkv_tile_dma.hip, bf16 weights only);
+// ids 30-32: its int4-weight twin (W4A16 only).
 const TileVariant kVariants[] = {
     {1, 128, 1, 2, 256},
     {2, 256, 1, 1, 256},
@@ -367,6 +368,9 @@ const TileVariant kVariants[] = {
     {16, 128, 3, 0, 512},
     {17, 256, 2, 0, 512},
     {18, 256, 2, 0, 512},
+    {30, 128, 3, 0, 512},
+    {31, 256, 2, 0, 512},
+    {32, 128, 2, 0, 256},
 };
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 
@@ -384,10 +388,15 @@ const TileVariant* find_variant(int id) {
   return nullptr;
 }
 
+// ids 1-5 take either weight type, 10-18 bf16 weights only, 30-32 int4 weights only
+static bool supports(const TileVariant& v, int int4) {
+  return v.id < 10 || (int4 ? v.id >= 30 : v.id < 30);
+}
+
 const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles, int int4) {
   if (requested_id > 0) {
     const TileVariant* v = find_variant(requested_id);
-    if (!v || n_tiles % v->hpt != 0 || (int4 && v->id >= 10)) return nullptr;
+    if (!v || n_tiles % v->hpt != 0 || !supports(*v, int4)) return nullptr;
     return v;
   }
   // Score = relative per-tile speed (measured on MI355X) x fraction of the last
@@ -397,15 +406,16 @@ const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles,
   // ones; 128x384 wins when its tiles fill the chip, 256x256 otherwise)
   static const Cand bf16_cands[] = {{16, 1.00f}, {18, 1.27f}, {17, 1.26f}, {11, 0.94f}, {10, 1.19f},
                                     {13, 0.75f}, {12, 0.75f}, {1, 0.50f}};
-  static const Cand int4_cands[] = {{4, 1.00f}, {2, 0.90f}, {3, 0.90f}, {1, 0.80f}};
+  static const Cand int4_cands[] = {{31, 1.00f}, {4, 0.94f}, {5, 0.78f}, {30, 0.75f}, {2, 0.63f},
+                                    {3, 0.61f}, {32, 0.54f}, {1, 0.51f}};
   const Cand* cands = int4 ? int4_cands : bf16_cands;
-  const int ncand = int4 ? 4 : int(sizeof(bf16_cands) / sizeof(bf16_cands[0]));
+  const int ncand = int(int4 ? sizeof(int4_cands) / sizeof(int4_cands[0]) : sizeof(bf16_cands) / sizeof(bf16_cands[0]));
   const int64_t cus = 256;
   const TileVariant* best = find_variant(1);
   float best_score = -1.f;
   for (int i = 0; i < ncand; ++i) {
     const TileVariant* v = find_variant(cands[i].id);
-    if (!v || n_tiles % v->hpt != 0) continue;
+    if (!v || n_tiles % v->hpt != 0 || !supports(*v, int4)) continue;
     const int64_t tiles = ((M + v->bm - 1) / v->bm) * (n_tiles / v->hpt);
     const int64_t rounds = (tiles + cus - 1) / cus;
     const float util = float(tiles) / float(rounds * cus);
@@ -422,6 +432,7 @@ const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles,
 
 hipError_t launch_tile(const TileVariant& v, int int4, const ProblemArgs& p, const WeightArgs& w,
                        const EpilogueArgs& e, int group_m, hipStream_t stream) {
+  if (v.id >= 30) return int4 ? launch_tile_dma_w4(v.id, p, w, e, group_m, stream) : hipErrorInvalidValue;
   if (v.id >= 10) return int4 ? hipErrorInvalidValue : launch_tile_dma(v.id, p, w, e, group_m, stream);
   switch (v.id) {
     case 1: return launch_dispatch<128, 1, 2>(int4, p, w, e, group_m, stream);

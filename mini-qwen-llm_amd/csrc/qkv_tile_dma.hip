@@ -93,6 +93,137 @@ __device__ __forceinline__ int stage_slot(int row, int chunk) {
   else return chunk ^ ((row >> 1) & 7);                       // 128 B rows: even / odd rows use bank halves
 }
 
+// Per-head epilogue of a BM x (NH*128) tile held in MFMA 32x32 accumulators:
+// wave (wm, wn) holds rows [wm*TM, +TM) x columns [wn*TN, +TN) as acc[mb][nb].
+// One head at a time, the waves covering it write their fp32 block to LDS `ep`,
+// then threads take 8-column pairs of a row (columns [8c, 8c+8) and
+// [64+8c, +8)), so the RMSNorm sum of squares is an 8-lane butterfly and every
+// RoPE pair is thread-local; each output row segment is written with 16-byte
+// stores.  prow[q] holds the RoPE table row of this thread's row (tid/8) + q*kRowStep.
+template <int BM, int NH, int WM, int WN, int THREADS, int MB, int NB>
+__device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], const int32_t* prow, int ht,
+                                              int64_t m0, const ProblemArgs& p, const EpilogueArgs& e,
+                                              unsigned char* smem) {
+  constexpr int kTM = BM / WM;
+  constexpr int kTN = NH * kHeadDim / WN;
+  constexpr int kRowStep = THREADS / 8;
+  constexpr int kPasses = BM / kRowStep;
+  // gamma / cos / sin depend only on the token: with few rows per thread they are
+  // loaded once for all NH heads of the tile (16 VGPRs per row)
+  constexpr bool kPreload = kPasses <= 4;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WM;
+  const int wn = wave / WM;
+  const int c32 = lane & 31;
+  // ---- epilogue, one head at a time --------------------------------------------------
+  const int c8 = tid & 7;
+  u32x4_t gq[2] = {}, gk[2] = {}, cs[kPreload ? kPasses : 1][2] = {}, sn[kPreload ? kPasses : 1][2] = {};
+  auto load_rows = [&](int q, u32x4_t (&c2)[2], u32x4_t (&s2)[2]) {
+    const int64_t base = int64_t(prow[q]) * kHeadDim;
+    c2[0] = *reinterpret_cast<const u32x4_t*>(e.cos + base + 8 * c8);
+    c2[1] = *reinterpret_cast<const u32x4_t*>(e.cos + base + kHalfDim + 8 * c8);
+    s2[0] = *reinterpret_cast<const u32x4_t*>(e.sin + base + 8 * c8);
+    s2[1] = *reinterpret_cast<const u32x4_t*>(e.sin + base + kHalfDim + 8 * c8);
+  };
+  if (e.qkv) {
+    gq[0] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + 8 * c8);
+    gq[1] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + kHalfDim + 8 * c8);
+    gk[0] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + 8 * c8);
+    gk[1] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + kHalfDim + 8 * c8);
+    if constexpr (kPreload) {
+#pragma unroll
+      for (int q = 0; q < kPasses; ++q) load_rows(q, cs[q], sn[q]);
+    }
+  }
+  float* ep = reinterpret_cast<float*>(smem);
+  const int half = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < NH; ++j) {
+    // columns [j*128, j*128+128) of the tile; wave columns [wn*TN, +TN)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int col = wn * kTN + nb * 32;  // first column of this 32-wide block
+      if (col >= j * kHeadDim && col < (j + 1) * kHeadDim) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int row = wm * kTM + mb * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
+            ep[row * kEpiPitch + (col - j * kHeadDim) + c32] = acc[mb][nb][i];
+          }
+      }
+    }
+    __syncthreads();
+    const int head = ht * NH + j;
+    int proj, hh;
+    split_head(head, e.Hq, e.Hkv, proj, hh);
+#pragma unroll
+    for (int q = 0; q < kPasses; ++q) {
+      const int r0 = (tid >> 3) + q * kRowStep;
+      const int64_t t = m0 + r0;
+      const float* rowp = ep + r0 * kEpiPitch;
+      float lo[8], hi[8];
+#pragma unroll
+      for (int v = 0; v < 2; ++v) {
+        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(rowp + 8 * c8 + 4 * v);
+        const f32x4_t b = *reinterpret_cast<const f32x4_t*>(rowp + kHalfDim + 8 * c8 + 4 * v);
+        lo[4 * v] = a.x; lo[4 * v + 1] = a.y; lo[4 * v + 2] = a.z; lo[4 * v + 3] = a.w;
+        hi[4 * v] = b.x; hi[4 * v + 1] = b.y; hi[4 * v + 2] = b.z; hi[4 * v + 3] = b.w;
+      }
+      if (e.qkv && proj != 2) {
+        // RMSNorm over the head (fused_qkv_rope.py:98-100), then rotate-half RoPE (:102-118)
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += lo[i] * lo[i] + hi[i] * hi[i];
+        ss += __shfl_xor(ss, 1);
+        ss += __shfl_xor(ss, 2);
+        ss += __shfl_xor(ss, 4);
+        const float rms = rsqrtf(ss * (1.0f / float(kHeadDim)) + e.eps);
+        u32x4_t c2[2], s2[2];
+        if constexpr (kPreload) {
+          c2[0] = cs[q][0]; c2[1] = cs[q][1]; s2[0] = sn[q][0]; s2[1] = sn[q][1];
+        } else {
+          load_rows(q, c2, s2);
+        }
+        const u32x4_t* g = proj == 0 ? gq : gk;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int wd = i >> 1, sh = (i & 1) * 16;
+          const float x1n = lo[i] * rms * bf16_to_f32((g[0][wd] >> sh) & 0xFFFFu);
+          const float x2n = hi[i] * rms * bf16_to_f32((g[1][wd] >> sh) & 0xFFFFu);
+          const float co1 = bf16_to_f32((c2[0][wd] >> sh) & 0xFFFFu);
+          const float co2 = bf16_to_f32((c2[1][wd] >> sh) & 0xFFFFu);
+          const float si1 = bf16_to_f32((s2[0][wd] >> sh) & 0xFFFFu);
+          const float si2 = bf16_to_f32((s2[1][wd] >> sh) & 0xFFFFu);
+          lo[i] = x1n * co1 - x2n * si1;
+          hi[i] = x2n * co2 + x1n * si2;
+        }
+      }
+      if (t < p.M) {
+        u32x4_t o1, o2;
+        o1.x = pack_bf16x2(lo[0], lo[1]); o1.y = pack_bf16x2(lo[2], lo[3]);
+        o1.z = pack_bf16x2(lo[4], lo[5]); o1.w = pack_bf16x2(lo[6], lo[7]);
+        o2.x = pack_bf16x2(hi[0], hi[1]); o2.y = pack_bf16x2(hi[2], hi[3]);
+        o2.z = pack_bf16x2(hi[4], hi[5]); o2.w = pack_bf16x2(hi[6], hi[7]);
+        if (e.qkv) {
+          const int H = proj == 0 ? e.Hq : e.Hkv;
+          uint16_t* dst = (proj == 0 ? e.q : (proj == 1 ? e.k : e.v)) + (t * H + hh) * kHeadDim;
+          *reinterpret_cast<u32x4_t*>(dst + 8 * c8) = o1;
+          *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8) = o2;
+        } else {
+          const int64_t col0 = int64_t(head) * kHeadDim;  // plain GEMM output [M, N]
+          uint16_t* dst = e.out + t * e.N + col0;
+          if (col0 + 8 * c8 + 8 <= e.N) *reinterpret_cast<u32x4_t*>(dst + 8 * c8) = o1;
+          if (col0 + kHalfDim + 8 * c8 + 8 <= e.N) *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8) = o2;
+        }
+      }
+    }
+    __syncthreads();  // the next head reuses ep
+  }
+}
+
 template <int BM, int NH, int WM, int WN, int NS, int SBK>
 __global__ void __launch_bounds__(WM* WN * 64)
 tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
@@ -126,9 +257,6 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   // rows (a positions[] load in positions mode) is read now, under the main loop.
   constexpr int kRowStep = S::kThreads / 8;
   constexpr int kPasses = BM / kRowStep;
-  // gamma / cos / sin depend only on the token: with few rows per thread they are
-  // loaded once for all NH heads of the tile (16 VGPRs per row)
-  constexpr bool kPreload = kPasses <= 4;
   int32_t prow[kPasses];
 #pragma unroll
   for (int q = 0; q < kPasses; ++q) {
@@ -232,111 +360,7 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   if (g_tile_trace && tid == 0) g_tile_trace[blockIdx.x * 256 + 252] = __builtin_amdgcn_s_memrealtime();
 #endif
 
-  // ---- epilogue, one head at a time --------------------------------------------------
-  const int c8 = tid & 7;
-  u32x4_t gq[2] = {}, gk[2] = {}, cs[kPreload ? kPasses : 1][2] = {}, sn[kPreload ? kPasses : 1][2] = {};
-  auto load_rows = [&](int q, u32x4_t (&c2)[2], u32x4_t (&s2)[2]) {
-    const int64_t base = int64_t(prow[q]) * kHeadDim;
-    c2[0] = *reinterpret_cast<const u32x4_t*>(e.cos + base + 8 * c8);
-    c2[1] = *reinterpret_cast<const u32x4_t*>(e.cos + base + kHalfDim + 8 * c8);
-    s2[0] = *reinterpret_cast<const u32x4_t*>(e.sin + base + 8 * c8);
-    s2[1] = *reinterpret_cast<const u32x4_t*>(e.sin + base + kHalfDim + 8 * c8);
-  };
-  if (e.qkv) {
-    gq[0] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + 8 * c8);
-    gq[1] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + kHalfDim + 8 * c8);
-    gk[0] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + 8 * c8);
-    gk[1] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + kHalfDim + 8 * c8);
-    if constexpr (kPreload) {
-#pragma unroll
-      for (int q = 0; q < kPasses; ++q) load_rows(q, cs[q], sn[q]);
-    }
-  }
-  float* ep = reinterpret_cast<float*>(smem);
-  const int half = lane >> 5;
-#pragma unroll
-  for (int j = 0; j < NH; ++j) {
-    // columns [j*128, j*128+128) of the tile; wave columns [wn*TN, +TN)
-#pragma unroll
-    for (int nb = 0; nb < S::kNB; ++nb) {
-      const int col = wn * S::kTN + nb * 32;  // first column of this 32-wide block
-      if (col >= j * kHeadDim && col < (j + 1) * kHeadDim) {
-#pragma unroll
-        for (int mb = 0; mb < S::kMB; ++mb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int row = wm * S::kTM + mb * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
-            ep[row * kEpiPitch + (col - j * kHeadDim) + c32] = acc[mb][nb][i];
-          }
-      }
-    }
-    __syncthreads();
-    const int head = ht * NH + j;
-    int proj, hh;
-    split_head(head, e.Hq, e.Hkv, proj, hh);
-#pragma unroll
-    for (int q = 0; q < kPasses; ++q) {
-      const int r0 = (tid >> 3) + q * kRowStep;
-      const int64_t t = m0 + r0;
-      const float* rowp = ep + r0 * kEpiPitch;
-      float lo[8], hi[8];
-#pragma unroll
-      for (int v = 0; v < 2; ++v) {
-        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(rowp + 8 * c8 + 4 * v);
-        const f32x4_t b = *reinterpret_cast<const f32x4_t*>(rowp + kHalfDim + 8 * c8 + 4 * v);
-        lo[4 * v] = a.x; lo[4 * v + 1] = a.y; lo[4 * v + 2] = a.z; lo[4 * v + 3] = a.w;
-        hi[4 * v] = b.x; hi[4 * v + 1] = b.y; hi[4 * v + 2] = b.z; hi[4 * v + 3] = b.w;
-      }
-      if (e.qkv && proj != 2) {
-        // RMSNorm over the head (fused_qkv_rope.py:98-100), then rotate-half RoPE (:102-118)
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) ss += lo[i] * lo[i] + hi[i] * hi[i];
-        ss += __shfl_xor(ss, 1);
-        ss += __shfl_xor(ss, 2);
-        ss += __shfl_xor(ss, 4);
-        const float rms = rsqrtf(ss * (1.0f / float(kHeadDim)) + e.eps);
-        u32x4_t c2[2], s2[2];
-        if constexpr (kPreload) {
-          c2[0] = cs[q][0]; c2[1] = cs[q][1]; s2[0] = sn[q][0]; s2[1] = sn[q][1];
-        } else {
-          load_rows(q, c2, s2);
-        }
-        const u32x4_t* g = proj == 0 ? gq : gk;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int wd = i >> 1, sh = (i & 1) * 16;
-          const float x1n = lo[i] * rms * bf16_to_f32((g[0][wd] >> sh) & 0xFFFFu);
-          const float x2n = hi[i] * rms * bf16_to_f32((g[1][wd] >> sh) & 0xFFFFu);
-          const float co1 = bf16_to_f32((c2[0][wd] >> sh) & 0xFFFFu);
-          const float co2 = bf16_to_f32((c2[1][wd] >> sh) & 0xFFFFu);
-          const float si1 = bf16_to_f32((s2[0][wd] >> sh) & 0xFFFFu);
-          const float si2 = bf16_to_f32((s2[1][wd] >> sh) & 0xFFFFu);
-          lo[i] = x1n * co1 - x2n * si1;
-          hi[i] = x2n * co2 + x1n * si2;
-        }
-      }
-      if (t < p.M) {
-        u32x4_t o1, o2;
-        o1.x = pack_bf16x2(lo[0], lo[1]); o1.y = pack_bf16x2(lo[2], lo[3]);
-        o1.z = pack_bf16x2(lo[4], lo[5]); o1.w = pack_bf16x2(lo[6], lo[7]);
-        o2.x = pack_bf16x2(hi[0], hi[1]); o2.y = pack_bf16x2(hi[2], hi[3]);
-        o2.z = pack_bf16x2(hi[4], hi[5]); o2.w = pack_bf16x2(hi[6], hi[7]);
-        if (e.qkv) {
-          const int H = proj == 0 ? e.Hq : e.Hkv;
-          uint16_t* dst = (proj == 0 ? e.q : (proj == 1 ? e.k : e.v)) + (t * H + hh) * kHeadDim;
-          *reinterpret_cast<u32x4_t*>(dst + 8 * c8) = o1;
-          *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8) = o2;
-        } else {
-          const int64_t col0 = int64_t(head) * kHeadDim;  // plain GEMM output [M, N]
-          uint16_t* dst = e.out + t * e.N + col0;
-          if (col0 + 8 * c8 + 8 <= e.N) *reinterpret_cast<u32x4_t*>(dst + 8 * c8) = o1;
-          if (col0 + kHalfDim + 8 * c8 + 8 <= e.N) *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8) = o2;
-        }
-      }
-    }
-    __syncthreads();  // the next head reuses ep
-  }
+  tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, ht, m0, p, e, smem);
 #ifdef MQK_TILE_TRACE
   if (g_tile_trace && tid == 0) g_tile_trace[blockIdx.x * 256 + 253] = __builtin_amdgcn_s_memrealtime();
 #endif
@@ -350,6 +374,221 @@ hipError_t launch_dma(const ProblemArgs& p, const WeightArgs& w, const EpilogueA
   const int blocks = n_mt * (p.n_tiles / NH);
   hipLaunchKernelGGL((tile_dma_kernel<BM, NH, WM, WN, NS, SBK>), dim3(blocks), dim3(S::kThreads), 0, stream, p, w, e,
                      group_m < 1 ? 1 : group_m);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// W4A16: the same pipeline with int4 weights.  A stage (64 k) holds the x rows
+// (128-byte rows, as above), the packed weight words of its 8 k-groups
+// ([k-group][BN] int32, 512-byte runs per head), and the scale and packed zero
+// of every column (a stage lies inside one quantisation group: group % 64 == 0).
+// Everything is filled with direct L2 -> LDS loads; the weights are dequantised
+// ((q - z) * s in fp32, one bf16 rounding) from the LDS word right before the
+// MFMA.  Weights take a quarter of the bf16 bytes, so the ring is deeper.
+// ---------------------------------------------------------------------------
+template <int BM, int NH, int WM, int WN, int NS>
+struct W4Shape {
+  static constexpr int kBN = NH * kHeadDim;
+  static constexpr int kWaves = WM * WN;
+  static constexpr int kThreads = kWaves * 64;
+  static constexpr int kTM = BM / WM;
+  static constexpr int kTN = kBN / WN;
+  static constexpr int kMB = kTM / 32;
+  static constexpr int kNB = kTN / 32;
+  static constexpr int kABytes = BM * 128;            // x: BM rows x 64 k
+  static constexpr int kBBytes = 8 * kBN * 4;         // 8 k-groups x BN packed words
+  static constexpr int kSBytes = kBN * 2;             // scales of the stage's group
+  static constexpr int kZBytes = kBN / 2;             // zeros of the stage's group (nibbles)
+  static constexpr int kStageBytes = (kABytes + kBBytes + kSBytes + kZBytes + 1023) / 1024 * 1024;
+  static constexpr int kNA = BM / 8;                  // 1 KB loads: 8 x rows each
+  static constexpr int kNW = kBN / 32;                // 1 KB loads: two 512-byte (k-group, head) runs
+  static constexpr int kLoads = kNA + kNW + 2;        // + one for the scales, one for the zeros
+  static constexpr int kMaxPerWave = (kLoads + kWaves - 1) / kWaves;
+  static constexpr int kRingBytes = NS * kStageBytes;
+  static constexpr int kEpiBytes = BM * kEpiPitch * 4;
+  static constexpr int kLdsBytes = kRingBytes > kEpiBytes ? kRingBytes : kEpiBytes;
+  static_assert(kTM % 32 == 0 && kTN % 32 == 0, "wave tile");
+  static_assert(kBN / 8 <= 64 && kBN / 32 <= 64, "scale / zero load fits one instruction");
+  static_assert(NS >= 2 && NS <= 8 && kMaxPerWave * (NS - 2) <= 63, "stages");
+  static_assert(kLdsBytes <= 160 * 1024, "LDS");
+};
+
+template <int BM, int NH, int WM, int WN, int NS>
+__global__ void __launch_bounds__(WM* WN * 64)
+tile_dma_w4_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
+  using S = W4Shape<BM, NH, WM, WN, NS>;
+  constexpr int BN = S::kBN;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[S::kLdsBytes];
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WM;
+  const int wn = wave / WM;
+
+  // ---- tile coordinates (as the bf16 kernel) ------------------------------------------
+  const int n_mt = int((p.M + BM - 1) / BM);
+  const int n_ht = p.n_tiles / NH;
+  const int tile = xcd_tile_id(blockIdx.x, gridDim.x);
+  const int per_group = group_m * n_ht;
+  const int grp = tile / per_group;
+  const int first_m = grp * group_m;
+  const int gsz = min(group_m, n_mt - first_m);
+  const int rr = tile - grp * per_group;
+  const int mt = first_m + rr % gsz;
+  const int ht = rr / gsz;
+  const int64_t m0 = int64_t(mt) * BM;
+  const int64_t K = p.K;
+
+  constexpr int kRowStep = S::kThreads / 8;
+  constexpr int kPasses = BM / kRowStep;
+  int32_t prow[kPasses];
+#pragma unroll
+  for (int q = 0; q < kPasses; ++q) {
+    const int64_t t = m0 + (tid >> 3) + q * kRowStep;
+    prow[q] = (e.qkv && t < p.M) ? int32_t(rope_row(e.positions, t, e.S, e.cos_rows)) : 0;
+  }
+
+  // ---- load slots: slot g of a stage is issued by wave g % W --------------------------
+  // kind 0: x rows; 1: packed weights; 2: scales; 3: zeros.  Source of stage kt =
+  // base + step(kt) * stride, step = kt (kinds 0, 1) or the group index (2, 3).
+  const char* base[S::kMaxPerWave];
+  int64_t stride[S::kMaxPerWave];
+  uint32_t dst[S::kMaxPerWave];
+  int kind[S::kMaxPerWave];
+  bool active[S::kMaxPerWave];
+  const int nslots = (S::kLoads - wave + S::kWaves - 1) / S::kWaves;
+#pragma unroll
+  for (int i = 0; i < S::kMaxPerWave; ++i) {
+    const int g = wave + i * S::kWaves;
+    base[i] = nullptr;
+    stride[i] = 0;
+    dst[i] = 0;
+    kind[i] = 0;
+    active[i] = false;
+    if (g < S::kNA) {
+      const int row = 8 * g + (lane >> 3);
+      const int chunk = stage_slot<64>(row, lane & 7);
+      int64_t grow = m0 + row;
+      grow = grow < p.M ? grow : p.M - 1;  // rows past M re-read the last row; never stored
+      base[i] = reinterpret_cast<const char*>(p.x + grow * K + chunk * 8);
+      stride[i] = 128;
+      dst[i] = uint32_t(g * 1024);
+      active[i] = true;
+    } else if (g < S::kNA + S::kNW) {
+      const int sg = 2 * (g - S::kNA) + (lane >> 5);  // (k-group, head) run
+      const int kg = sg / NH, j = sg % NH;
+      int proj, hh;
+      split_head(ht * NH + j, e.Hq, e.Hkv, proj, hh);
+      const int64_t n = w.n_cols[proj];
+      base[i] = reinterpret_cast<const char*>(w.qw[proj] + kg * n + int64_t(hh) * kHeadDim + (lane & 31) * 4);
+      stride[i] = 8 * n * 4;
+      dst[i] = uint32_t(S::kABytes + (g - S::kNA) * 1024);
+      kind[i] = 1;
+      active[i] = true;
+    } else if (g == S::kNA + S::kNW) {
+      const int j = lane / 16;  // 16 lanes x 8 scales per head
+      if (j < NH) {
+        int proj, hh;
+        split_head(ht * NH + j, e.Hq, e.Hkv, proj, hh);
+        const int64_t n = w.n_cols[proj];
+        base[i] = reinterpret_cast<const char*>(static_cast<const uint16_t*>(w.sc[proj]) + int64_t(hh) * kHeadDim +
+                                                (lane % 16) * 8);
+        stride[i] = n * 2;
+        active[i] = true;
+      }
+      dst[i] = uint32_t(S::kABytes + S::kBBytes);
+      kind[i] = 2;
+    } else if (g == S::kNA + S::kNW + 1) {
+      const int j = lane / 4;  // 4 lanes x 32 zeros per head
+      if (j < NH) {
+        int proj, hh;
+        split_head(ht * NH + j, e.Hq, e.Hkv, proj, hh);
+        const int64_t n = w.n_cols[proj];
+        base[i] = reinterpret_cast<const char*>(w.qz[proj] + int64_t(hh) * (kHeadDim / 8) + (lane % 4) * 4);
+        stride[i] = (n / 8) * 4;
+        active[i] = true;
+      }
+      dst[i] = uint32_t(S::kABytes + S::kBBytes + S::kSBytes);
+      kind[i] = 3;
+    }
+  }
+  const int group = w.group;
+  auto issue = [&](int kt) {
+    const uint32_t sbase = lds0 + uint32_t((kt % NS) * S::kStageBytes);
+    const int64_t gstep = (int64_t(kt) * 64) / group;
+#pragma unroll
+    for (int i = 0; i < S::kMaxPerWave; ++i) {
+      if (i < nslots) {
+        const int64_t stp = kind[i] >= 2 ? gstep : int64_t(kt);
+        if (active[i]) dma16(base[i] + stp * stride[i], sbase + dst[i]);
+      }
+    }
+  };
+
+  f32x16_t acc[S::kMB][S::kNB];
+#pragma unroll
+  for (int mb = 0; mb < S::kMB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < S::kNB; ++nb) acc[mb][nb] = f32x16_t{};
+
+  const int c32 = lane & 31;
+  const int khalf = lane >> 5;
+  const bool fp16 = w.scale_fp16 != 0;
+  const int nkt = int(K / 64);
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nkt) issue(s);
+
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int ahead = min(NS - 2, nkt - 1 - kt);  // stages already issued after kt
+    wait_vm_n(ahead * nslots);
+    barrier();
+    if (kt + NS - 1 < nkt) issue(kt + NS - 1);
+    const unsigned char* st = smem + (kt % NS) * S::kStageBytes;
+    float scl[S::kNB], zro[S::kNB];
+#pragma unroll
+    for (int nb = 0; nb < S::kNB; ++nb) {
+      const int col = wn * S::kTN + nb * 32 + c32;
+      const uint32_t sraw = *reinterpret_cast<const uint16_t*>(st + S::kABytes + S::kBBytes + col * 2);
+      const uint32_t zw = *reinterpret_cast<const uint32_t*>(st + S::kABytes + S::kBBytes + S::kSBytes + (col / 8) * 4);
+      scl[nb] = fp16 ? f16_to_f32(sraw) : bf16_to_f32(sraw);
+      zro[nb] = float((zw >> ((col % 8) * 4)) & 0xFu);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int chunk = 2 * ks + khalf;  // x chunk == weight k-group of this lane
+      u32x4_t af[S::kMB], bf[S::kNB];
+#pragma unroll
+      for (int mb = 0; mb < S::kMB; ++mb) {
+        const int row = wm * S::kTM + mb * 32 + c32;
+        af[mb] = *reinterpret_cast<const u32x4_t*>(st + row * 128 + stage_slot<64>(row, chunk) * 16);
+      }
+#pragma unroll
+      for (int nb = 0; nb < S::kNB; ++nb) {
+        const int col = wn * S::kTN + nb * 32 + c32;
+        const uint32_t word = *reinterpret_cast<const uint32_t*>(st + S::kABytes + (chunk * BN + col) * 4);
+        bf[nb] = dequant_int4x8(word, zro[nb], scl[nb]);
+      }
+#pragma unroll
+      for (int mb = 0; mb < S::kMB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < S::kNB; ++nb) acc[mb][nb] = mfma_32x32x16(af[mb], bf[nb], acc[mb][nb]);
+    }
+  }
+  barrier();  // every wave is done with the ring; the epilogue reuses the LDS
+  tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, ht, m0, p, e, smem);
+}
+
+template <int BM, int NH, int WM, int WN, int NS>
+hipError_t launch_dma_w4(const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e, int group_m,
+                         hipStream_t stream) {
+  using S = W4Shape<BM, NH, WM, WN, NS>;
+  const int n_mt = int((p.M + BM - 1) / BM);
+  const int blocks = n_mt * (p.n_tiles / NH);
+  hipLaunchKernelGGL((tile_dma_w4_kernel<BM, NH, WM, WN, NS>), dim3(blocks), dim3(S::kThreads), 0, stream, p, w,
+                     e, group_m < 1 ? 1 : group_m);
   return hipGetLastError();
 }
 
@@ -367,6 +606,16 @@ hipError_t launch_tile_dma(int id, const ProblemArgs& p, const WeightArgs& w, co
     case 16: return launch_dma<128, 3, 2, 4, 2, 64>(p, w, e, group_m, stream);  // 128x384, 2 stages of 64 k
     case 17: return launch_dma<256, 2, 4, 2, 2, 64>(p, w, e, group_m, stream);  // 256x256, 2 stages of 64 k
     case 18: return launch_dma<256, 2, 2, 4, 2, 64>(p, w, e, group_m, stream);  // 256x256 (128x64 waves), 64 k
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_tile_dma_w4(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
+                              int group_m, hipStream_t stream) {
+  switch (id) {
+    case 30: return launch_dma_w4<128, 3, 2, 4, 4>(p, w, e, group_m, stream);  // 128x384, 4 stages
+    case 31: return launch_dma_w4<256, 2, 2, 4, 3>(p, w, e, group_m, stream);  // 256x256, 3 stages
+    case 32: return launch_dma_w4<128, 2, 2, 2, 4>(p, w, e, group_m, stream);  // 128x256, 4 waves
     default: return hipErrorInvalidValue;
   }
 }

@@ -317,15 +317,22 @@ def gptq_zero_fix(qzeros: np.ndarray) -> np.ndarray:
     return pack_int4(np.clip(unpack_int4(qzeros) + 1, 0, 15))
 
 
-def w4a16_gemm(x, qweight, scales_f32, qzeros, group_size: int = 128, dtype=np.float64):
-    """``x [M, K] @ dequant(...)`` (w4a16_gemm.py:194-247), unrounded."""
+def w4a16_gemm(x, qweight, scales_f32, qzeros, group_size: int = 128, dtype=np.float64,
+               round_weight: bool = False):
+    """``x [M, K] @ dequant(...)`` (w4a16_gemm.py:194-247), unrounded.
+
+    ``round_weight=True`` rounds the fp32 dequantised weight to bf16 first: the
+    numerics of an implementation that feeds bf16 matrix units (the reference's
+    fp32 ``tl.dot`` is itself a reduced-precision product on tensor cores)."""
     w = dequant(qweight, scales_f32, qzeros, group_size)
+    if round_weight:
+        w = round_bf16(w)
     return np.asarray(x, dtype=dtype) @ w.astype(dtype)
 
 
 def fused_qkv_rope_w4a16(x, qw, sc, qz, q_norm_w, k_norm_w, cos, sin, Hq, Hkv,
                          positions=None, group_size: int = 128, eps: float = DEFAULT_EPS,
-                         dtype=np.float64):
+                         dtype=np.float64, round_weight: bool = False):
     """W4A16 front (attention.py:102-109 / :136-148) with the norm kept in fp32.
 
     ``qw/sc/qz`` are 3-tuples (q, k, v projection) of packed weights, scale
@@ -335,7 +342,7 @@ def fused_qkv_rope_w4a16(x, qw, sc, qz, q_norm_w, k_norm_w, cos, sin, Hq, Hkv,
     B, S, H = x.shape
     D = int(np.asarray(q_norm_w).shape[0])
     x2d = x.reshape(B * S, H)
-    proj = [w4a16_gemm(x2d, qw[i], sc[i], qz[i], group_size, dtype) for i in range(3)]
+    proj = [w4a16_gemm(x2d, qw[i], sc[i], qz[i], group_size, dtype, round_weight) for i in range(3)]
     q = proj[0].reshape(B * S, Hq, D)
     k = proj[1].reshape(B * S, Hkv, D)
     v = proj[2].reshape(B * S, Hkv, D)
