@@ -78,3 +78,43 @@ def dequantize(qweight: Tensor, scales: Tensor, qzeros: Tensor, group_size: int 
 def gptq_zero_fix(qzeros: Tensor) -> Tensor:
     """GPTQ v1 stores ``z - 1``: add 1 and clamp to 0..15 (linear_w4a16.py:96-99)."""
     return pack_int4((unpack_int4(qzeros.to(torch.int32)) + 1).clamp(0, 15))
+
+
+# AutoAWQ ("GEMM" kernels) checkpoint layout: qweight [K, N // 8] and qzeros
+# [K // g, N // 8] int32 packed along N, nibble i of a word holding column
+# 8*j + AWQ_ORDER[i] of its 8-column group; scales [K // g, N] fp16.
+AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
+
+
+def _unpack_awq_cols(packed: Tensor) -> Tensor:
+    """AutoAWQ words ``[R, N // 8]`` -> values ``[R, N]`` in natural column order."""
+    nib = unpack_int4(packed.to(torch.int32))            # [R, N], nibble order
+    R, N = nib.shape
+    nib = nib.view(R, N // 8, 8)
+    out = torch.empty_like(nib)
+    for i, c in enumerate(AWQ_ORDER):
+        out[:, :, c] = nib[:, :, i]
+    return out.view(R, N)
+
+
+def from_autoawq(qweight: Tensor, qzeros: Tensor, scales: Tensor):
+    """Repack an AutoAWQ checkpoint tensor triple into this package's int4 format.
+
+    AutoAWQ packs along N with the nibble order ``AWQ_ORDER``; this format packs
+    qweight along K in natural order (packing.py:11-24) and qzeros along N in
+    natural order.  The integer values and the scales are unchanged, so the
+    dequantised weight is identical.  Returns ``(qweight [K//8, N], scales
+    [K//g, N] (dtype kept), qzeros [K//g, N//8])``.
+    """
+    K, n8 = qweight.shape
+    N = n8 * 8
+    if qzeros.shape[1] != n8 or scales.shape[1] != N or scales.shape[0] != qzeros.shape[0]:
+        raise ValueError(f"inconsistent AutoAWQ shapes: qweight {tuple(qweight.shape)}, "
+                         f"qzeros {tuple(qzeros.shape)}, scales {tuple(scales.shape)}")
+    if K % 8 != 0:
+        raise ValueError(f"K={K} must be a multiple of 8")
+    w = _unpack_awq_cols(qweight)                         # [K, N]
+    z = _unpack_awq_cols(qzeros)                          # [K//g, N]
+    new_qweight = pack_int4(w.T.contiguous()).T.contiguous()
+    new_qzeros = pack_int4(z)
+    return new_qweight, scales, new_qzeros

@@ -26,7 +26,7 @@ import torch.nn as nn
 
 from . import _native
 from .fused_qkv_rope import EPS, _positions, _require, _rope_tables
-from .quantization import gptq_zero_fix, per_group_minmax_quantize
+from .quantization import from_autoawq, gptq_zero_fix, per_group_minmax_quantize
 
 
 def _scale_type(scales: torch.Tensor) -> int:
@@ -121,6 +121,20 @@ class LinearW4A16(nn.Module):
         layer.qweight.copy_(qweight.to(torch.int32))
         layer.scales.copy_(scales.to(torch.bfloat16))
         layer.qzeros.copy_(gptq_zero_fix(qzeros) if zero_plus_one else qzeros.to(torch.int32))
+        return layer
+
+    @classmethod
+    def from_autoawq(cls, qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
+                     group_size: int = 128) -> "LinearW4A16":
+        """Build from an AutoAWQ checkpoint (qweight [K, N/8] packed along N with the
+        AWQ nibble order, fp16 scales).  The values are repacked, not requantised;
+        the fp16 scales are kept (the kernels read fp16 or bf16 scales)."""
+        qw, sc, qz = from_autoawq(qweight, qzeros, scales)
+        K, N = qw.shape[0] * 8, qw.shape[1]
+        layer = cls(K, N, group_size, scale_dtype=sc.dtype).to(qw.device)
+        layer.qweight.copy_(qw)
+        layer.scales.copy_(sc)
+        layer.qzeros.copy_(qz)
         return layer
 
     def extra_repr(self) -> str:

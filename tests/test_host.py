@@ -244,3 +244,41 @@ def test_torch_gptq_fix_matches_oracle():
     z = np.random.default_rng(3).integers(0, 16, (4, 32))
     pz = orc.pack_int4(z)
     assert np.array_equal(mqk.gptq_zero_fix(torch.from_numpy(pz)).numpy(), orc.gptq_zero_fix(pz))
+
+
+# ── AutoAWQ ingest (format conversion, exact) ─────────────────────────────────
+
+def test_autoawq_known_answer():
+    """One 8-column group with column c holding value c: AutoAWQ packs nibble i =
+    column AWQ_ORDER[i] = (0,2,4,6,1,3,5,7)[i], i.e. the word 0x75316420."""
+    import mqk
+    word = torch.tensor([[0x75316420]], dtype=torch.int32).repeat(8, 1)   # K = 8 rows, N = 8
+    zeros = torch.tensor([[0x75316420]], dtype=torch.int32)                # one group
+    scales = torch.full((1, 8), 0.5, dtype=torch.float16)
+    qw, sc, qz = mqk.from_autoawq(word, zeros, scales)
+    w = mqk.unpack_int4(qw.T.contiguous()).T                               # [K, N]
+    assert torch.equal(w, torch.arange(8, dtype=torch.int32).repeat(8, 1))
+    assert torch.equal(mqk.unpack_int4(qz), torch.arange(8, dtype=torch.int32)[None])
+    assert sc.dtype == torch.float16 and torch.equal(sc, scales)
+
+
+def test_autoawq_roundtrip_dequant_equal():
+    """Repacking keeps every integer: dequant of the repacked triple equals the
+    dequant read directly from the AutoAWQ words."""
+    import mqk
+    from mqk.quantization import AWQ_ORDER
+    rng = np.random.default_rng(5)
+    K, N, g = 256, 64, 128
+    W = rng.integers(0, 16, (K, N))
+    Z = rng.integers(0, 16, (K // g, N))
+    def awq_pack(v):                     # independent restatement of the AutoAWQ packer
+        out = np.zeros((v.shape[0], v.shape[1] // 8), dtype=np.uint32)
+        for col in range(v.shape[1] // 8):
+            for i, c in enumerate(AWQ_ORDER):
+                out[:, col] |= (v[:, col * 8 + c].astype(np.uint32) << np.uint32(4 * i))
+        return torch.from_numpy(out.view(np.int32))
+    s = torch.from_numpy(rng.uniform(0.01, 0.02, (K // g, N)).astype(np.float16))
+    qw, sc, qz = mqk.from_autoawq(awq_pack(W), awq_pack(Z), s)
+    deq = mqk.dequantize(qw, sc, qz, g).numpy()
+    ref = (W - np.repeat(Z, g, axis=0)).astype(np.float32) * np.repeat(s.float().numpy(), g, axis=0)
+    np.testing.assert_array_equal(deq, ref)
