@@ -18,6 +18,8 @@
  *   mqk_w4a16_gemm            <- w4a16_gemm()          mini_qwen/kernels/w4a16_gemm.py:194-247
  *   mqk_fused_qkv_rope_w4a16  <- the W4A16 attention front (3x LinearW4A16 + RMSNorm + RoPE),
  *                                mini_qwen/model/layers/attention.py:102-109 (prefill), :136-148 (decode)
+ *   mqk_fused_qkv_rope_paged_* <- the above + the paged KV-cache scatter, write_kv_decode /
+ *                                _write_kv_cache_kernel (mini_qwen/kernels/paged_attn_prefill.py:27-56, :232-254)
  */
 #ifndef MQK_H_
 #define MQK_H_
@@ -134,6 +136,53 @@ int mqk_fused_qkv_rope_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void*
                              int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
                              int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
                              void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Paged KV cache destination of the fused ops below: K and V rows are also written
+ * into the caches of mini_qwen/cache/kv_cache.py:3-6 (both [num_blocks, block_size,
+ * Hkv, D] bf16).  Token t belongs to sequence kv_seq[t] (NULL: t / S) at position
+ * kv_pos[t] (NULL: t % S) and lands in block block_table[seq * bt_cols + pos /
+ * block_size], slot pos % block_size -- the addressing of the reference's
+ * _write_kv_cache_kernel (mini_qwen/kernels/paged_attn_prefill.py:27-56).  Entries
+ * whose sequence, page or block falls outside the given table are skipped.
+ */
+typedef struct mqk_paged_kv {
+  mqk_bf16* k_cache;            /* [num_blocks, block_size, Hkv, D], 16-byte aligned */
+  mqk_bf16* v_cache;
+  const int32_t* block_table;   /* [bt_rows, bt_cols] int32 */
+  int64_t bt_rows;
+  int64_t bt_cols;
+  int64_t num_blocks;
+  int32_t block_size;           /* the reference fixes 16 */
+  const int32_t* kv_seq;        /* [T] or NULL (required when positions != NULL) */
+  const int32_t* kv_pos;        /* [T] or NULL (required when positions != NULL) */
+} mqk_paged_kv;
+
+/*
+ * mqk_fused_qkv_rope_bf16 / _w4a16 that also write K and V into a paged KV cache,
+ * fusing the reference's separate scatter (write_kv_decode, paged_attn_prefill.py
+ * :232-254, and the scatter at :203-213) into the projection epilogue.  k and v
+ * may be NULL to write the cache only (the decode step, whose attention reads
+ * the cache).  Everything else as the unpaged entry points.
+ */
+int mqk_fused_qkv_rope_paged_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
+                                  const mqk_bf16* w_v, const mqk_bf16* q_gamma,
+                                  const mqk_bf16* k_gamma, const mqk_bf16* cos, const mqk_bf16* sin,
+                                  const int32_t* positions, int64_t T, int64_t S, int64_t hidden,
+                                  int Hq, int Hkv, int D, int64_t cos_rows, float eps, mqk_bf16* q,
+                                  mqk_bf16* k, mqk_bf16* v, const mqk_paged_kv* kv, void* workspace,
+                                  size_t ws_bytes, void* stream);
+
+int mqk_fused_qkv_rope_paged_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void* sc_q,
+                                   const int32_t* qz_q, const int32_t* qw_k, const void* sc_k,
+                                   const int32_t* qz_k, const int32_t* qw_v, const void* sc_v,
+                                   const int32_t* qz_v, int group, int scale_type,
+                                   const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                                   const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                                   int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                                   int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                                   const mqk_paged_kv* kv, void* workspace, size_t ws_bytes,
+                                   void* stream);
 
 /*
  * Process-wide tuning knobs (used by benchmarks and tests; defaults are

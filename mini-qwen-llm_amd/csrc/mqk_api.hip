@@ -145,7 +145,8 @@ size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hid
 }
 
 static int validate_fused_common(const mqk_bf16* x, int64_t T, int64_t S, int64_t hidden, int Hq,
-                                 int Hkv, int D, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v) {
+                                 int Hkv, int D, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                                 bool kv_optional = false) {
   if (T < 0 || hidden <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0)
     return fail(MQK_ERR_BAD_SHAPE, "need T >= 0, hidden > 0, Hq > 0, Hkv > 0, D > 0");
   if (D % 2 != 0) return fail(MQK_ERR_BAD_SHAPE, "head_dim must be even (RoPE rotate_half), got %d", D);
@@ -156,19 +157,47 @@ static int validate_fused_common(const mqk_bf16* x, int64_t T, int64_t S, int64_
   if (T > (int64_t(1) << 31) / 2) return fail(MQK_ERR_UNSUPPORTED, "T too large");
   (void)S;
   if (T == 0) return MQK_OK;
-  if (!x || !q || !k || !v) return fail(MQK_ERR_NULL_POINTER, "x/q/k/v must be non-NULL");
+  if (!x || !q) return fail(MQK_ERR_NULL_POINTER, "x/q must be non-NULL");
+  if (!kv_optional && (!k || !v)) return fail(MQK_ERR_NULL_POINTER, "x/q/k/v must be non-NULL");
   if (!aligned16(x) || !aligned16(q) || !aligned16(k) || !aligned16(v))
     return fail(MQK_ERR_MISALIGNED, "x/q/k/v must be 16-byte aligned");
   return MQK_OK;
 }
 
-int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
-                            const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
-                            const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
-                            int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
-                            int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
-                            void* workspace, size_t ws_bytes, void* stream) {
-  int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v);
+// Paged-KV-cache arguments -> epilogue fields (kv == NULL: no cache).
+static int apply_paged(const mqk_paged_kv* kv, const int32_t* positions, int64_t S, int64_t T,
+                       EpilogueArgs& e) {
+  if (!kv) return MQK_OK;
+  if (!kv->k_cache || !kv->v_cache || !kv->block_table)
+    return fail(MQK_ERR_NULL_POINTER, "paged kv: k_cache/v_cache/block_table must be non-NULL");
+  if (!aligned16(kv->k_cache) || !aligned16(kv->v_cache))
+    return fail(MQK_ERR_MISALIGNED, "paged kv: caches must be 16-byte aligned");
+  if (kv->block_size < 1 || kv->bt_rows < 1 || kv->bt_cols < 1 || kv->num_blocks < 1)
+    return fail(MQK_ERR_BAD_SHAPE, "paged kv: block_size, bt_rows, bt_cols, num_blocks must be >= 1");
+  if (positions && (!kv->kv_seq || !kv->kv_pos))
+    return fail(MQK_ERR_NULL_POINTER, "paged kv: positions mode needs kv_seq and kv_pos");
+  if (!positions && S <= 0) return fail(MQK_ERR_BAD_SHAPE, "paged kv: S must be > 0");
+  (void)T;
+  e.k_cache = kv->k_cache;
+  e.v_cache = kv->v_cache;
+  e.block_table = kv->block_table;
+  e.kv_seq = kv->kv_seq;
+  e.kv_pos = kv->kv_pos;
+  e.bt_rows = kv->bt_rows;
+  e.bt_cols = kv->bt_cols;
+  e.num_blocks = kv->num_blocks;
+  e.kv_len = positions ? 1 : S;
+  e.block_size = kv->block_size;
+  return MQK_OK;
+}
+
+static int fused_bf16_impl(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
+                           const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                           const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                           int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                           int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                           const mqk_paged_kv* kv, void* workspace, size_t ws_bytes, void* stream) {
+  int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v, kv != nullptr);
   if (st != MQK_OK) return st;
   if (T == 0) return ok();
   if (!w_q || !w_k || !w_v) return fail(MQK_ERR_NULL_POINTER, "w_q/w_k/w_v must be non-NULL");
@@ -184,9 +213,32 @@ int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
   w.w[2] = w_v;
   w.n_cols[0] = int64_t(Hq) * kHeadDim;
   w.n_cols[1] = w.n_cols[2] = int64_t(Hkv) * kHeadDim;
-  const EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
-                                           q, k, v, Hq, Hkv);
+  EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
+                                     q, k, v, Hq, Hkv);
+  if ((st = apply_paged(kv, positions, S, T, e)) != MQK_OK) return st;
   return run_fused(0, p, w, e, workspace, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
+                            const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                            const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                            int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                            int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                            void* workspace, size_t ws_bytes, void* stream) {
+  return fused_bf16_impl(x, w_q, w_k, w_v, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D,
+                         cos_rows, eps, q, k, v, nullptr, workspace, ws_bytes, stream);
+}
+
+int mqk_fused_qkv_rope_paged_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
+                                  const mqk_bf16* w_v, const mqk_bf16* q_gamma,
+                                  const mqk_bf16* k_gamma, const mqk_bf16* cos, const mqk_bf16* sin,
+                                  const int32_t* positions, int64_t T, int64_t S, int64_t hidden,
+                                  int Hq, int Hkv, int D, int64_t cos_rows, float eps, mqk_bf16* q,
+                                  mqk_bf16* k, mqk_bf16* v, const mqk_paged_kv* kv, void* workspace,
+                                  size_t ws_bytes, void* stream) {
+  if (!kv) return fail(MQK_ERR_NULL_POINTER, "paged kv descriptor is NULL");
+  return fused_bf16_impl(x, w_q, w_k, w_v, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D,
+                         cos_rows, eps, q, k, v, kv, workspace, ws_bytes, stream);
 }
 
 int mqk_qk_norm_rope_bf16(const mqk_bf16* q_raw, const mqk_bf16* k_raw, const mqk_bf16* q_gamma,
@@ -256,16 +308,16 @@ int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales
                     "w4a16 tile kernel launch");
 }
 
-int mqk_fused_qkv_rope_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void* sc_q,
-                             const int32_t* qz_q, const int32_t* qw_k, const void* sc_k,
-                             const int32_t* qz_k, const int32_t* qw_v, const void* sc_v,
-                             const int32_t* qz_v, int group, int scale_type,
-                             const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
-                             const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
-                             int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
-                             int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
-                             void* workspace, size_t ws_bytes, void* stream) {
-  int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v);
+static int fused_w4a16_impl(const mqk_bf16* x, const int32_t* qw_q, const void* sc_q,
+                            const int32_t* qz_q, const int32_t* qw_k, const void* sc_k,
+                            const int32_t* qz_k, const int32_t* qw_v, const void* sc_v,
+                            const int32_t* qz_v, int group, int scale_type,
+                            const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                            const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                            int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                            int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                            const mqk_paged_kv* kv, void* workspace, size_t ws_bytes, void* stream) {
+  int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v, kv != nullptr);
   if (st != MQK_OK) return st;
   if (T == 0) return ok();
   const int64_t nq = int64_t(Hq) * kHeadDim, nkv = int64_t(Hkv) * kHeadDim;
@@ -289,9 +341,40 @@ int mqk_fused_qkv_rope_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void*
   w.n_cols[1] = w.n_cols[2] = nkv;
   w.group = group;
   w.scale_fp16 = scale_type == MQK_SCALE_FP16;
-  const EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
-                                           q, k, v, Hq, Hkv);
+  EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
+                                     q, k, v, Hq, Hkv);
+  if ((st = apply_paged(kv, positions, S, T, e)) != MQK_OK) return st;
   return run_fused(1, p, w, e, workspace, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+int mqk_fused_qkv_rope_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void* sc_q,
+                             const int32_t* qz_q, const int32_t* qw_k, const void* sc_k,
+                             const int32_t* qz_k, const int32_t* qw_v, const void* sc_v,
+                             const int32_t* qz_v, int group, int scale_type,
+                             const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                             const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                             int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                             int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                             void* workspace, size_t ws_bytes, void* stream) {
+  return fused_w4a16_impl(x, qw_q, sc_q, qz_q, qw_k, sc_k, qz_k, qw_v, sc_v, qz_v, group, scale_type, q_gamma,
+                          k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D, cos_rows, eps, q, k, v, nullptr,
+                          workspace, ws_bytes, stream);
+}
+
+int mqk_fused_qkv_rope_paged_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void* sc_q,
+                                   const int32_t* qz_q, const int32_t* qw_k, const void* sc_k,
+                                   const int32_t* qz_k, const int32_t* qw_v, const void* sc_v,
+                                   const int32_t* qz_v, int group, int scale_type,
+                                   const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                                   const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                                   int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                                   int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                                   const mqk_paged_kv* kv, void* workspace, size_t ws_bytes,
+                                   void* stream) {
+  if (!kv) return fail(MQK_ERR_NULL_POINTER, "paged kv descriptor is NULL");
+  return fused_w4a16_impl(x, qw_q, sc_q, qz_q, qw_k, sc_k, qz_k, qw_v, sc_v, qz_v, group, scale_type, q_gamma,
+                          k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D, cos_rows, eps, q, k, v, kv,
+                          workspace, ws_bytes, stream);
 }
 
 int mqk_set_option(const char* name, int64_t value) {

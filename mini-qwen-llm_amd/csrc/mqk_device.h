@@ -94,6 +94,29 @@ __device__ __forceinline__ int64_t rope_row(const int32_t* __restrict__ position
   return p >= rows ? rows - 1 : p;
 }
 
+// Slot of token t in the paged KV cache (mini_qwen/kernels/paged_attn_prefill.py:45-50:
+// page = pos / block_size, slot = pos % block_size, block = block_table[seq][page]),
+// as block * block_size + slot, or -1 when there is no cache or the token's entry
+// is out of range (such rows are not written rather than written out of bounds).
+template <class E>
+__device__ __forceinline__ int64_t paged_slot(const E& e, int64_t t) {
+  if (!e.k_cache) return -1;
+  const int64_t seq = e.kv_seq ? int64_t(e.kv_seq[t]) : t / e.kv_len;
+  const int64_t pos = e.kv_pos ? int64_t(e.kv_pos[t]) : t % e.kv_len;
+  if (seq < 0 || seq >= e.bt_rows || pos < 0) return -1;
+  const int64_t page = pos / e.block_size;
+  if (page >= e.bt_cols) return -1;
+  const int64_t blk = e.block_table[seq * e.bt_cols + page];
+  if (blk < 0 || blk >= e.num_blocks) return -1;
+  return blk * e.block_size + pos % e.block_size;
+}
+
+// Cache row of head hh of projection proj (1 = K, 2 = V) for a slot from paged_slot.
+template <class E>
+__device__ __forceinline__ uint16_t* paged_row(const E& e, int64_t slot, int proj, int hh) {
+  return (proj == 1 ? e.k_cache : e.v_cache) + (slot * e.Hkv + hh) * kHeadDim;
+}
+
 // Which projection a 128-column tile belongs to: 0 = Q, 1 = K, 2 = V, and the
 // tile's head index inside that projection.
 __device__ __forceinline__ void split_head(int h, int Hq, int Hkv, int& proj, int& hh) {

@@ -40,6 +40,15 @@ struct EpilogueArgs {
   uint16_t* v;
   uint16_t* out;   // plain GEMM output
   int64_t N;       // plain GEMM width
+  // Paged KV cache (null k_cache: none).  K / V row of token t also goes to
+  // cache[(block * block_size + slot) * Hkv + head] (see paged_slot).
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  const int32_t* block_table;  // [bt_rows, bt_cols]
+  const int32_t* kv_seq;       // [T] or null: t / kv_len
+  const int32_t* kv_pos;       // [T] or null: t % kv_len
+  int64_t bt_rows, bt_cols, num_blocks, kv_len;
+  int block_size;
 };
 
 struct ProblemArgs {

@@ -322,6 +322,7 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   // RoPE table row of this thread's finisher row (tid / 8), read now: a
   // positions[] load here is off every critical path
   const int64_t prow = (proj != 2 && (tid >> 3) < M) ? rope_row(e.positions, tid >> 3, e.S, e.cos_rows) * kHeadDim : 0;
+  const int64_t cslot = (proj != 0 && (tid >> 3) < M) ? paged_slot(e, tid >> 3) : -1;  // paged-KV-cache slot
 
   int kt0, nk;
   split_range(split, splits, nkt, kt0, nk);
@@ -473,18 +474,26 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   }
   if (r < M) {
     const int H = proj == 0 ? e.Hq : e.Hkv;
-    uint16_t* dst = (proj == 0 ? e.q : (proj == 1 ? e.k : e.v)) + (int64_t(r) * H + hh) * kHeadDim;
-    u32x4_t o;
-    o.x = pack_bf16x2(lo[0], lo[1]);
-    o.y = pack_bf16x2(lo[2], lo[3]);
-    o.z = pack_bf16x2(lo[4], lo[5]);
-    o.w = pack_bf16x2(lo[6], lo[7]);
-    *reinterpret_cast<u32x4_t*>(dst + 8 * c) = o;
-    o.x = pack_bf16x2(hi[0], hi[1]);
-    o.y = pack_bf16x2(hi[2], hi[3]);
-    o.z = pack_bf16x2(hi[4], hi[5]);
-    o.w = pack_bf16x2(hi[6], hi[7]);
-    *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c) = o;
+    u32x4_t o1, o2;
+    o1.x = pack_bf16x2(lo[0], lo[1]);
+    o1.y = pack_bf16x2(lo[2], lo[3]);
+    o1.z = pack_bf16x2(lo[4], lo[5]);
+    o1.w = pack_bf16x2(lo[6], lo[7]);
+    o2.x = pack_bf16x2(hi[0], hi[1]);
+    o2.y = pack_bf16x2(hi[2], hi[3]);
+    o2.z = pack_bf16x2(hi[4], hi[5]);
+    o2.w = pack_bf16x2(hi[6], hi[7]);
+    uint16_t* base = proj == 0 ? e.q : (proj == 1 ? e.k : e.v);  // k / v may be null (cache only)
+    if (base) {
+      uint16_t* dst = base + (int64_t(r) * H + hh) * kHeadDim;
+      *reinterpret_cast<u32x4_t*>(dst + 8 * c) = o1;
+      *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c) = o2;
+    }
+    if (cslot >= 0) {
+      uint16_t* crow = paged_row(e, cslot, proj, hh);
+      *reinterpret_cast<u32x4_t*>(crow + 8 * c) = o1;
+      *reinterpret_cast<u32x4_t*>(crow + kHalfDim + 8 * c) = o2;
+    }
   }
   if (tid == 0) __hip_atomic_store(counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #ifdef MQK_DECODE_TRACE

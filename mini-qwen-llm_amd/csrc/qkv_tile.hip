@@ -80,9 +80,15 @@ __device__ __forceinline__ void store_block(const f32x16_t (&acc)[4], int64_t ro
     for (int i = 0; i < 16; ++i) {
       const int64_t t = row_base + 8 * (i >> 2) + 4 * half + (i & 3);
       if (t < p.M) {
-        uint16_t* o = dst + (t * H + hh) * kHeadDim + c32;
+        const int64_t cs = paged_slot(e, t);
+        uint16_t* o = dst ? dst + (t * H + hh) * kHeadDim + c32 : nullptr;  // v may be null (cache only)
+        uint16_t* oc = cs >= 0 ? paged_row(e, cs, proj, hh) + c32 : nullptr;
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) o[nb * 32] = f32_to_bf16(acc[nb][i]);
+        for (int nb = 0; nb < 4; ++nb) {
+          const uint16_t b = f32_to_bf16(acc[nb][i]);
+          if (o) o[nb * 32] = b;
+          if (oc) oc[nb * 32] = b;
+        }
       }
     }
     return;
@@ -111,7 +117,9 @@ __device__ __forceinline__ void store_block(const f32x16_t (&acc)[4], int64_t ro
     const int64_t t = row_base + 8 * (i >> 2) + 4 * half + (i & 3);
     if (t < p.M) {
       const int64_t prow = rope_row(e.positions, t, e.S, e.cos_rows) * kHeadDim;
-      uint16_t* o = dst + (t * H + hh) * kHeadDim;
+      const int64_t cs = proj == 1 ? paged_slot(e, t) : -1;
+      uint16_t* o = dst ? dst + (t * H + hh) * kHeadDim : nullptr;  // k may be null (cache only)
+      uint16_t* oc = cs >= 0 ? paged_row(e, cs, proj, hh) : nullptr;
 #pragma unroll
       for (int pr = 0; pr < 2; ++pr) {
         const int d = pr * 32 + c32;
@@ -121,8 +129,16 @@ __device__ __forceinline__ void store_block(const f32x16_t (&acc)[4], int64_t ro
         const float c2 = bf16_to_f32(e.cos[prow + d + kHalfDim]);
         const float s1 = bf16_to_f32(e.sin[prow + d]);
         const float s2 = bf16_to_f32(e.sin[prow + d + kHalfDim]);
-        o[d] = f32_to_bf16(x1n * c1 - x2n * s1);
-        o[d + kHalfDim] = f32_to_bf16(x2n * c2 + x1n * s2);
+        const uint16_t b1 = f32_to_bf16(x1n * c1 - x2n * s1);
+        const uint16_t b2 = f32_to_bf16(x2n * c2 + x1n * s2);
+        if (o) {
+          o[d] = b1;
+          o[d + kHalfDim] = b2;
+        }
+        if (oc) {
+          oc[d] = b1;
+          oc[d + kHalfDim] = b2;
+        }
       }
     }
   }

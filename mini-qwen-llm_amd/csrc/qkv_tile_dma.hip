@@ -99,11 +99,12 @@ __device__ __forceinline__ int stage_slot(int row, int chunk) {
 // then threads take 8-column pairs of a row (columns [8c, 8c+8) and
 // [64+8c, +8)), so the RMSNorm sum of squares is an 8-lane butterfly and every
 // RoPE pair is thread-local; each output row segment is written with 16-byte
-// stores.  prow[q] holds the RoPE table row of this thread's row (tid/8) + q*kRowStep.
+// stores.  prow[q] holds the RoPE table row of this thread's row (tid/8) + q*kRowStep,
+// cslot[q] its paged-KV-cache slot (-1: none).
 template <int BM, int NH, int WM, int WN, int THREADS, int MB, int NB>
-__device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], const int32_t* prow, int ht,
-                                              int64_t m0, const ProblemArgs& p, const EpilogueArgs& e,
-                                              unsigned char* smem) {
+__device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], const int32_t* prow,
+                                              const int64_t* cslot, int ht, int64_t m0, const ProblemArgs& p,
+                                              const EpilogueArgs& e, unsigned char* smem) {
   constexpr int kTM = BM / WM;
   constexpr int kTN = NH * kHeadDim / WN;
   constexpr int kRowStep = THREADS / 8;
@@ -209,9 +210,17 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
         o2.z = pack_bf16x2(hi[4], hi[5]); o2.w = pack_bf16x2(hi[6], hi[7]);
         if (e.qkv) {
           const int H = proj == 0 ? e.Hq : e.Hkv;
-          uint16_t* dst = (proj == 0 ? e.q : (proj == 1 ? e.k : e.v)) + (t * H + hh) * kHeadDim;
-          *reinterpret_cast<u32x4_t*>(dst + 8 * c8) = o1;
-          *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8) = o2;
+          uint16_t* base = proj == 0 ? e.q : (proj == 1 ? e.k : e.v);  // k / v may be null (cache only)
+          if (base) {
+            uint16_t* dst = base + (t * H + hh) * kHeadDim;
+            *reinterpret_cast<u32x4_t*>(dst + 8 * c8) = o1;
+            *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8) = o2;
+          }
+          if (proj != 0 && cslot[q] >= 0) {
+            uint16_t* crow = paged_row(e, cslot[q], proj, hh);
+            *reinterpret_cast<u32x4_t*>(crow + 8 * c8) = o1;
+            *reinterpret_cast<u32x4_t*>(crow + kHalfDim + 8 * c8) = o2;
+          }
         } else {
           const int64_t col0 = int64_t(head) * kHeadDim;  // plain GEMM output [M, N]
           uint16_t* dst = e.out + t * e.N + col0;
@@ -258,10 +267,12 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   constexpr int kRowStep = S::kThreads / 8;
   constexpr int kPasses = BM / kRowStep;
   int32_t prow[kPasses];
+  int64_t cslot[kPasses];  // paged-KV-cache slot of the row (-1: none)
 #pragma unroll
   for (int q = 0; q < kPasses; ++q) {
     const int64_t t = m0 + (tid >> 3) + q * kRowStep;
     prow[q] = (e.qkv && t < p.M) ? int32_t(rope_row(e.positions, t, e.S, e.cos_rows)) : 0;
+    cslot[q] = (e.qkv && t < p.M) ? paged_slot(e, t) : -1;
   }
   const int64_t K = p.K;
 
@@ -360,7 +371,7 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   if (g_tile_trace && tid == 0) g_tile_trace[blockIdx.x * 256 + 252] = __builtin_amdgcn_s_memrealtime();
 #endif
 
-  tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, ht, m0, p, e, smem);
+  tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, cslot, ht, m0, p, e, smem);
 #ifdef MQK_TILE_TRACE
   if (g_tile_trace && tid == 0) g_tile_trace[blockIdx.x * 256 + 253] = __builtin_amdgcn_s_memrealtime();
 #endif
@@ -444,10 +455,12 @@ tile_dma_w4_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   constexpr int kRowStep = S::kThreads / 8;
   constexpr int kPasses = BM / kRowStep;
   int32_t prow[kPasses];
+  int64_t cslot[kPasses];  // paged-KV-cache slot of the row (-1: none)
 #pragma unroll
   for (int q = 0; q < kPasses; ++q) {
     const int64_t t = m0 + (tid >> 3) + q * kRowStep;
     prow[q] = (e.qkv && t < p.M) ? int32_t(rope_row(e.positions, t, e.S, e.cos_rows)) : 0;
+    cslot[q] = (e.qkv && t < p.M) ? paged_slot(e, t) : -1;
   }
 
   // ---- load slots: slot g of a stage is issued by wave g % W --------------------------
@@ -578,7 +591,7 @@ tile_dma_w4_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
     }
   }
   barrier();  // every wave is done with the ring; the epilogue reuses the LDS
-  tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, ht, m0, p, e, smem);
+  tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, cslot, ht, m0, p, e, smem);
 }
 
 template <int BM, int NH, int WM, int WN, int NS>

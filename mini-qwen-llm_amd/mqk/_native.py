@@ -27,6 +27,23 @@ _I = ctypes.c_int
 _F = ctypes.c_float
 _SZ = ctypes.c_size_t
 
+class PagedKV(ctypes.Structure):
+    """struct mqk_paged_kv (include/mqk.h)."""
+    _fields_ = [
+        ("k_cache", ctypes.c_void_p),
+        ("v_cache", ctypes.c_void_p),
+        ("block_table", ctypes.c_void_p),
+        ("bt_rows", ctypes.c_int64),
+        ("bt_cols", ctypes.c_int64),
+        ("num_blocks", ctypes.c_int64),
+        ("block_size", ctypes.c_int32),
+        ("kv_seq", ctypes.c_void_p),
+        ("kv_pos", ctypes.c_void_p),
+    ]
+
+
+_KV = ctypes.POINTER(PagedKV)
+
 # name -> (restype, argtypes); mirrors include/mqk.h.
 SIGNATURES = {
     "mqk_version": (_I, []),
@@ -55,6 +72,20 @@ SIGNATURES = {
          _P, _P, _P, _P, _P,                      # q_gamma k_gamma cos sin positions
          _I64, _I64, _I64, _I, _I, _I,            # T S hidden Hq Hkv D
          _I64, _F, _P, _P, _P, _P, _SZ, _P],      # cos_rows eps q k v workspace ws_bytes stream
+    ),
+    "mqk_fused_qkv_rope_paged_bf16": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P,     # x w_q w_k w_v q_gamma k_gamma cos sin positions
+         _I64, _I64, _I64, _I, _I, _I,           # T S hidden Hq Hkv D
+         _I64, _F, _P, _P, _P, _KV, _P, _SZ, _P],  # cos_rows eps q k v kv workspace ws_bytes stream
+    ),
+    "mqk_fused_qkv_rope_paged_w4a16": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P,  # x, (qw, sc, qz) x 3
+         _I, _I,                                  # group scale_type
+         _P, _P, _P, _P, _P,                      # q_gamma k_gamma cos sin positions
+         _I64, _I64, _I64, _I, _I, _I,            # T S hidden Hq Hkv D
+         _I64, _F, _P, _P, _P, _KV, _P, _SZ, _P], # cos_rows eps q k v kv workspace ws_bytes stream
     ),
     "mqk_set_option": (_I, [ctypes.c_char_p, _I64]),
     "mqk_get_option": (_I64, [ctypes.c_char_p]),

@@ -30,6 +30,7 @@ Differences from the reference, all deliberate:
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional, Tuple
 
 import torch
@@ -123,6 +124,104 @@ def fused_qkv_rope(
         q.data_ptr(), k.data_ptr(), v.data_ptr(),
         _native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
     _native.check(status, "mqk_fused_qkv_rope_bf16")
+    return q, k, v
+
+
+def paged_kv(k_cache: torch.Tensor, v_cache: torch.Tensor, block_table: torch.Tensor,
+             kv_seq: Optional[torch.Tensor], kv_pos: Optional[torch.Tensor], T: int, H_KV: int, D: int,
+             device, positions: Optional[torch.Tensor]):
+    """Validated ``mqk_paged_kv`` descriptor and the tensors it points to (kept alive
+    by the caller for the duration of the launch).
+
+    Caches: ``[num_blocks, block_size, H_KV, D]`` bf16, contiguous (written in
+    place, so never copied).  ``block_table [rows, cols]`` int32.  ``kv_seq`` /
+    ``kv_pos`` ``[T]``: the token's sequence (row of block_table) and position in
+    it; both default to ``t // S`` and ``t % S`` and are required in positions mode.
+    """
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        if not isinstance(c, torch.Tensor) or c.device != device or c.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be a bf16 tensor on {device}")
+        if c.dim() != 4 or c.shape[2] != H_KV or c.shape[3] != D:
+            raise ValueError(f"{name} must be [num_blocks, block_size, {H_KV}, {D}], got {tuple(c.shape)}")
+        if not c.is_contiguous():
+            raise ValueError(f"{name} must be contiguous (it is written in place)")
+    if v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache and v_cache shapes differ")
+    if block_table.dtype not in (torch.int32, torch.int64) or block_table.dim() != 2:
+        raise TypeError("block_table must be a 2-D int32 tensor")
+    bt = _require(block_table, "block_table", device, dtype=None).to(torch.int32).contiguous()
+    if positions is not None and (kv_seq is None or kv_pos is None):
+        raise ValueError("positions mode needs kv_seq and kv_pos (the cache slot of each token)")
+    seq = None if kv_seq is None else _positions(kv_seq, T, device)
+    pos = None if kv_pos is None else _positions(kv_pos, T, device)
+    desc = _native.PagedKV(k_cache.data_ptr(), v_cache.data_ptr(), bt.data_ptr(), bt.shape[0], bt.shape[1],
+                           k_cache.shape[0], k_cache.shape[1], _native.ptr(seq), _native.ptr(pos))
+    return desc, (bt, seq, pos)
+
+
+def fused_qkv_rope_paged(
+    x: torch.Tensor,
+    w_q: torch.Tensor,
+    w_k: torch.Tensor,
+    w_v: torch.Tensor,
+    q_norm_w: torch.Tensor,
+    k_norm_w: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    positions: Optional[torch.Tensor] = None,
+    kv_seq: Optional[torch.Tensor] = None,
+    kv_pos: Optional[torch.Tensor] = None,
+    return_kv: bool = True,
+):
+    """:func:`fused_qkv_rope` that also writes K and V into a paged KV cache.
+
+    Fuses the reference's separate cache scatter (``write_kv_decode`` and the
+    prefill scatter, mini_qwen/kernels/paged_attn_prefill.py:27-56, :203-213,
+    :232-254) into the same kernel: the K/V rows are stored once to ``k``/``v``
+    (unless ``return_kv`` is False) and once to their cache slot.  Returns
+    ``(q, k, v)``, with ``k``/``v`` None when ``return_kv`` is False.
+    """
+    B, S, H = x.shape
+    D = q_norm_w.shape[0]
+    H_Q = w_q.shape[0] // D
+    H_KV = w_k.shape[0] // D
+    assert D % 2 == 0, "head_dim must be even (RoPE rotate_half)"
+    device = x.device
+    x = _require(x, "x", device)
+    w_q = _require(w_q, "w_q", device)
+    w_k = _require(w_k, "w_k", device)
+    w_v = _require(w_v, "w_v", device)
+    q_norm_w = _require(q_norm_w, "q_norm_w", device)
+    k_norm_w = _require(k_norm_w, "k_norm_w", device)
+    if w_q.shape != (H_Q * D, H) or w_k.shape != (H_KV * D, H) or w_v.shape != (H_KV * D, H):
+        raise ValueError(
+            f"weight shapes {tuple(w_q.shape)}, {tuple(w_k.shape)}, {tuple(w_v.shape)} do not match "
+            f"H_Q={H_Q}, H_KV={H_KV}, D={D}, hidden={H}")
+    cos, sin = _rope_tables(cos, sin, D, device)
+    T = B * S
+    pos = _positions(positions, T, device)
+    desc, keep = paged_kv(k_cache, v_cache, block_table, kv_seq, kv_pos, T, H_KV, D, device, positions)
+
+    q = torch.empty(B, S, H_Q, D, dtype=torch.bfloat16, device=device)
+    k = torch.empty(B, S, H_KV, D, dtype=torch.bfloat16, device=device) if return_kv else None
+    v = torch.empty(B, S, H_KV, D, dtype=torch.bfloat16, device=device) if return_kv else None
+    if T == 0:
+        return q, k, v
+    lib = _native.library()
+    stream = torch.cuda.current_stream(device)
+    nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, H_Q, H_KV, H))
+    ws = _native.workspace(device, stream, nbytes)
+    status = lib.mqk_fused_qkv_rope_paged_bf16(
+        x.data_ptr(), w_q.data_ptr(), w_k.data_ptr(), w_v.data_ptr(),
+        q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), _native.ptr(pos),
+        T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
+        q.data_ptr(), _native.ptr(k), _native.ptr(v), ctypes.byref(desc),
+        _native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
+    _native.check(status, "mqk_fused_qkv_rope_paged_bf16")
+    del keep
     return q, k, v
 
 

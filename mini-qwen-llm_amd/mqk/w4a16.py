@@ -19,13 +19,14 @@ kernels need K % 64 == 0 and group_size % 64 == 0.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional, Sequence, Tuple
 
 import torch
 import torch.nn as nn
 
 from . import _native
-from .fused_qkv_rope import EPS, _positions, _require, _rope_tables
+from .fused_qkv_rope import EPS, _positions, _require, _rope_tables, paged_kv
 from .quantization import from_autoawq, gptq_zero_fix, per_group_minmax_quantize
 
 
@@ -171,6 +172,35 @@ def fused_qkv_rope_w4a16(
     front rounds to bf16 before multiplying by the norm weight,
     rms_norm.py:15-18; the difference is below one bf16 ulp of the output).
     """
+    return _fused_w4a16(x, q_proj, k_proj, v_proj, q_norm_w, k_norm_w, cos, sin, positions, group_size)
+
+
+def fused_qkv_rope_w4a16_paged(
+    x: torch.Tensor,
+    q_proj,
+    k_proj,
+    v_proj,
+    q_norm_w: torch.Tensor,
+    k_norm_w: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    positions: Optional[torch.Tensor] = None,
+    kv_seq: Optional[torch.Tensor] = None,
+    kv_pos: Optional[torch.Tensor] = None,
+    return_kv: bool = True,
+    group_size: Optional[int] = None,
+):
+    """:func:`fused_qkv_rope_w4a16` that also writes K and V into a paged KV cache
+    (see :func:`mqk.fused_qkv_rope_paged`)."""
+    return _fused_w4a16(x, q_proj, k_proj, v_proj, q_norm_w, k_norm_w, cos, sin, positions, group_size,
+                        paged=(k_cache, v_cache, block_table, kv_seq, kv_pos), return_kv=return_kv)
+
+
+def _fused_w4a16(x, q_proj, k_proj, v_proj, q_norm_w, k_norm_w, cos, sin, positions, group_size,
+                 paged=None, return_kv=True):
     B, S, H = x.shape
     D = q_norm_w.shape[0]
     assert D % 2 == 0, "head_dim must be even (RoPE rotate_half)"
@@ -196,9 +226,12 @@ def fused_qkv_rope_w4a16(
     cos, sin = _rope_tables(cos, sin, D, device)
     T = B * S
     pos = _positions(positions, T, device)
+    desc = keep = None
+    if paged is not None:
+        desc, keep = paged_kv(*paged, T, H_KV, D, device, positions)
     q = torch.empty(B, S, H_Q, D, dtype=torch.bfloat16, device=device)
-    k = torch.empty(B, S, H_KV, D, dtype=torch.bfloat16, device=device)
-    v = torch.empty(B, S, H_KV, D, dtype=torch.bfloat16, device=device)
+    k = torch.empty(B, S, H_KV, D, dtype=torch.bfloat16, device=device) if return_kv else None
+    v = torch.empty(B, S, H_KV, D, dtype=torch.bfloat16, device=device) if return_kv else None
     if T == 0:
         return q, k, v
     lib = _native.library()
@@ -206,11 +239,16 @@ def fused_qkv_rope_w4a16(
     nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, H_Q, H_KV, H))
     ws = _native.workspace(device, stream, nbytes)
     flat = [t.data_ptr() for trio in parts for t in trio]
-    status = lib.mqk_fused_qkv_rope_w4a16(
-        x.data_ptr(), *flat, group_size, sts[0],
-        q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(),
-        _native.ptr(pos), T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
-        q.data_ptr(), k.data_ptr(), v.data_ptr(),
-        _native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
-    _native.check(status, "mqk_fused_qkv_rope_w4a16")
+    head = (x.data_ptr(), *flat, group_size, sts[0],
+            q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+            _native.ptr(pos), T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
+            q.data_ptr(), _native.ptr(k), _native.ptr(v))
+    tail = (_native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
+    if desc is None:
+        status = lib.mqk_fused_qkv_rope_w4a16(*head, *tail)
+        _native.check(status, "mqk_fused_qkv_rope_w4a16")
+    else:
+        status = lib.mqk_fused_qkv_rope_paged_w4a16(*head, ctypes.byref(desc), *tail)
+        _native.check(status, "mqk_fused_qkv_rope_paged_w4a16")
+    del keep
     return q, k, v

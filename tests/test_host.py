@@ -90,7 +90,8 @@ def _fused(lib, **kw):
     (dict(hidden=96), -3, "multiple of 64"),
     (dict(T=-1), -2, "T >= 0"),
     (dict(Hkv=0), -2, "Hkv > 0"),
-    (dict(x=None), -1, "x/q/k/v"),
+    (dict(x=None), -1, "x/q must"),
+    (dict(v=None), -1, "x/q/k/v"),
     (dict(w_v=None), -1, "w_q/w_k/w_v"),
     (dict(cos=None), -1, "cos"),
     (dict(q=(1 << 20) + 2), -4, "aligned"),
@@ -282,3 +283,28 @@ def test_autoawq_roundtrip_dequant_equal():
     deq = mqk.dequantize(qw, sc, qz, g).numpy()
     ref = (W - np.repeat(Z, g, axis=0)).astype(np.float32) * np.repeat(s.float().numpy(), g, axis=0)
     np.testing.assert_array_equal(deq, ref)
+
+
+def test_paged_validation(lib):
+    """mqk_fused_qkv_rope_paged_bf16 argument checks (fake pointers, never launched)."""
+    import ctypes
+    from mqk import _native
+    fake = 1 << 20
+
+    def call(kv, positions=None, T=100, k=fake):
+        return lib.mqk_fused_qkv_rope_paged_bf16(
+            fake, fake, fake, fake, fake, fake, fake, fake, positions, T, 100, 256, 2, 1, 128, 100, 1e-6,
+            fake, k, fake, kv, None, 0, None)
+
+    good = dict(k_cache=fake, v_cache=fake, block_table=fake, bt_rows=1, bt_cols=8, num_blocks=8,
+                block_size=16, kv_seq=None, kv_pos=None)
+    def desc(**kw):
+        d = dict(good); d.update(kw)
+        return ctypes.byref(_native.PagedKV(**d))
+    assert call(None) == -1 and "descriptor" in lib.mqk_last_error_detail().decode()
+    assert call(desc(k_cache=None)) == -1
+    assert call(desc(v_cache=fake + 8)) == -4
+    assert call(desc(block_size=0)) == -2
+    assert call(desc(), positions=fake) == -1
+    assert "kv_seq" in lib.mqk_last_error_detail().decode()
+    assert call(desc(), T=0) == 0
