@@ -20,6 +20,8 @@
  *                                mini_qwen/model/layers/attention.py:102-109 (prefill), :136-148 (decode)
  *   mqk_fused_qkv_rope_paged_* <- the above + the paged KV-cache scatter, write_kv_decode /
  *                                _write_kv_cache_kernel (mini_qwen/kernels/paged_attn_prefill.py:27-56, :232-254)
+ *   mqk_fused_qkv_rope_ex_*    <- the above + varlen (cu_seqlens) positions (paged_attn_prefill.py:188-199)
+ *                                and the decoder layer's input RMSNorm (qwen3.py:58-59, rms_norm.py:11-18)
  */
 #ifndef MQK_H_
 #define MQK_H_
@@ -183,6 +185,66 @@ int mqk_fused_qkv_rope_paged_w4a16(const mqk_bf16* x, const int32_t* qw_q, const
                                    int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
                                    const mqk_paged_kv* kv, void* workspace, size_t ws_bytes,
                                    void* stream);
+
+/*
+ * Optional features of the extended entry points below.  Zero-fill the struct and
+ * set what is used; an all-zero struct (or ext == NULL) gives the plain op.
+ *
+ * Varlen prefill (cu_seqlens != NULL; `positions` must then be NULL): the T
+ * tokens are n_seqs packed sequences, token t belonging to sequence s with
+ * cu_seqlens[s] <= t < cu_seqlens[s+1].  Its RoPE row, and its position in the
+ * paged KV cache, is t - cu_seqlens[s] + (seq_pos0 ? seq_pos0[s] : 0), and its
+ * block_table row is s -- the batch_ids / positions that paged_attn_prefill
+ * derives from cu_seqlens (mini_qwen/kernels/paged_attn_prefill.py:188-199).
+ * This lifts fused_qkv_rope's equal-length restriction (row t % S,
+ * fused_qkv_rope.py:109), so one call serves a whole continuous batch.
+ * cu_seqlens lives in device memory and is not read by the host: offsets that
+ * are not non-decreasing from 0 to T give unspecified rows (clamped into the
+ * table, never read or written out of bounds).
+ *
+ * Input RMSNorm (in_gamma != NULL): the projection input is
+ * in_gamma * bf16(x_fp32 * rsqrt(mean(x^2) + in_eps)), rounded to bf16 -- the
+ * decoder layer's input_layernorm (mini_qwen/model/layers/rms_norm.py:11-18,
+ * applied at mini_qwen/model/qwen3.py:58-59) computed inside the op, so the
+ * normalised activations never go to HBM.  The per-token scale is computed by a
+ * pre-pass into the workspace: size it with mqk_fused_qkv_rope_ex_workspace_size.
+ *
+ * kv != NULL: the paged KV-cache write of mqk_fused_qkv_rope_paged_* (in
+ * varlen mode kv_seq / kv_pos may be NULL: the sequence and position above).
+ */
+typedef struct mqk_fused_ext {
+  const int32_t* cu_seqlens;    /* [n_seqs + 1] int32, device memory, or NULL */
+  const int32_t* seq_pos0;      /* [n_seqs] position of each sequence's first token, or NULL (0) */
+  int64_t n_seqs;
+  const mqk_bf16* in_gamma;     /* [hidden] input RMSNorm weight, or NULL */
+  float in_eps;
+  const mqk_paged_kv* kv;       /* paged KV cache, or NULL */
+} mqk_fused_ext;
+
+/* Workspace bytes needed by the _ex entry points (the plain size plus the
+ * input-norm scales when ext->in_gamma is set). */
+size_t mqk_fused_qkv_rope_ex_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden,
+                                            const mqk_fused_ext* ext);
+
+/* mqk_fused_qkv_rope_bf16 / _w4a16 with the features of `ext` (NULL: none).  With
+ * ext->kv set, k and v may be NULL (cache only). */
+int mqk_fused_qkv_rope_ex_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
+                               const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                               const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                               int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                               int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                               const mqk_fused_ext* ext, void* workspace, size_t ws_bytes, void* stream);
+
+int mqk_fused_qkv_rope_ex_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void* sc_q,
+                                const int32_t* qz_q, const int32_t* qw_k, const void* sc_k,
+                                const int32_t* qz_k, const int32_t* qw_v, const void* sc_v,
+                                const int32_t* qz_v, int group, int scale_type,
+                                const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                                const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                                int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                                int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                                const mqk_fused_ext* ext, void* workspace, size_t ws_bytes,
+                                void* stream);
 
 /*
  * Process-wide tuning knobs (used by benchmarks and tests; defaults are

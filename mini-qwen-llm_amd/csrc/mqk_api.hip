@@ -35,6 +35,7 @@ int hip_status(hipError_t err, const char* what) {
 }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+size_t align_up(size_t n, size_t a) { return (n + a - 1) / a * a; }
 
 // Process-wide knobs (mqk_set_option).
 std::atomic<int64_t> g_prefill_tile{0};
@@ -46,11 +47,11 @@ constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace 
 
 // Shared validation of the position / table / gamma arguments.
 int check_rope_args(const void* q_gamma, const void* k_gamma, const void* cos, const void* sin,
-                    int64_t S, int64_t cos_rows, const int32_t* positions, float eps) {
+                    int64_t S, int64_t cos_rows, const int32_t* positions, float eps, bool varlen = false) {
   if (!q_gamma || !k_gamma || !cos || !sin)
     return fail(MQK_ERR_NULL_POINTER, "q_gamma/k_gamma/cos/sin must be non-NULL");
   if (cos_rows <= 0) return fail(MQK_ERR_BAD_SHAPE, "cos_rows must be > 0 (got %lld)", (long long)cos_rows);
-  if (!positions && S <= 0)
+  if (!positions && !varlen && S <= 0)
     return fail(MQK_ERR_BAD_SHAPE, "prefill mode (positions == NULL) needs S > 0 (got %lld)", (long long)S);
   if (!(eps >= 0.0f)) return fail(MQK_ERR_BAD_SHAPE, "eps must be >= 0");
   return MQK_OK;
@@ -144,6 +145,13 @@ size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hid
   return splits > 0 ? decode_workspace_bytes(tiles, splits) : 0;
 }
 
+size_t mqk_fused_qkv_rope_ex_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden,
+                                            const mqk_fused_ext* ext) {
+  size_t n = mqk_fused_qkv_rope_workspace_size(T, Hq, Hkv, hidden);
+  if (ext && ext->in_gamma && T > 0) n = align_up(n, 256) + align_up(size_t(T) * sizeof(float), 256);
+  return n;
+}
+
 static int validate_fused_common(const mqk_bf16* x, int64_t T, int64_t S, int64_t hidden, int Hq,
                                  int Hkv, int D, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
                                  bool kv_optional = false) {
@@ -166,7 +174,7 @@ static int validate_fused_common(const mqk_bf16* x, int64_t T, int64_t S, int64_
 
 // Paged-KV-cache arguments -> epilogue fields (kv == NULL: no cache).
 static int apply_paged(const mqk_paged_kv* kv, const int32_t* positions, int64_t S, int64_t T,
-                       EpilogueArgs& e) {
+                       bool varlen, EpilogueArgs& e) {
   if (!kv) return MQK_OK;
   if (!kv->k_cache || !kv->v_cache || !kv->block_table)
     return fail(MQK_ERR_NULL_POINTER, "paged kv: k_cache/v_cache/block_table must be non-NULL");
@@ -176,7 +184,7 @@ static int apply_paged(const mqk_paged_kv* kv, const int32_t* positions, int64_t
     return fail(MQK_ERR_BAD_SHAPE, "paged kv: block_size, bt_rows, bt_cols, num_blocks must be >= 1");
   if (positions && (!kv->kv_seq || !kv->kv_pos))
     return fail(MQK_ERR_NULL_POINTER, "paged kv: positions mode needs kv_seq and kv_pos");
-  if (!positions && S <= 0) return fail(MQK_ERR_BAD_SHAPE, "paged kv: S must be > 0");
+  if (!positions && !varlen && S <= 0) return fail(MQK_ERR_BAD_SHAPE, "paged kv: S must be > 0");
   (void)T;
   e.k_cache = kv->k_cache;
   e.v_cache = kv->v_cache;
@@ -186,9 +194,28 @@ static int apply_paged(const mqk_paged_kv* kv, const int32_t* positions, int64_t
   e.bt_rows = kv->bt_rows;
   e.bt_cols = kv->bt_cols;
   e.num_blocks = kv->num_blocks;
-  e.kv_len = positions ? 1 : S;
+  e.kv_len = (positions || varlen) ? 1 : S;
   e.block_size = kv->block_size;
   return MQK_OK;
+}
+
+// Optional features of the _ex entry points -> epilogue / problem fields.
+static int apply_ext(const mqk_fused_ext* ext, const int32_t* positions, int64_t S, int64_t T,
+                     EpilogueArgs& e) {
+  if (!ext) return MQK_OK;
+  const bool varlen = ext->cu_seqlens != nullptr;
+  if (varlen) {
+    if (positions) return fail(MQK_ERR_BAD_SHAPE, "varlen mode (cu_seqlens) and positions are exclusive");
+    if (ext->n_seqs < 1 || ext->n_seqs > (int64_t(1) << 30))
+      return fail(MQK_ERR_BAD_SHAPE, "varlen mode needs 1 <= n_seqs (got %lld)", (long long)ext->n_seqs);
+    e.cu_seqlens = ext->cu_seqlens;
+    e.seq_pos0 = ext->seq_pos0;
+    e.n_seqs = ext->n_seqs;
+  } else if (ext->seq_pos0) {
+    return fail(MQK_ERR_BAD_SHAPE, "seq_pos0 needs cu_seqlens");
+  }
+  if (ext->in_gamma) return fail(MQK_ERR_UNSUPPORTED, "input RMSNorm is not available yet");
+  return apply_paged(ext->kv, positions, S, T, varlen, e);
 }
 
 static int fused_bf16_impl(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
@@ -196,14 +223,15 @@ static int fused_bf16_impl(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf1
                            const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
                            int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
                            int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
-                           const mqk_paged_kv* kv, void* workspace, size_t ws_bytes, void* stream) {
-  int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v, kv != nullptr);
+                           const mqk_fused_ext* ext, void* workspace, size_t ws_bytes, void* stream) {
+  const bool varlen = ext && ext->cu_seqlens;
+  int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v, ext && ext->kv);
   if (st != MQK_OK) return st;
   if (T == 0) return ok();
   if (!w_q || !w_k || !w_v) return fail(MQK_ERR_NULL_POINTER, "w_q/w_k/w_v must be non-NULL");
   if (!aligned16(w_q) || !aligned16(w_k) || !aligned16(w_v))
     return fail(MQK_ERR_MISALIGNED, "weights must be 16-byte aligned");
-  st = check_rope_args(q_gamma, k_gamma, cos, sin, S, cos_rows, positions, eps);
+  st = check_rope_args(q_gamma, k_gamma, cos, sin, S, cos_rows, positions, eps, varlen);
   if (st != MQK_OK) return st;
 
   ProblemArgs p{x, T, hidden, Hq + 2 * Hkv};
@@ -215,7 +243,7 @@ static int fused_bf16_impl(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf1
   w.n_cols[1] = w.n_cols[2] = int64_t(Hkv) * kHeadDim;
   EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
                                      q, k, v, Hq, Hkv);
-  if ((st = apply_paged(kv, positions, S, T, e)) != MQK_OK) return st;
+  if ((st = apply_ext(ext, positions, S, T, e)) != MQK_OK) return st;
   return run_fused(0, p, w, e, workspace, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
@@ -237,8 +265,20 @@ int mqk_fused_qkv_rope_paged_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const 
                                   mqk_bf16* k, mqk_bf16* v, const mqk_paged_kv* kv, void* workspace,
                                   size_t ws_bytes, void* stream) {
   if (!kv) return fail(MQK_ERR_NULL_POINTER, "paged kv descriptor is NULL");
+  mqk_fused_ext ext{};
+  ext.kv = kv;
   return fused_bf16_impl(x, w_q, w_k, w_v, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D,
-                         cos_rows, eps, q, k, v, kv, workspace, ws_bytes, stream);
+                         cos_rows, eps, q, k, v, &ext, workspace, ws_bytes, stream);
+}
+
+int mqk_fused_qkv_rope_ex_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
+                               const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                               const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                               int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                               int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                               const mqk_fused_ext* ext, void* workspace, size_t ws_bytes, void* stream) {
+  return fused_bf16_impl(x, w_q, w_k, w_v, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D,
+                         cos_rows, eps, q, k, v, ext, workspace, ws_bytes, stream);
 }
 
 int mqk_qk_norm_rope_bf16(const mqk_bf16* q_raw, const mqk_bf16* k_raw, const mqk_bf16* q_gamma,
@@ -316,15 +356,16 @@ static int fused_w4a16_impl(const mqk_bf16* x, const int32_t* qw_q, const void* 
                             const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
                             int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
                             int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
-                            const mqk_paged_kv* kv, void* workspace, size_t ws_bytes, void* stream) {
-  int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v, kv != nullptr);
+                            const mqk_fused_ext* ext, void* workspace, size_t ws_bytes, void* stream) {
+  const bool varlen = ext && ext->cu_seqlens;
+  int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v, ext && ext->kv);
   if (st != MQK_OK) return st;
   if (T == 0) return ok();
   const int64_t nq = int64_t(Hq) * kHeadDim, nkv = int64_t(Hkv) * kHeadDim;
   if ((st = validate_int4(qw_q, sc_q, qz_q, hidden, nq, group, scale_type, "q_proj")) != MQK_OK) return st;
   if ((st = validate_int4(qw_k, sc_k, qz_k, hidden, nkv, group, scale_type, "k_proj")) != MQK_OK) return st;
   if ((st = validate_int4(qw_v, sc_v, qz_v, hidden, nkv, group, scale_type, "v_proj")) != MQK_OK) return st;
-  st = check_rope_args(q_gamma, k_gamma, cos, sin, S, cos_rows, positions, eps);
+  st = check_rope_args(q_gamma, k_gamma, cos, sin, S, cos_rows, positions, eps, varlen);
   if (st != MQK_OK) return st;
 
   ProblemArgs p{x, T, hidden, Hq + 2 * Hkv};
@@ -343,7 +384,7 @@ static int fused_w4a16_impl(const mqk_bf16* x, const int32_t* qw_q, const void* 
   w.scale_fp16 = scale_type == MQK_SCALE_FP16;
   EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
                                      q, k, v, Hq, Hkv);
-  if ((st = apply_paged(kv, positions, S, T, e)) != MQK_OK) return st;
+  if ((st = apply_ext(ext, positions, S, T, e)) != MQK_OK) return st;
   return run_fused(1, p, w, e, workspace, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
@@ -372,8 +413,25 @@ int mqk_fused_qkv_rope_paged_w4a16(const mqk_bf16* x, const int32_t* qw_q, const
                                    const mqk_paged_kv* kv, void* workspace, size_t ws_bytes,
                                    void* stream) {
   if (!kv) return fail(MQK_ERR_NULL_POINTER, "paged kv descriptor is NULL");
+  mqk_fused_ext ext{};
+  ext.kv = kv;
   return fused_w4a16_impl(x, qw_q, sc_q, qz_q, qw_k, sc_k, qz_k, qw_v, sc_v, qz_v, group, scale_type, q_gamma,
-                          k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D, cos_rows, eps, q, k, v, kv,
+                          k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D, cos_rows, eps, q, k, v, &ext,
+                          workspace, ws_bytes, stream);
+}
+
+int mqk_fused_qkv_rope_ex_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void* sc_q,
+                                const int32_t* qz_q, const int32_t* qw_k, const void* sc_k,
+                                const int32_t* qz_k, const int32_t* qw_v, const void* sc_v,
+                                const int32_t* qz_v, int group, int scale_type,
+                                const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                                const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                                int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                                int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                                const mqk_fused_ext* ext, void* workspace, size_t ws_bytes,
+                                void* stream) {
+  return fused_w4a16_impl(x, qw_q, sc_q, qz_q, qw_k, sc_k, qz_k, qw_v, sc_v, qz_v, group, scale_type, q_gamma,
+                          k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D, cos_rows, eps, q, k, v, ext,
                           workspace, ws_bytes, stream);
 }
 

@@ -85,13 +85,35 @@ __device__ __forceinline__ u32x4_t dequant_int4x8(uint32_t packed, float zero, f
   return r;
 }
 
-// Row of the RoPE table used by token t (reference fused_qkv_rope.py:106-111),
-// clamped into [0, rows).
-__device__ __forceinline__ int64_t rope_row(const int32_t* __restrict__ positions, int64_t t,
-                                            int64_t S, int64_t rows) {
-  int64_t p = positions ? static_cast<int64_t>(positions[t]) : (t % S);
+// Varlen mode: sequence s of token t (cu_seqlens[s] <= t < cu_seqlens[s+1]) by
+// binary search over the n_seqs + 1 offsets, and its position t - cu_seqlens[s]
+// (+ seq_pos0[s]) -- the batch_ids / positions of paged_attn_prefill.py:188-199.
+// Only offsets 0..n_seqs are read, whatever their values.
+template <class E>
+__device__ __forceinline__ void varlen_locate(const E& e, int64_t t, int64_t& seq, int64_t& pos) {
+  int64_t lo = 0, hi = e.n_seqs;
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (int64_t(e.cu_seqlens[mid]) <= t) lo = mid;
+    else hi = mid;
+  }
+  seq = lo;
+  pos = t - int64_t(e.cu_seqlens[lo]) + (e.seq_pos0 ? int64_t(e.seq_pos0[lo]) : 0);
+}
+
+// Row of the RoPE table used by token t, clamped into [0, rows): prefill t % S
+// (reference fused_qkv_rope.py:109), positions[t] (:107), or the varlen position.
+template <class E>
+__device__ __forceinline__ int64_t rope_row(const E& e, int64_t t) {
+  int64_t p;
+  if (e.cu_seqlens) {
+    int64_t s;
+    varlen_locate(e, t, s, p);
+  } else {
+    p = e.positions ? static_cast<int64_t>(e.positions[t]) : (t % e.S);
+  }
   p = p < 0 ? 0 : p;
-  return p >= rows ? rows - 1 : p;
+  return p >= e.cos_rows ? e.cos_rows - 1 : p;
 }
 
 // Slot of token t in the paged KV cache (mini_qwen/kernels/paged_attn_prefill.py:45-50:
@@ -101,8 +123,15 @@ __device__ __forceinline__ int64_t rope_row(const int32_t* __restrict__ position
 template <class E>
 __device__ __forceinline__ int64_t paged_slot(const E& e, int64_t t) {
   if (!e.k_cache) return -1;
-  const int64_t seq = e.kv_seq ? int64_t(e.kv_seq[t]) : t / e.kv_len;
-  const int64_t pos = e.kv_pos ? int64_t(e.kv_pos[t]) : t % e.kv_len;
+  int64_t seq, pos;
+  if (e.cu_seqlens && !(e.kv_seq && e.kv_pos)) {
+    varlen_locate(e, t, seq, pos);
+    if (e.kv_seq) seq = int64_t(e.kv_seq[t]);
+    if (e.kv_pos) pos = int64_t(e.kv_pos[t]);
+  } else {
+    seq = e.kv_seq ? int64_t(e.kv_seq[t]) : t / e.kv_len;
+    pos = e.kv_pos ? int64_t(e.kv_pos[t]) : t % e.kv_len;
+  }
   if (seq < 0 || seq >= e.bt_rows || pos < 0) return -1;
   const int64_t page = pos / e.block_size;
   if (page >= e.bt_cols) return -1;
@@ -114,7 +143,11 @@ __device__ __forceinline__ int64_t paged_slot(const E& e, int64_t t) {
 // Cache row of head hh of projection proj (1 = K, 2 = V) for a slot from paged_slot.
 template <class E>
 __device__ __forceinline__ uint16_t* paged_row(const E& e, int64_t slot, int proj, int hh) {
-  return (proj == 1 ? e.k_cache : e.v_cache) + (slot * e.Hkv + hh) * kHeadDim;
+  // arithmetic select of the two pointer values: a select of the two argument
+  // fields' addresses would make the compiler copy them to scratch memory
+  const uintptr_t kc = reinterpret_cast<uintptr_t>(e.k_cache), vc = reinterpret_cast<uintptr_t>(e.v_cache);
+  uint16_t* const cache = reinterpret_cast<uint16_t*>(vc + (kc - vc) * uintptr_t(proj == 1));
+  return cache + (slot * e.Hkv + hh) * kHeadDim;
 }
 
 // Which projection a 128-column tile belongs to: 0 = Q, 1 = K, 2 = V, and the

@@ -49,6 +49,12 @@ struct EpilogueArgs {
   const int32_t* kv_pos;       // [T] or null: t % kv_len
   int64_t bt_rows, bt_cols, num_blocks, kv_len;
   int block_size;
+  // Varlen mode (non-null cu_seqlens): token t is in sequence s with
+  // cu_seqlens[s] <= t < cu_seqlens[s+1], at position t - cu_seqlens[s] (+ seq_pos0[s]);
+  // that position selects its RoPE row and (with no kv_seq / kv_pos) its cache slot.
+  const int32_t* cu_seqlens;
+  const int32_t* seq_pos0;
+  int64_t n_seqs;
 };
 
 struct ProblemArgs {

@@ -37,7 +37,7 @@ norm_rope_kernel(const uint16_t* __restrict__ q_raw, const uint16_t* __restrict_
   const float rms = rsqrtf(ss * (1.0f / float(kHeadDim)) + e.eps);
   const float x1n = x1 * rms * bf16_to_f32(gamma[lane]);
   const float x2n = x2 * rms * bf16_to_f32(gamma[lane + kHalfDim]);
-  const int64_t prow = rope_row(e.positions, t, e.S, e.cos_rows) * kHeadDim;
+  const int64_t prow = rope_row(e, t) * kHeadDim;
   const float c1 = bf16_to_f32(e.cos[prow + lane]);
   const float c2 = bf16_to_f32(e.cos[prow + lane + kHalfDim]);
   const float s1 = bf16_to_f32(e.sin[prow + lane]);

@@ -321,7 +321,7 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
 
   // RoPE table row of this thread's finisher row (tid / 8), read now: a
   // positions[] load here is off every critical path
-  const int64_t prow = (proj != 2 && (tid >> 3) < M) ? rope_row(e.positions, tid >> 3, e.S, e.cos_rows) * kHeadDim : 0;
+  const int64_t prow = (proj != 2 && (tid >> 3) < M) ? rope_row(e, tid >> 3) * kHeadDim : 0;
   const int64_t cslot = (proj != 0 && (tid >> 3) < M) ? paged_slot(e, tid >> 3) : -1;  // paged-KV-cache slot
 
   int kt0, nk;

@@ -116,7 +116,7 @@ __device__ __forceinline__ void store_block(const f32x16_t (&acc)[4], int64_t ro
     const float rms = rsqrtf(ss * inv_d + e.eps);
     const int64_t t = row_base + 8 * (i >> 2) + 4 * half + (i & 3);
     if (t < p.M) {
-      const int64_t prow = rope_row(e.positions, t, e.S, e.cos_rows) * kHeadDim;
+      const int64_t prow = rope_row(e, t) * kHeadDim;
       const int64_t cs = proj == 1 ? paged_slot(e, t) : -1;
       uint16_t* o = dst ? dst + (t * H + hh) * kHeadDim : nullptr;  // k may be null (cache only)
       uint16_t* oc = cs >= 0 ? paged_row(e, cs, proj, hh) : nullptr;

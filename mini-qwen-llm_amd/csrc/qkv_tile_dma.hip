@@ -101,9 +101,9 @@ __device__ __forceinline__ int stage_slot(int row, int chunk) {
 // RoPE pair is thread-local; each output row segment is written with 16-byte
 // stores.  prow[q] holds the RoPE table row of this thread's row (tid/8) + q*kRowStep,
 // cslot[q] its paged-KV-cache slot (-1: none).
-template <int BM, int NH, int WM, int WN, int THREADS, int MB, int NB>
-__device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], const int32_t* prow,
-                                              const int64_t* cslot, int ht, int64_t m0, const ProblemArgs& p,
+template <int BM, int NH, int WM, int WN, int THREADS, int MB, int NB, class RowV, class SlotV>
+__device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], const RowV& prow,
+                                              const SlotV& cslot, int ht, int64_t m0, const ProblemArgs& p,
                                               const EpilogueArgs& e, unsigned char* smem) {
   constexpr int kTM = BM / WM;
   constexpr int kTN = NH * kHeadDim / WN;
@@ -266,12 +266,16 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   // rows (a positions[] load in positions mode) is read now, under the main loop.
   constexpr int kRowStep = S::kThreads / 8;
   constexpr int kPasses = BM / kRowStep;
-  int32_t prow[kPasses];
-  int64_t cslot[kPasses];  // paged-KV-cache slot of the row (-1: none)
+  // (vector types: indexed in registers even where the compiler merges the
+  // per-row code paths, where a plain array would go to scratch memory)
+  typedef int32_t RowV __attribute__((ext_vector_type(kPasses)));
+  typedef int64_t SlotV __attribute__((ext_vector_type(kPasses)));
+  RowV prow;
+  SlotV cslot;  // paged-KV-cache slot of the row (-1: none)
 #pragma unroll
   for (int q = 0; q < kPasses; ++q) {
     const int64_t t = m0 + (tid >> 3) + q * kRowStep;
-    prow[q] = (e.qkv && t < p.M) ? int32_t(rope_row(e.positions, t, e.S, e.cos_rows)) : 0;
+    prow[q] = (e.qkv && t < p.M) ? int32_t(rope_row(e, t)) : 0;
     cslot[q] = (e.qkv && t < p.M) ? paged_slot(e, t) : -1;
   }
   const int64_t K = p.K;
@@ -454,12 +458,16 @@ tile_dma_w4_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
 
   constexpr int kRowStep = S::kThreads / 8;
   constexpr int kPasses = BM / kRowStep;
-  int32_t prow[kPasses];
-  int64_t cslot[kPasses];  // paged-KV-cache slot of the row (-1: none)
+  // (vector types: indexed in registers even where the compiler merges the
+  // per-row code paths, where a plain array would go to scratch memory)
+  typedef int32_t RowV __attribute__((ext_vector_type(kPasses)));
+  typedef int64_t SlotV __attribute__((ext_vector_type(kPasses)));
+  RowV prow;
+  SlotV cslot;  // paged-KV-cache slot of the row (-1: none)
 #pragma unroll
   for (int q = 0; q < kPasses; ++q) {
     const int64_t t = m0 + (tid >> 3) + q * kRowStep;
-    prow[q] = (e.qkv && t < p.M) ? int32_t(rope_row(e.positions, t, e.S, e.cos_rows)) : 0;
+    prow[q] = (e.qkv && t < p.M) ? int32_t(rope_row(e, t)) : 0;
     cslot[q] = (e.qkv && t < p.M) ? paged_slot(e, t) : -1;
   }
 

@@ -44,6 +44,21 @@ class PagedKV(ctypes.Structure):
 
 _KV = ctypes.POINTER(PagedKV)
 
+
+class FusedExt(ctypes.Structure):
+    """struct mqk_fused_ext (include/mqk.h)."""
+    _fields_ = [
+        ("cu_seqlens", ctypes.c_void_p),
+        ("seq_pos0", ctypes.c_void_p),
+        ("n_seqs", ctypes.c_int64),
+        ("in_gamma", ctypes.c_void_p),
+        ("in_eps", ctypes.c_float),
+        ("kv", _KV),
+    ]
+
+
+_EXT = ctypes.POINTER(FusedExt)
+
 # name -> (restype, argtypes); mirrors include/mqk.h.
 SIGNATURES = {
     "mqk_version": (_I, []),
@@ -86,6 +101,21 @@ SIGNATURES = {
          _P, _P, _P, _P, _P,                      # q_gamma k_gamma cos sin positions
          _I64, _I64, _I64, _I, _I, _I,            # T S hidden Hq Hkv D
          _I64, _F, _P, _P, _P, _KV, _P, _SZ, _P], # cos_rows eps q k v kv workspace ws_bytes stream
+    ),
+    "mqk_fused_qkv_rope_ex_workspace_size": (_SZ, [_I64, _I, _I, _I64, _EXT]),
+    "mqk_fused_qkv_rope_ex_bf16": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P,     # x w_q w_k w_v q_gamma k_gamma cos sin positions
+         _I64, _I64, _I64, _I, _I, _I,           # T S hidden Hq Hkv D
+         _I64, _F, _P, _P, _P, _EXT, _P, _SZ, _P],  # cos_rows eps q k v ext workspace ws_bytes stream
+    ),
+    "mqk_fused_qkv_rope_ex_w4a16": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P,  # x, (qw, sc, qz) x 3
+         _I, _I,                                  # group scale_type
+         _P, _P, _P, _P, _P,                      # q_gamma k_gamma cos sin positions
+         _I64, _I64, _I64, _I, _I, _I,            # T S hidden Hq Hkv D
+         _I64, _F, _P, _P, _P, _EXT, _P, _SZ, _P],  # cos_rows eps q k v ext workspace ws_bytes stream
     ),
     "mqk_set_option": (_I, [ctypes.c_char_p, _I64]),
     "mqk_get_option": (_I64, [ctypes.c_char_p]),

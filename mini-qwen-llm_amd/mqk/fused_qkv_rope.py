@@ -225,6 +225,151 @@ def fused_qkv_rope_paged(
     return q, k, v
 
 
+def fused_ext(T: int, H_KV: int, D: int, hidden: int, device, positions=None, cu_seqlens=None,
+              seq_pos0=None, input_norm_w=None, input_eps: float = EPS, k_cache=None, v_cache=None,
+              block_table=None, kv_seq=None, kv_pos=None):
+    """Validated ``mqk_fused_ext`` descriptor of the optional features and the
+    tensors it points to (kept alive by the caller for the duration of the launch).
+
+    ``cu_seqlens [n_seqs + 1]`` int32 (varlen mode, exclusive with ``positions``),
+    ``seq_pos0 [n_seqs]`` (position of each sequence's first token, default 0),
+    ``input_norm_w [hidden]`` bf16 (input RMSNorm), and the paged cache
+    (``k_cache``/``v_cache``/``block_table`` together, see :func:`paged_kv`).
+    """
+    keep = []
+    ext = _native.FusedExt()
+    if cu_seqlens is not None:
+        if positions is not None:
+            raise ValueError("cu_seqlens (varlen) and positions are exclusive")
+        if cu_seqlens.dtype not in (torch.int32, torch.int64) or cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
+            raise ValueError("cu_seqlens must be a 1-D int32 tensor of n_seqs + 1 >= 2 offsets")
+        cu = _require(cu_seqlens, "cu_seqlens", device, dtype=None).to(torch.int32)
+        keep.append(cu)
+        ext.cu_seqlens = cu.data_ptr()
+        ext.n_seqs = cu.numel() - 1
+        if seq_pos0 is not None:
+            if seq_pos0.numel() != ext.n_seqs:
+                raise ValueError(f"seq_pos0 has {seq_pos0.numel()} entries, expected n_seqs = {ext.n_seqs}")
+            p0 = _require(seq_pos0, "seq_pos0", device, dtype=None).reshape(-1).to(torch.int32)
+            keep.append(p0)
+            ext.seq_pos0 = p0.data_ptr()
+    elif seq_pos0 is not None:
+        raise ValueError("seq_pos0 needs cu_seqlens")
+    if input_norm_w is not None:
+        g = _require(input_norm_w, "input_norm_w", device)
+        if g.shape != (hidden,):
+            raise ValueError(f"input_norm_w must be [{hidden}], got {tuple(g.shape)}")
+        keep.append(g)
+        ext.in_gamma = g.data_ptr()
+        ext.in_eps = float(input_eps)
+    if k_cache is not None or v_cache is not None or block_table is not None:
+        if k_cache is None or v_cache is None or block_table is None:
+            raise ValueError("k_cache, v_cache and block_table go together")
+        desc, kv_keep = paged_kv(k_cache, v_cache, block_table, kv_seq, kv_pos, T, H_KV, D, device, positions)
+        keep.append((desc, kv_keep))
+        ext.kv = ctypes.pointer(desc)
+    elif kv_seq is not None or kv_pos is not None:
+        raise ValueError("kv_seq / kv_pos need a paged cache")
+    return ext, keep
+
+
+def _lead_shape(x: torch.Tensor, cu_seqlens) -> Tuple[tuple, int]:
+    """Leading output dims and S for x [B, S, hidden] or (varlen) [T, hidden]."""
+    if x.dim() == 3:
+        return tuple(x.shape[:2]), x.shape[1]
+    if x.dim() == 2 and cu_seqlens is not None:
+        return (x.shape[0],), x.shape[0]
+    raise ValueError(f"x must be [B, S, hidden] (or [T, hidden] with cu_seqlens), got {tuple(x.shape)}")
+
+
+def fused_qkv_rope_ex(
+    x: torch.Tensor,
+    w_q: torch.Tensor,
+    w_k: torch.Tensor,
+    w_v: torch.Tensor,
+    q_norm_w: torch.Tensor,
+    k_norm_w: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    positions: Optional[torch.Tensor] = None,
+    *,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    seq_pos0: Optional[torch.Tensor] = None,
+    input_norm_w: Optional[torch.Tensor] = None,
+    input_eps: float = EPS,
+    k_cache: Optional[torch.Tensor] = None,
+    v_cache: Optional[torch.Tensor] = None,
+    block_table: Optional[torch.Tensor] = None,
+    kv_seq: Optional[torch.Tensor] = None,
+    kv_pos: Optional[torch.Tensor] = None,
+    return_kv: bool = True,
+):
+    """:func:`fused_qkv_rope` with the optional features of ``mqk_fused_qkv_rope_ex_bf16``.
+
+    * ``cu_seqlens`` (varlen prefill): ``x`` is ``[T, hidden]`` (or ``[1, T, hidden]``)
+      holding packed sequences; token t of sequence s uses RoPE row / cache
+      position ``t - cu_seqlens[s] (+ seq_pos0[s])`` and block-table row s, the
+      batch_ids / positions of paged_attn_prefill.py:188-199.
+    * ``input_norm_w``: the decoder's input RMSNorm (rms_norm.py:11-18) is applied
+      to ``x`` inside the op.
+    * ``k_cache``/``v_cache``/``block_table``: the paged-KV-cache write of
+      :func:`fused_qkv_rope_paged` (``return_kv=False`` writes the cache only).
+
+    Outputs are shaped ``x.shape[:-1] + (H, D)``.
+    """
+    lead, S = _lead_shape(x, cu_seqlens)
+    H = x.shape[-1]
+    D = q_norm_w.shape[0]
+    H_Q = w_q.shape[0] // D
+    H_KV = w_k.shape[0] // D
+    assert D % 2 == 0, "head_dim must be even (RoPE rotate_half)"
+    device = x.device
+    x = _require(x, "x", device)
+    w_q = _require(w_q, "w_q", device)
+    w_k = _require(w_k, "w_k", device)
+    w_v = _require(w_v, "w_v", device)
+    q_norm_w = _require(q_norm_w, "q_norm_w", device)
+    k_norm_w = _require(k_norm_w, "k_norm_w", device)
+    if w_q.shape != (H_Q * D, H) or w_k.shape != (H_KV * D, H) or w_v.shape != (H_KV * D, H):
+        raise ValueError(
+            f"weight shapes {tuple(w_q.shape)}, {tuple(w_k.shape)}, {tuple(w_v.shape)} do not match "
+            f"H_Q={H_Q}, H_KV={H_KV}, D={D}, hidden={H}")
+    cos, sin = _rope_tables(cos, sin, D, device)
+    T = x.numel() // H
+    pos = _positions(positions, T, device)
+    ext, keep = fused_ext(T, H_KV, D, H, device, positions, cu_seqlens, seq_pos0, input_norm_w, input_eps,
+                          k_cache, v_cache, block_table, kv_seq, kv_pos)
+    if not return_kv and not ext.kv:
+        raise ValueError("return_kv=False needs a paged cache")
+    q = torch.empty(*lead, H_Q, D, dtype=torch.bfloat16, device=device)
+    k = torch.empty(*lead, H_KV, D, dtype=torch.bfloat16, device=device) if return_kv else None
+    v = torch.empty(*lead, H_KV, D, dtype=torch.bfloat16, device=device) if return_kv else None
+    if T == 0:
+        return q, k, v
+    lib = _native.library()
+    stream = torch.cuda.current_stream(device)
+    nbytes = int(lib.mqk_fused_qkv_rope_ex_workspace_size(T, H_Q, H_KV, H, ctypes.byref(ext)))
+    ws = _native.workspace(device, stream, nbytes)
+    status = lib.mqk_fused_qkv_rope_ex_bf16(
+        x.data_ptr(), w_q.data_ptr(), w_k.data_ptr(), w_v.data_ptr(),
+        q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), _native.ptr(pos),
+        T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
+        q.data_ptr(), _native.ptr(k), _native.ptr(v), ctypes.byref(ext),
+        _native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
+    _native.check(status, "mqk_fused_qkv_rope_ex_bf16")
+    del keep
+    return q, k, v
+
+
+def fused_qkv_rope_varlen(x, w_q, w_k, w_v, q_norm_w, k_norm_w, cos, sin, cu_seqlens, seq_pos0=None,
+                          **kwargs):
+    """Varlen prefill: ``x [T, hidden]`` packed sequences delimited by ``cu_seqlens``;
+    returns ``q [T, H_Q, D]``, ``k``/``v [T, H_KV, D]`` (the layout paged_attn_prefill
+    takes).  Keyword arguments as :func:`fused_qkv_rope_ex`."""
+    return fused_qkv_rope_ex(x, w_q, w_k, w_v, q_norm_w, k_norm_w, cos, sin, cu_seqlens=cu_seqlens,
+                             seq_pos0=seq_pos0, **kwargs)
+
+
 def qk_norm_rope(
     q_raw: torch.Tensor,
     k_raw: torch.Tensor,

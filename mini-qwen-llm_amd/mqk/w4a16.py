@@ -26,7 +26,7 @@ import torch
 import torch.nn as nn
 
 from . import _native
-from .fused_qkv_rope import EPS, _positions, _require, _rope_tables, paged_kv
+from .fused_qkv_rope import EPS, _lead_shape, _positions, _require, _rope_tables, fused_ext, paged_kv
 from .quantization import from_autoawq, gptq_zero_fix, per_group_minmax_quantize
 
 
@@ -199,9 +199,42 @@ def fused_qkv_rope_w4a16_paged(
                         paged=(k_cache, v_cache, block_table, kv_seq, kv_pos), return_kv=return_kv)
 
 
+def fused_qkv_rope_w4a16_ex(
+    x: torch.Tensor,
+    q_proj,
+    k_proj,
+    v_proj,
+    q_norm_w: torch.Tensor,
+    k_norm_w: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    positions: Optional[torch.Tensor] = None,
+    *,
+    group_size: Optional[int] = None,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    seq_pos0: Optional[torch.Tensor] = None,
+    input_norm_w: Optional[torch.Tensor] = None,
+    input_eps: float = EPS,
+    k_cache: Optional[torch.Tensor] = None,
+    v_cache: Optional[torch.Tensor] = None,
+    block_table: Optional[torch.Tensor] = None,
+    kv_seq: Optional[torch.Tensor] = None,
+    kv_pos: Optional[torch.Tensor] = None,
+    return_kv: bool = True,
+):
+    """W4A16 twin of :func:`mqk.fused_qkv_rope_ex` (varlen positions, input RMSNorm,
+    paged-KV-cache write)."""
+    return _fused_w4a16(x, q_proj, k_proj, v_proj, q_norm_w, k_norm_w, cos, sin, positions, group_size,
+                        return_kv=return_kv,
+                        ext_args=dict(cu_seqlens=cu_seqlens, seq_pos0=seq_pos0, input_norm_w=input_norm_w,
+                                      input_eps=input_eps, k_cache=k_cache, v_cache=v_cache,
+                                      block_table=block_table, kv_seq=kv_seq, kv_pos=kv_pos))
+
+
 def _fused_w4a16(x, q_proj, k_proj, v_proj, q_norm_w, k_norm_w, cos, sin, positions, group_size,
-                 paged=None, return_kv=True):
-    B, S, H = x.shape
+                 paged=None, return_kv=True, ext_args=None):
+    lead, S = _lead_shape(x, None if ext_args is None else ext_args.get("cu_seqlens"))
+    H = x.shape[-1]
     D = q_norm_w.shape[0]
     assert D % 2 == 0, "head_dim must be even (RoPE rotate_half)"
     if group_size is None:
@@ -224,19 +257,26 @@ def _fused_w4a16(x, q_proj, k_proj, v_proj, q_norm_w, k_norm_w, cos, sin, positi
             parts[2][0].shape[1] != H_KV * D:
         raise ValueError("projection widths must be whole heads (H_Q*D, H_KV*D, H_KV*D)")
     cos, sin = _rope_tables(cos, sin, D, device)
-    T = B * S
+    T = x.numel() // H
     pos = _positions(positions, T, device)
-    desc = keep = None
+    desc = keep = ext = None
     if paged is not None:
         desc, keep = paged_kv(*paged, T, H_KV, D, device, positions)
-    q = torch.empty(B, S, H_Q, D, dtype=torch.bfloat16, device=device)
-    k = torch.empty(B, S, H_KV, D, dtype=torch.bfloat16, device=device) if return_kv else None
-    v = torch.empty(B, S, H_KV, D, dtype=torch.bfloat16, device=device) if return_kv else None
+    if ext_args is not None:
+        ext, keep = fused_ext(T, H_KV, D, H, device, positions, **ext_args)
+        if not return_kv and not ext.kv:
+            raise ValueError("return_kv=False needs a paged cache")
+    q = torch.empty(*lead, H_Q, D, dtype=torch.bfloat16, device=device)
+    k = torch.empty(*lead, H_KV, D, dtype=torch.bfloat16, device=device) if return_kv else None
+    v = torch.empty(*lead, H_KV, D, dtype=torch.bfloat16, device=device) if return_kv else None
     if T == 0:
         return q, k, v
     lib = _native.library()
     stream = torch.cuda.current_stream(device)
-    nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, H_Q, H_KV, H))
+    if ext is not None:
+        nbytes = int(lib.mqk_fused_qkv_rope_ex_workspace_size(T, H_Q, H_KV, H, ctypes.byref(ext)))
+    else:
+        nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, H_Q, H_KV, H))
     ws = _native.workspace(device, stream, nbytes)
     flat = [t.data_ptr() for trio in parts for t in trio]
     head = (x.data_ptr(), *flat, group_size, sts[0],
@@ -244,7 +284,10 @@ def _fused_w4a16(x, q_proj, k_proj, v_proj, q_norm_w, k_norm_w, cos, sin, positi
             _native.ptr(pos), T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
             q.data_ptr(), _native.ptr(k), _native.ptr(v))
     tail = (_native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
-    if desc is None:
+    if ext is not None:
+        status = lib.mqk_fused_qkv_rope_ex_w4a16(*head, ctypes.byref(ext), *tail)
+        _native.check(status, "mqk_fused_qkv_rope_ex_w4a16")
+    elif desc is None:
         status = lib.mqk_fused_qkv_rope_w4a16(*head, *tail)
         _native.check(status, "mqk_fused_qkv_rope_w4a16")
     else:

@@ -21,6 +21,8 @@ Pinning (what checks each function against something other than itself):
                            independent complex-number formulation of RoPE.
   * projection          -- brute-force triple loop on tiny shapes.
   * row selection       -- prefill ``t % S`` vs positions mode, sentinel tables.
+  * varlen_positions    -- hand-worked offsets with an empty sequence, and a
+                           brute-force scan of cu_seqlens for every token.
   * int4 pack/unpack    -- hand-packed 0x76543210 known answer, round trips.
   * minmax quantizer    -- hand-computed group, error <= scale/2, zero exact.
   * dequant / w4a16     -- brute-force nibble-by-nibble restatement.
@@ -118,6 +120,22 @@ def rope_rows(T: int, S: int, positions=None) -> np.ndarray:
     p = np.asarray(positions).astype(np.int64).reshape(-1)
     assert p.shape[0] == T
     return p
+
+
+def varlen_positions(cu_seqlens, seq_pos0=None):
+    """``(batch_ids, positions)`` of packed sequences, as paged_attn_prefill derives
+    them from ``cu_seqlens`` (mini_qwen/kernels/paged_attn_prefill.py:188-199):
+    ``batch_ids = repeat_interleave(arange(B), lengths)``,
+    ``positions = arange(total) - cu_seqlens[batch_ids]``; with ``seq_pos0`` the
+    position of each sequence's first token is added (continued sequences).
+    """
+    cu = np.asarray(cu_seqlens, dtype=np.int64).reshape(-1)
+    lengths = cu[1:] - cu[:-1]
+    batch = np.repeat(np.arange(lengths.shape[0], dtype=np.int64), lengths)
+    pos = np.arange(batch.shape[0], dtype=np.int64) - cu[batch]
+    if seq_pos0 is not None:
+        pos = pos + np.asarray(seq_pos0, dtype=np.int64).reshape(-1)[batch]
+    return batch, pos
 
 
 # ---------------------------------------------------------------------------

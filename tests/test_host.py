@@ -308,3 +308,30 @@ def test_paged_validation(lib):
     assert call(desc(), positions=fake) == -1
     assert "kv_seq" in lib.mqk_last_error_detail().decode()
     assert call(desc(), T=0) == 0
+
+
+def test_ext_validation(lib):
+    """mqk_fused_qkv_rope_ex_bf16 checks of the optional features (fake pointers,
+    never launched) and the input-norm workspace size."""
+    import ctypes
+    from mqk import _native
+    fake = 1 << 20
+
+    def call(ext, positions=None, T=100, S=100):
+        return lib.mqk_fused_qkv_rope_ex_bf16(
+            fake, fake, fake, fake, fake, fake, fake, fake, positions, T, S, 256, 2, 1, 128, 100, 1e-6,
+            fake, fake, fake, None if ext is None else ctypes.byref(ext), None, 0, None)
+
+    assert call(_native.FusedExt(), T=0) == 0
+    assert call(_native.FusedExt(cu_seqlens=fake, n_seqs=3), positions=fake) == -2
+    assert "exclusive" in lib.mqk_last_error_detail().decode()
+    assert call(_native.FusedExt(cu_seqlens=fake, n_seqs=0)) == -2
+    assert call(_native.FusedExt(seq_pos0=fake)) == -2
+    assert "cu_seqlens" in lib.mqk_last_error_detail().decode()
+    # prefill mode without varlen still needs S > 0
+    assert call(_native.FusedExt(), S=0) == -2 and "S > 0" in lib.mqk_last_error_detail().decode()
+    plain = lib.mqk_fused_qkv_rope_ex_workspace_size(1000, 32, 8, 4096, None)
+    assert plain == lib.mqk_fused_qkv_rope_workspace_size(1000, 32, 8, 4096)
+    normed = lib.mqk_fused_qkv_rope_ex_workspace_size(1000, 32, 8, 4096,
+                                                       ctypes.byref(_native.FusedExt(in_gamma=fake)))
+    assert normed >= plain + 4000

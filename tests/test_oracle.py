@@ -300,3 +300,22 @@ def test_metrics():
     neg = orc.f32_to_bf16(np.float32(-0.0))
     assert orc.bf16_ulp_distance(one, nxt) == 1
     assert orc.bf16_ulp_distance(neg, orc.f32_to_bf16(np.float32(0.0))) == 0
+
+
+def test_varlen_positions_known_answer():
+    b, p = orc.varlen_positions([0, 3, 3, 7])
+    assert b.tolist() == [0, 0, 0, 2, 2, 2, 2]
+    assert p.tolist() == [0, 1, 2, 0, 1, 2, 3]
+    b, p = orc.varlen_positions([0, 2, 5], seq_pos0=[10, 100])
+    assert b.tolist() == [0, 0, 1, 1, 1] and p.tolist() == [10, 11, 100, 101, 102]
+
+
+def test_varlen_positions_brute_force():
+    rng = np.random.default_rng(7)
+    lengths = rng.integers(0, 9, 13)
+    cu = np.concatenate([[0], np.cumsum(lengths)])
+    start = rng.integers(0, 50, 13)
+    b, p = orc.varlen_positions(cu, start)
+    for t in range(int(cu[-1])):
+        s = [i for i in range(13) if cu[i] <= t < cu[i + 1]]
+        assert len(s) == 1 and b[t] == s[0] and p[t] == t - cu[s[0]] + start[s[0]]
