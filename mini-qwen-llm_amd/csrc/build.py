@@ -23,7 +23,7 @@ CSRC = Path(__file__).resolve().parent
 PKG = CSRC.parent / "mqk"
 OUT = PKG / "libmqk.so"
 BUILD_DIR = CSRC.parent / "_build"
-SOURCES = ["qkv_tile.hip", "qkv_tile_dma.hip", "qkv_decode.hip", "norm_rope.hip", "mqk_api.hip"]
+SOURCES = ["qkv_tile.hip", "qkv_tile_dma.hip", "qkv_decode.hip", "norm_rope.hip", "input_norm.hip", "mqk_api.hip"]
 ARCH = "gfx950"
 
 COMMON_FLAGS = [

@@ -93,25 +93,38 @@ bool epilogue_aligned(const EpilogueArgs& e) {
   return aligned16(e.q_gamma) && aligned16(e.k_gamma) && aligned16(e.cos) && aligned16(e.sin);
 }
 
-// Common launcher of the fused op (bf16 or int4 weights).
-int run_fused(int int4, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
+// Common launcher of the fused op (bf16 or int4 weights).  With an input norm
+// (p.in_gamma set, epsilon in_eps), the per-token scales go to the workspace
+// after the decode kernel's region and are computed by a pre-pass first.
+int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& e, float in_eps,
               void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (p.M == 0) return ok();
   const int splits = use_decode(p.M) && epilogue_aligned(e)
                          ? decode_splits_for(p.M, p.K, p.n_tiles, int(g_decode_splits.load()))
                          : 0;
-  if (splits > 0) {
-    const size_t need = decode_workspace_bytes(p.n_tiles, splits);
-    if (!workspace || ws_bytes < need)
-      return fail(MQK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given%s", need, ws_bytes,
-                  workspace ? "" : " (NULL)");
-    return hip_status(launch_decode(int4, p, w, e, splits, workspace, stream), "decode kernel launch");
+  // (the decode kernel's arrival counters open every workspace and must stay zero,
+  // so the scales never start before them, whichever kernel runs this call)
+  const size_t base = splits > 0 ? decode_workspace_bytes(p.n_tiles, splits) : decode_counter_bytes();
+  const size_t scale_off = align_up(base, 256);
+  const size_t need = p.in_gamma ? scale_off + size_t(p.M) * sizeof(float) : (splits > 0 ? base : 0);
+  if (need > 0 && (!workspace || ws_bytes < need))
+    return fail(MQK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given%s", need, ws_bytes,
+                workspace ? "" : " (NULL)");
+  if (p.in_gamma) {
+    float* scale = reinterpret_cast<float*>(static_cast<char*>(workspace) + scale_off);
+    const int st = hip_status(launch_row_scale(p.x, p.M, p.K, in_eps, scale, stream), "input norm pre-pass launch");
+    if (st != MQK_OK) return st;
+    p.in_scale = scale;
   }
+  if (splits > 0)
+    return hip_status(launch_decode(int4, p, w, e, splits, workspace, stream), "decode kernel launch");
   const TileVariant* v = choose_tile_variant(int(g_prefill_tile.load()), p.M, p.n_tiles, int4);
   if (!v) return fail(MQK_ERR_BAD_OPTION, "prefill_tile variant %lld cannot run this problem (%d heads%s)",
                       (long long)g_prefill_tile.load(), p.n_tiles, int4 ? ", int4 weights" : "");
-  // The pipelined variants (ids >= 10) read every operand with 16-byte direct loads.
-  if (v->id >= 10 && !(epilogue_aligned(e) && (!int4 || int4_aligned(w))))
+  // The pipelined variants (ids >= 10) read every operand with 16-byte direct loads,
+  // and with an input norm hold gamma in LDS next to their ring.
+  if (v->id >= 10 && (!(epilogue_aligned(e) && (!int4 || int4_aligned(w))) ||
+                      (p.in_gamma && tile_dma_lds_bytes(v->id) + p.K * 2 > 160 * 1024)))
     v = choose_tile_variant(p.n_tiles % 2 == 0 ? 4 : 1, p.M, p.n_tiles, int4);
   return hip_status(launch_tile(*v, int4, p, w, e, int(g_group_m.load()), stream), "tile kernel launch");
 }
@@ -148,7 +161,8 @@ size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hid
 size_t mqk_fused_qkv_rope_ex_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden,
                                             const mqk_fused_ext* ext) {
   size_t n = mqk_fused_qkv_rope_workspace_size(T, Hq, Hkv, hidden);
-  if (ext && ext->in_gamma && T > 0) n = align_up(n, 256) + align_up(size_t(T) * sizeof(float), 256);
+  if (ext && ext->in_gamma && T > 0)
+    n = align_up(n > 0 ? n : decode_counter_bytes(), 256) + align_up(size_t(T) * sizeof(float), 256);
   return n;
 }
 
@@ -201,7 +215,7 @@ static int apply_paged(const mqk_paged_kv* kv, const int32_t* positions, int64_t
 
 // Optional features of the _ex entry points -> epilogue / problem fields.
 static int apply_ext(const mqk_fused_ext* ext, const int32_t* positions, int64_t S, int64_t T,
-                     EpilogueArgs& e) {
+                     ProblemArgs& p, EpilogueArgs& e) {
   if (!ext) return MQK_OK;
   const bool varlen = ext->cu_seqlens != nullptr;
   if (varlen) {
@@ -214,7 +228,12 @@ static int apply_ext(const mqk_fused_ext* ext, const int32_t* positions, int64_t
   } else if (ext->seq_pos0) {
     return fail(MQK_ERR_BAD_SHAPE, "seq_pos0 needs cu_seqlens");
   }
-  if (ext->in_gamma) return fail(MQK_ERR_UNSUPPORTED, "input RMSNorm is not available yet");
+  if (ext->in_gamma) {
+    if (!aligned16(ext->in_gamma)) return fail(MQK_ERR_MISALIGNED, "in_gamma must be 16-byte aligned");
+    if (p.K > 16384) return fail(MQK_ERR_UNSUPPORTED, "input RMSNorm needs hidden <= 16384");
+    if (!(ext->in_eps >= 0.0f)) return fail(MQK_ERR_BAD_SHAPE, "in_eps must be >= 0");
+    p.in_gamma = ext->in_gamma;
+  }
   return apply_paged(ext->kv, positions, S, T, varlen, e);
 }
 
@@ -243,8 +262,8 @@ static int fused_bf16_impl(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf1
   w.n_cols[1] = w.n_cols[2] = int64_t(Hkv) * kHeadDim;
   EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
                                      q, k, v, Hq, Hkv);
-  if ((st = apply_ext(ext, positions, S, T, e)) != MQK_OK) return st;
-  return run_fused(0, p, w, e, workspace, ws_bytes, static_cast<hipStream_t>(stream));
+  if ((st = apply_ext(ext, positions, S, T, p, e)) != MQK_OK) return st;
+  return run_fused(0, p, w, e, ext ? ext->in_eps : 0.f, workspace, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
@@ -384,8 +403,8 @@ static int fused_w4a16_impl(const mqk_bf16* x, const int32_t* qw_q, const void* 
   w.scale_fp16 = scale_type == MQK_SCALE_FP16;
   EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
                                      q, k, v, Hq, Hkv);
-  if ((st = apply_ext(ext, positions, S, T, e)) != MQK_OK) return st;
-  return run_fused(1, p, w, e, workspace, ws_bytes, static_cast<hipStream_t>(stream));
+  if ((st = apply_ext(ext, positions, S, T, p, e)) != MQK_OK) return st;
+  return run_fused(1, p, w, e, ext ? ext->in_eps : 0.f, workspace, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 int mqk_fused_qkv_rope_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void* sc_q,

@@ -101,6 +101,23 @@ __device__ __forceinline__ void varlen_locate(const E& e, int64_t t, int64_t& se
   pos = t - int64_t(e.cu_seqlens[lo]) + (e.seq_pos0 ? int64_t(e.seq_pos0[lo]) : 0);
 }
 
+// The decoder's input RMSNorm applied to 8 activations of one token
+// (mini_qwen/model/layers/rms_norm.py:15-18): bf16(gamma * bf16(x * scale)) with
+// scale = rsqrt(mean(x^2) + eps) of the token, i.e. the product is rounded to bf16
+// before the gamma multiply, which is rounded again -- the bf16 operand the
+// reference's projection reads.
+__device__ __forceinline__ u32x4_t input_norm8(const u32x4_t& xv, float scale, const u32x4_t& gv) {
+  u32x4_t r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t xw = xv[j], gw = gv[j];
+    const uint32_t y = pack_bf16x2(bf16_to_f32(xw & 0xFFFFu) * scale, bf16_to_f32(xw >> 16) * scale);
+    r[j] = pack_bf16x2(bf16_to_f32(y & 0xFFFFu) * bf16_to_f32(gw & 0xFFFFu),
+                       bf16_to_f32(y >> 16) * bf16_to_f32(gw >> 16));
+  }
+  return r;
+}
+
 // Row of the RoPE table used by token t, clamped into [0, rows): prefill t % S
 // (reference fused_qkv_rope.py:109), positions[t] (:107), or the varlen position.
 template <class E>

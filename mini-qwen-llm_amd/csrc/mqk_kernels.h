@@ -62,6 +62,10 @@ struct ProblemArgs {
   int64_t M;
   int64_t K;
   int n_tiles;         // number of 128-column tiles (heads)
+  // Input RMSNorm (null in_gamma: none): the projection reads
+  // bf16(in_gamma[k] * bf16(x[m, k] * in_scale[m])) instead of x (input_norm8).
+  const uint16_t* in_gamma;  // [K] bf16
+  const float* in_scale;     // [M] rsqrt(mean(x^2) + eps), from launch_row_scale
 };
 
 // One tile-kernel variant: BM rows x (HPT*128) columns per workgroup, with KZ
@@ -90,8 +94,16 @@ hipError_t launch_tile_dma_w4(int id, const ProblemArgs& p, const WeightArgs& w,
 // Split-K decode kernel for T <= 64.  decode_splits_for returns 0 when no
 // valid split count exists (each split covers at most 16 64-wide k tiles);
 // the caller then uses the tile kernel.
+// LDS bytes (static) of pipelined tile variant id (10..32); 0 for other ids.
+int tile_dma_lds_bytes(int id);
+
+// Input RMSNorm pre-pass: scale[m] = rsqrt(mean(x[m, :]^2) + eps) for x [M, K] bf16.
+hipError_t launch_row_scale(const uint16_t* x, int64_t M, int64_t K, float eps, float* scale,
+                            hipStream_t stream);
+
 int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested);
 size_t decode_workspace_bytes(int n_tiles, int splits);
+size_t decode_counter_bytes();  // the arrival counters at the start of every workspace
 hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                          int splits, void* workspace, hipStream_t stream);
 

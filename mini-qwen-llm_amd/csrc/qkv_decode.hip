@@ -111,6 +111,47 @@ __device__ __forceinline__ void stage_x_tile(const ProblemArgs& p, int64_t kbeg,
         xs_lds + uint32_t(t * kDecRows * 128 + wave * 1024));
 }
 
+// Input RMSNorm (ProblemArgs::in_gamma): gamma is staged in the dynamic LDS that
+// follows the x slice, and each wave normalises the x chunks its own direct
+// loads brought in (rows [8w, 8w+8) of every tile: lane L holds row 8w + L/8,
+// slot L % 8), in place, once they have landed.
+extern __shared__ __attribute__((aligned(16))) unsigned char g_dec_dyn_lds[];
+constexpr int kGamPerThread = 4;  // gamma chunks per thread: hidden <= 4 * 512 * 8
+
+// Issue this thread's gamma loads (registers); stored to LDS by gamma_to_lds.
+__device__ __forceinline__ void gamma_load(const ProblemArgs& p, u32x4_t (&gv)[kGamPerThread]) {
+#pragma unroll
+  for (int j = 0; j < kGamPerThread; ++j) {
+    const int64_t c = threadIdx.x + j * kDecThreads;
+    gv[j] = c < p.K / 8 ? *reinterpret_cast<const u32x4_t*>(p.in_gamma + c * 8) : u32x4_t{0, 0, 0, 0};
+  }
+}
+
+__device__ __forceinline__ void gamma_to_lds(const ProblemArgs& p, const u32x4_t (&gv)[kGamPerThread]) {
+#pragma unroll
+  for (int j = 0; j < kGamPerThread; ++j) {
+    const int64_t c = threadIdx.x + j * kDecThreads;
+    if (c < p.K / 8) *reinterpret_cast<u32x4_t*>(g_dec_dyn_lds + c * 16) = gv[j];
+  }
+}
+
+// Normalise this wave's chunks of x tiles [0, nk) of the slice starting at k = kbeg
+// (gamma must be in LDS); ends with this wave's LDS writes complete.
+__device__ __forceinline__ void norm_x_tiles(const ProblemArgs& p, uint16_t* xs, int64_t kbeg, int nk) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row = wave * 8 + (lane >> 3);
+  const int gq = (lane & 7) ^ ((row >> 1) & 7);
+  const float scale = p.in_scale[row < int(p.M) ? row : int(p.M) - 1];
+  unsigned char* base = reinterpret_cast<unsigned char*>(xs) + wave * 1024 + lane * 16;
+  for (int t = 0; t < nk; ++t) {
+    u32x4_t* q = reinterpret_cast<u32x4_t*>(base + t * kDecRows * 128);
+    const u32x4_t g = *reinterpret_cast<const u32x4_t*>(g_dec_dyn_lds + (kbeg + t * kBK + gq * 8) * 2);
+    *q = input_norm8(*q, scale, g);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
 // 16x16x32 operand layout: lane (c, g) = (lane & 15, lane >> 4) holds column c
 // of the wave's 16 (B) / row c of a 16-row block (A) and 8 k values; inside a
 // 64-wide k tile, block kk (0, 1) of 32 and lane group g give k = kk*32 + g*8.
@@ -198,6 +239,8 @@ __device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const Weight
     constexpr int kLook = NK < kDecLookahead ? NK : kDecLookahead;
     const uint16_t* wp = w.w[proj] + col * p.K + kbeg + g4 * 8;
     u32x4_t b[NK][2];
+    u32x4_t gv[kGamPerThread];
+    if (p.in_gamma) gamma_load(p, gv);
 #pragma unroll
     for (int t = 0; t < NK; ++t) stage_x_tile(p, kbeg, t, xs_lds);
 #pragma unroll
@@ -206,6 +249,12 @@ __device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const Weight
       for (int kk = 0; kk < 2; ++kk)
         b[t][kk] = wload(wp + t * kBK + kk * 32);
     wait_vm<2 * kLook>();  // the x slice has landed (older than the weight loads) ...
+    if (p.in_gamma) {      // (gamma too: loaded before it)
+      gamma_to_lds(p, gv);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      barrier();
+      norm_x_tiles(p, const_cast<uint16_t*>(xs), kbeg, NK);
+    }
     barrier();             // ... in every wave
     DECODE_TRACE(5)
 #pragma unroll
@@ -232,9 +281,17 @@ __device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const Weight
       sraw[t] = ic.sc[grp * ic.n + col];
       zw[t] = uint32_t(ic.qz[grp * (ic.n / 8) + col / 8]);
     }
+    u32x4_t gv[kGamPerThread];
+    if (p.in_gamma) gamma_load(p, gv);
 #pragma unroll
     for (int t = 0; t < NK; ++t) stage_x_tile(p, kbeg, t, xs_lds);
     wait_vm<0>();
+    if (p.in_gamma) {
+      gamma_to_lds(p, gv);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      barrier();
+      norm_x_tiles(p, const_cast<uint16_t*>(xs), kbeg, NK);
+    }
     barrier();
 #pragma unroll
     for (int t = 0; t < NK; ++t) {
@@ -260,6 +317,7 @@ __device__ void partial_any(const ProblemArgs& p, const WeightArgs& w, int proj,
   for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4_t{};
   for (int t = 0; t < nk; ++t) stage_x_tile(p, kbeg, t, xs_lds);
   wait_vm<0>();
+  if (p.in_gamma) norm_x_tiles(p, const_cast<uint16_t*>(xs), kbeg, nk);  // gamma is in LDS already
   barrier();
   for (int t = 0; t < nk; ++t) {
     const int64_t k0 = kbeg + int64_t(t) * kBK;
@@ -538,6 +596,8 @@ int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested) {
   return s;
 }
 
+size_t decode_counter_bytes() { return size_t(kCounterBytes); }
+
 size_t decode_workspace_bytes(int n_tiles, int splits) {
   return size_t(kCounterBytes) + size_t(splits) * n_tiles * kTileFloats * sizeof(float);
 }
@@ -554,11 +614,15 @@ hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, co
   const int fr = g_decode_force_recompute;
   auto a16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; };
   if (!(a16(e.q_gamma) && a16(e.k_gamma) && a16(e.cos) && a16(e.sin))) return hipErrorInvalidValue;
+  const size_t dyn = p.in_gamma ? size_t(p.K) * 2 : 0;
+  if (p.in_gamma && (p.K / 8 > int64_t(kGamPerThread) * kDecThreads ||
+                     kDecRows * kDecKc * 2 + 16 + dyn > 160 * 1024 || !a16(p.in_gamma)))
+    return hipErrorInvalidValue;
   if (int4)
-    hipLaunchKernelGGL(decode_kernel<true>, grid, dim3(kDecThreads), 0, stream, p, w, e, splits, part, counters,
+    hipLaunchKernelGGL(decode_kernel<true>, grid, dim3(kDecThreads), dyn, stream, p, w, e, splits, part, counters,
                        fr);
   else
-    hipLaunchKernelGGL(decode_kernel<false>, grid, dim3(kDecThreads), 0, stream, p, w, e, splits, part,
+    hipLaunchKernelGGL(decode_kernel<false>, grid, dim3(kDecThreads), dyn, stream, p, w, e, splits, part,
                        counters, fr);
   return hipGetLastError();
 }

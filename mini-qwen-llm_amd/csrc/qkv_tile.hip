@@ -177,6 +177,9 @@ tile_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   // ---- per-thread global sources and LDS slots ------------------------------
   const uint16_t* a_src[TS::kCA];
   int a_lds[TS::kCA];
+  float a_scale[TS::kCA];  // input RMSNorm scale of the chunk's row
+  int a_cc[TS::kCA];
+  const bool in_norm = p.in_gamma != nullptr;
 #pragma unroll
   for (int i = 0; i < TS::kCA; ++i) {
     const int ci = tid + i * NT;
@@ -185,6 +188,8 @@ tile_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
     grow = grow < p.M ? grow : p.M - 1;  // rows past M re-read the last row; never stored
     a_src[i] = p.x + grow * K + cc * 8;
     a_lds[i] = lds_off(row, cc);
+    a_cc[i] = cc;
+    a_scale[i] = in_norm ? p.in_scale[grow] : 1.f;
   }
 
   const uint16_t* b_src[INT4 ? 1 : TS::kCB];
@@ -227,6 +232,7 @@ tile_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   }
 
   u32x4_t ra[TS::kCA];
+  u32x4_t rg[TS::kCA];  // input-norm gamma of each A chunk
   u32x4_t rb[INT4 ? 1 : TS::kCB];
   uint32_t rq[INT4 ? TS::kCB : 1];
   uint32_t rs = 0, rz = 0;
@@ -235,6 +241,10 @@ tile_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
     const int64_t k0 = int64_t(kt) * kBK;
 #pragma unroll
     for (int i = 0; i < TS::kCA; ++i) ra[i] = *reinterpret_cast<const u32x4_t*>(a_src[i] + k0);
+    if (in_norm) {
+#pragma unroll
+      for (int i = 0; i < TS::kCA; ++i) rg[i] = *reinterpret_cast<const u32x4_t*>(p.in_gamma + k0 + a_cc[i] * 8);
+    }
     if constexpr (!INT4) {
 #pragma unroll
       for (int i = 0; i < TS::kCB; ++i) rb[i] = *reinterpret_cast<const u32x4_t*>(b_src[i] + k0);
@@ -252,6 +262,10 @@ tile_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   auto sstore = [&](int buf) {
     uint16_t* sA = smem + buf * TS::kStage;
     uint16_t* sB = sA + BM * kBK;
+    if (in_norm) {
+#pragma unroll
+      for (int i = 0; i < TS::kCA; ++i) ra[i] = input_norm8(ra[i], a_scale[i], rg[i]);
+    }
 #pragma unroll
     for (int i = 0; i < TS::kCA; ++i) *reinterpret_cast<u32x4_t*>(sA + a_lds[i]) = ra[i];
     if constexpr (!INT4) {

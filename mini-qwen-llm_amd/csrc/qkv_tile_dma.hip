@@ -66,6 +66,8 @@ struct DmaShape {
   static constexpr int kLdsBytes = kRingBytes > kEpiBytes ? kRingBytes : kEpiBytes;
   static_assert(kTM % 32 == 0 && kTN % 32 == 0, "wave tile");
   static_assert(kLoadsPerStage % kWaves == 0, "loads per wave");
+  static constexpr int kALoads = BM / (kRowsPerLoad * kWaves);  // this wave's loads i < kALoads fill x rows
+  static_assert(BM % (kRowsPerLoad * kWaves) == 0, "x rows are whole load rounds");
   static_assert(NS >= 2 && NS <= 8, "stages");
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
 };
@@ -91,6 +93,27 @@ template <int SBK>
 __device__ __forceinline__ int stage_slot(int row, int chunk) {
   if constexpr (SBK == 32) return chunk ^ ((row >> 2) & 3);  // 64 B rows: rows r, r+4, r+8, r+12 share banks
   else return chunk ^ ((row >> 1) & 7);                       // 128 B rows: even / odd rows use bank halves
+}
+
+// Input RMSNorm support (ProblemArgs::in_gamma): the gamma vector is staged once
+// in the dynamic LDS that follows the kernel's static LDS, and every wave applies
+// input_norm8 in place to the x chunks its own direct loads brought in, after
+// waiting for them and before the stage barrier, so the MFMA reads see normalised
+// activations without any extra barrier in the main loop.
+extern __shared__ __attribute__((aligned(16))) unsigned char g_dyn_lds[];
+
+template <int THREADS>
+__device__ __forceinline__ void stage_gamma(const ProblemArgs& p) {
+  for (int64_t c = threadIdx.x; c < p.K / 8; c += THREADS)
+    *reinterpret_cast<u32x4_t*>(g_dyn_lds + c * 16) = *reinterpret_cast<const u32x4_t*>(p.in_gamma + c * 8);
+}
+
+// In place: the 16-byte x chunk at LDS `chunk_ptr` (k = k0 .. k0+7 of a row whose
+// scale is `scale`) becomes bf16(gamma * bf16(x * scale)).
+__device__ __forceinline__ void norm_chunk(unsigned char* chunk_ptr, int64_t k0, float scale) {
+  const u32x4_t g = *reinterpret_cast<const u32x4_t*>(g_dyn_lds + k0 * 2);
+  u32x4_t* q = reinterpret_cast<u32x4_t*>(chunk_ptr);
+  *q = input_norm8(*q, scale, g);
 }
 
 // Per-head epilogue of a BM x (NH*128) tile held in MFMA 32x32 accumulators:
@@ -303,6 +326,23 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
     }
     dst_off[i] = uint32_t(row0 * kRowBytes);
   }
+  // input RMSNorm: scale of the x row and k offset of the chunk each of this
+  // lane's x loads brings in (load i < kALoads, row0 + lane / chunks, slot lane % chunks)
+  const bool in_norm = p.in_gamma != nullptr;
+  float a_scale[S::kALoads];
+  int a_koff[S::kALoads];
+#pragma unroll
+  for (int i = 0; i < S::kALoads; ++i) {
+    const int row = S::kRowsPerLoad * (wave + i * S::kWaves) + lane / S::kChunks;
+    int64_t grow = m0 + row;
+    grow = grow < p.M ? grow : p.M - 1;
+    a_scale[i] = in_norm ? p.in_scale[grow] : 1.f;
+    a_koff[i] = stage_slot<SBK>(row, lane % S::kChunks) * 8;
+  }
+  if (in_norm) {
+    stage_gamma<S::kThreads>(p);
+    __syncthreads();
+  }
   auto issue = [&](int kt) {
     const uint32_t base = lds0 + uint32_t((kt % NS) * S::kStageBytes);
 #pragma unroll
@@ -338,6 +378,13 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
 #ifdef MQK_TILE_TRACE  // diagnostic build: per-stage timestamps of wave 0 of each workgroup
     if (g_tile_trace && tid == 0 && kt < 126) g_tile_trace[blockIdx.x * 256 + 2 * kt] = __builtin_amdgcn_s_memrealtime();
 #endif
+    if (in_norm) {  // this wave's x chunks of stage kt have landed: normalise them in place
+#pragma unroll
+      for (int i = 0; i < S::kALoads; ++i)
+        norm_chunk(smem + (kt % NS) * S::kStageBytes + dst_off[i] + lane * 16, int64_t(kt) * SBK + a_koff[i],
+                   a_scale[i]);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
     barrier();
 #ifdef MQK_TILE_TRACE
     if (g_tile_trace && tid == 0 && kt < 126) g_tile_trace[blockIdx.x * 256 + 2 * kt + 1] = __builtin_amdgcn_s_memrealtime();
@@ -387,7 +434,9 @@ hipError_t launch_dma(const ProblemArgs& p, const WeightArgs& w, const EpilogueA
   using S = DmaShape<BM, NH, WM, WN, NS, SBK>;
   const int n_mt = int((p.M + BM - 1) / BM);
   const int blocks = n_mt * (p.n_tiles / NH);
-  hipLaunchKernelGGL((tile_dma_kernel<BM, NH, WM, WN, NS, SBK>), dim3(blocks), dim3(S::kThreads), 0, stream, p, w, e,
+  const size_t dyn = p.in_gamma ? size_t(p.K) * 2 : 0;
+  if (S::kLdsBytes + dyn > 160 * 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((tile_dma_kernel<BM, NH, WM, WN, NS, SBK>), dim3(blocks), dim3(S::kThreads), dyn, stream, p, w, e,
                      group_m < 1 ? 1 : group_m);
   return hipGetLastError();
 }
@@ -535,6 +584,23 @@ tile_dma_w4_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
       kind[i] = 3;
     }
   }
+  // input RMSNorm: scale of the x row and k offset of the chunk of each x load slot
+  const bool in_norm = p.in_gamma != nullptr;
+  float a_scale[S::kMaxPerWave];
+  int a_koff[S::kMaxPerWave];
+#pragma unroll
+  for (int i = 0; i < S::kMaxPerWave; ++i) {
+    const int g = wave + i * S::kWaves;
+    const int row = 8 * g + (lane >> 3);
+    int64_t grow = m0 + (row < BM ? row : 0);
+    grow = grow < p.M ? grow : p.M - 1;
+    a_scale[i] = (in_norm && g < S::kNA) ? p.in_scale[grow] : 1.f;
+    a_koff[i] = stage_slot<64>(row, lane & 7) * 8;
+  }
+  if (in_norm) {
+    stage_gamma<S::kThreads>(p);
+    __syncthreads();
+  }
   const int group = w.group;
   auto issue = [&](int kt) {
     const uint32_t sbase = lds0 + uint32_t((kt % NS) * S::kStageBytes);
@@ -565,6 +631,14 @@ tile_dma_w4_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   for (int kt = 0; kt < nkt; ++kt) {
     const int ahead = min(NS - 2, nkt - 1 - kt);  // stages already issued after kt
     wait_vm_n(ahead * nslots);
+    if (in_norm) {  // this wave's x chunks of stage kt have landed: normalise them in place
+#pragma unroll
+      for (int i = 0; i < S::kMaxPerWave; ++i)
+        if (wave + i * S::kWaves < S::kNA)
+          norm_chunk(smem + (kt % NS) * S::kStageBytes + dst[i] + lane * 16, int64_t(kt) * 64 + a_koff[i],
+                     a_scale[i]);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
     barrier();
     if (kt + NS - 1 < nkt) issue(kt + NS - 1);
     const unsigned char* st = smem + (kt % NS) * S::kStageBytes;
@@ -608,7 +682,9 @@ hipError_t launch_dma_w4(const ProblemArgs& p, const WeightArgs& w, const Epilog
   using S = W4Shape<BM, NH, WM, WN, NS>;
   const int n_mt = int((p.M + BM - 1) / BM);
   const int blocks = n_mt * (p.n_tiles / NH);
-  hipLaunchKernelGGL((tile_dma_w4_kernel<BM, NH, WM, WN, NS>), dim3(blocks), dim3(S::kThreads), 0, stream, p, w,
+  const size_t dyn = p.in_gamma ? size_t(p.K) * 2 : 0;
+  if (S::kLdsBytes + dyn > 160 * 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((tile_dma_w4_kernel<BM, NH, WM, WN, NS>), dim3(blocks), dim3(S::kThreads), dyn, stream, p, w,
                      e, group_m < 1 ? 1 : group_m);
   return hipGetLastError();
 }
@@ -628,6 +704,24 @@ hipError_t launch_tile_dma(int id, const ProblemArgs& p, const WeightArgs& w, co
     case 17: return launch_dma<256, 2, 4, 2, 2, 64>(p, w, e, group_m, stream);  // 256x256, 2 stages of 64 k
     case 18: return launch_dma<256, 2, 2, 4, 2, 64>(p, w, e, group_m, stream);  // 256x256 (128x64 waves), 64 k
     default: return hipErrorInvalidValue;
+  }
+}
+
+int tile_dma_lds_bytes(int id) {
+  switch (id) {
+    case 10: return DmaShape<256, 2, 4, 2, 4, 32>::kLdsBytes;
+    case 11: return DmaShape<128, 3, 2, 4, 4, 32>::kLdsBytes;
+    case 12: return DmaShape<256, 1, 4, 1, 4, 32>::kLdsBytes;
+    case 13: return DmaShape<128, 2, 2, 2, 4, 32>::kLdsBytes;
+    case 14: return DmaShape<256, 2, 2, 4, 4, 32>::kLdsBytes;
+    case 15: return DmaShape<128, 3, 2, 4, 5, 32>::kLdsBytes;
+    case 16: return DmaShape<128, 3, 2, 4, 2, 64>::kLdsBytes;
+    case 17: return DmaShape<256, 2, 4, 2, 2, 64>::kLdsBytes;
+    case 18: return DmaShape<256, 2, 2, 4, 2, 64>::kLdsBytes;
+    case 30: return W4Shape<128, 3, 2, 4, 4>::kLdsBytes;
+    case 31: return W4Shape<256, 2, 2, 4, 3>::kLdsBytes;
+    case 32: return W4Shape<128, 2, 2, 2, 4>::kLdsBytes;
+    default: return 0;
   }
 }
 

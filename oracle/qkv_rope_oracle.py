@@ -253,14 +253,20 @@ def unfused_composition(x, w_q, w_k, w_v, q_norm_w, k_norm_w, cos, sin,
 # (mini_qwen/model/layers/rms_norm.py:11-18)
 # ---------------------------------------------------------------------------
 
-def rms_norm_hf(x, weight, eps: float = DEFAULT_EPS, round_to_bf16: bool = True):
-    """``weight * (x_fp32 * rms).to(input_dtype)`` -- rounds before the gamma multiply."""
+def rms_norm_hf(x, weight, eps: float = DEFAULT_EPS, round_to_bf16: bool = True, round_out: bool = False):
+    """``weight * (x_fp32 * rms).to(input_dtype)`` -- rounds before the gamma multiply.
+
+    With bf16 activations and weight (the model dtype) the product is a bf16
+    tensor too: ``round_out=True`` rounds it, giving the bf16 input the decoder
+    layer hands to the attention projections (qwen3.py:58-59).
+    """
     xf = np.asarray(x, dtype=np.float32)
     rms = np.float32(1.0) / np.sqrt(np.mean(xf * xf, axis=-1, keepdims=True) + np.float32(eps))
     y = xf * rms
     if round_to_bf16:
         y = round_bf16(y)
-    return np.asarray(weight, dtype=np.float32) * y
+    out = np.asarray(weight, dtype=np.float32) * y
+    return round_bf16(out) if round_out else out
 
 
 # ---------------------------------------------------------------------------

@@ -330,6 +330,8 @@ def test_ext_validation(lib):
     assert "cu_seqlens" in lib.mqk_last_error_detail().decode()
     # prefill mode without varlen still needs S > 0
     assert call(_native.FusedExt(), S=0) == -2 and "S > 0" in lib.mqk_last_error_detail().decode()
+    assert call(_native.FusedExt(in_gamma=fake + 2, in_eps=1e-6)) == -4
+    assert call(_native.FusedExt(in_gamma=fake, in_eps=-1.0)) == -2
     plain = lib.mqk_fused_qkv_rope_ex_workspace_size(1000, 32, 8, 4096, None)
     assert plain == lib.mqk_fused_qkv_rope_workspace_size(1000, 32, 8, 4096)
     normed = lib.mqk_fused_qkv_rope_ex_workspace_size(1000, 32, 8, 4096,

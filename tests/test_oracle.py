@@ -214,6 +214,18 @@ def test_rms_norm_hf_rounds_before_gamma():
     assert y[0, 0] == np.float32(1.5) * orc.round_bf16(np.float32(1.0) * np.float32(rms))
 
 
+def test_rms_norm_hf_round_out_closed_form():
+    """bf16 model: weight * y is a bf16 product.  x = 2 everywhere gives y = bf16(0.99999988)
+    = 1 exactly, so the output is the weight rounded to bf16: 1 + 2^-8 is a tie that
+    rounds to even (1.0)."""
+    x = np.full((2, 64), 2.0, np.float32)
+    g = np.full(64, 1.0 + 2.0 ** -8, np.float32)
+    assert np.all(orc.rms_norm_hf(x, g, round_out=True) == 1.0)
+    assert np.all(orc.rms_norm_hf(x, g) == np.float32(1.0 + 2.0 ** -8))
+    g2 = np.full(64, 1.0 + 3 * 2.0 ** -8, np.float32)  # tie between 1+2^-7 and 1+2^-6: even is 1+2^-6
+    assert np.all(orc.rms_norm_hf(x, g2, round_out=True) == np.float32(1.0 + 2.0 ** -6))
+
+
 # ── int4 format (packing.py, awq.py, linear_w4a16.py) ─────────────────────────
 
 def test_pack_known_answer():
