@@ -220,7 +220,7 @@ __device__ __forceinline__ void dequant_tile(const Int4Col& ic, const uint32_t (
 // in every wave (own wait: the 3*(NK-1-t)+2 later loads may still be pending;
 // then a barrier) and its weight fragments have arrived (the compiler's per-use
 // waits), so the MFMAs run under the rest of the stream.
-template <bool INT4, int NK>
+template <bool INT4, bool INORM, int NK>
 __device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const WeightArgs& w, int proj, int hh,
                                               int kt0, const uint16_t* xs, uint32_t xs_lds, f32x4_t (&acc)[4]) {
   const int lane = threadIdx.x & 63;
@@ -240,7 +240,7 @@ __device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const Weight
     const uint16_t* wp = w.w[proj] + col * p.K + kbeg + g4 * 8;
     u32x4_t b[NK][2];
     u32x4_t gv[kGamPerThread];
-    if (p.in_gamma) gamma_load(p, gv);
+    if (INORM) gamma_load(p, gv);
 #pragma unroll
     for (int t = 0; t < NK; ++t) stage_x_tile(p, kbeg, t, xs_lds);
 #pragma unroll
@@ -249,7 +249,7 @@ __device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const Weight
       for (int kk = 0; kk < 2; ++kk)
         b[t][kk] = wload(wp + t * kBK + kk * 32);
     wait_vm<2 * kLook>();  // the x slice has landed (older than the weight loads) ...
-    if (p.in_gamma) {      // (gamma too: loaded before it)
+    if (INORM) {           // (gamma too: loaded before it)
       gamma_to_lds(p, gv);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       barrier();
@@ -282,11 +282,11 @@ __device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const Weight
       zw[t] = uint32_t(ic.qz[grp * (ic.n / 8) + col / 8]);
     }
     u32x4_t gv[kGamPerThread];
-    if (p.in_gamma) gamma_load(p, gv);
+    if (INORM) gamma_load(p, gv);
 #pragma unroll
     for (int t = 0; t < NK; ++t) stage_x_tile(p, kbeg, t, xs_lds);
     wait_vm<0>();
-    if (p.in_gamma) {
+    if (INORM) {
       gamma_to_lds(p, gv);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       barrier();
@@ -305,7 +305,7 @@ __device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const Weight
 // The same partial with a run-time k-range and one tile's loads at a time: the
 // arithmetic (per-tile dequant, MFMA order) is identical to partial_fixed, so
 // its result is bit-identical.  Used by the recompute path only.
-template <bool INT4>
+template <bool INT4, bool INORM>
 __device__ void partial_any(const ProblemArgs& p, const WeightArgs& w, int proj, int hh, int kt0, int nk,
                             const uint16_t* xs, uint32_t xs_lds, f32x4_t (&acc)[4]) {
   const int lane = threadIdx.x & 63;
@@ -317,7 +317,7 @@ __device__ void partial_any(const ProblemArgs& p, const WeightArgs& w, int proj,
   for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4_t{};
   for (int t = 0; t < nk; ++t) stage_x_tile(p, kbeg, t, xs_lds);
   wait_vm<0>();
-  if (p.in_gamma) norm_x_tiles(p, const_cast<uint16_t*>(xs), kbeg, nk);  // gamma is in LDS already
+  if (INORM) norm_x_tiles(p, const_cast<uint16_t*>(xs), kbeg, nk);  // gamma is in LDS already
   barrier();
   for (int t = 0; t < nk; ++t) {
     const int64_t k0 = kbeg + int64_t(t) * kBK;
@@ -337,13 +337,13 @@ __device__ void partial_any(const ProblemArgs& p, const WeightArgs& w, int proj,
   }
 }
 
-template <bool INT4>
+template <bool INT4, bool INORM>
 __device__ __forceinline__ void partial_dispatch(const ProblemArgs& p, const WeightArgs& w, int proj, int hh,
                                                  int kt0, int nk, const uint16_t* xs, uint32_t xs_lds,
                                                  f32x4_t (&acc)[4]) {
   switch (nk) {
 #define MQK_DEC_CASE(n) \
-  case n: partial_fixed<INT4, n>(p, w, proj, hh, kt0, xs, xs_lds, acc); break;
+  case n: partial_fixed<INT4, INORM, n>(p, w, proj, hh, kt0, xs, xs_lds, acc); break;
     MQK_DEC_CASE(1) MQK_DEC_CASE(2) MQK_DEC_CASE(3) MQK_DEC_CASE(4)
     MQK_DEC_CASE(5) MQK_DEC_CASE(6) MQK_DEC_CASE(7) MQK_DEC_CASE(8)
     MQK_DEC_CASE(9) MQK_DEC_CASE(10) MQK_DEC_CASE(11) MQK_DEC_CASE(12)
@@ -353,7 +353,7 @@ __device__ __forceinline__ void partial_dispatch(const ProblemArgs& p, const Wei
   }
 }
 
-template <bool INT4>
+template <bool INT4, bool INORM>
 __global__ void __launch_bounds__(kDecThreads, 1)
 decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __restrict__ part,
               uint32_t* __restrict__ counters, int force_recompute) {
@@ -385,7 +385,7 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   int kt0, nk;
   split_range(split, splits, nkt, kt0, nk);
   f32x4_t acc[4];
-  partial_dispatch<INT4>(p, w, proj, hh, kt0, nk, xs, xs_lds, acc);
+  partial_dispatch<INT4, INORM>(p, w, proj, hh, kt0, nk, xs, xs_lds, acc);
   DECODE_TRACE(1)
 
   // ---- publish the partial in fragment order: part[split][head][wave][mb][lane] ----
@@ -480,7 +480,7 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
       int s_kt0, s_nk;
       split_range(s, splits, nkt, s_kt0, s_nk);
       __syncthreads();  // every wave is done with the x slice of the previous split
-      partial_any<INT4>(p, w, proj, hh, s_kt0, s_nk, xs, xs_lds, acc);
+      partial_any<INT4, INORM>(p, w, proj, hh, s_kt0, s_nk, xs, xs_lds, acc);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) sum[mb] += acc[mb];
     }
@@ -618,12 +618,10 @@ hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, co
   if (p.in_gamma && (p.K / 8 > int64_t(kGamPerThread) * kDecThreads ||
                      kDecRows * kDecKc * 2 + 16 + dyn > 160 * 1024 || !a16(p.in_gamma)))
     return hipErrorInvalidValue;
-  if (int4)
-    hipLaunchKernelGGL(decode_kernel<true>, grid, dim3(kDecThreads), dyn, stream, p, w, e, splits, part, counters,
-                       fr);
-  else
-    hipLaunchKernelGGL(decode_kernel<false>, grid, dim3(kDecThreads), dyn, stream, p, w, e, splits, part,
-                       counters, fr);
+  // (the input norm is a template switch: the plain kernels carry none of its code)
+  auto* kernel = int4 ? (p.in_gamma ? decode_kernel<true, true> : decode_kernel<true, false>)
+                      : (p.in_gamma ? decode_kernel<false, true> : decode_kernel<false, false>);
+  hipLaunchKernelGGL(kernel, grid, dim3(kDecThreads), dyn, stream, p, w, e, splits, part, counters, fr);
   return hipGetLastError();
 }
 
