@@ -374,8 +374,15 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
 
   for (int kt = 0; kt < nkt; ++kt) {
     const int ahead = min(NS - 2, nkt - 1 - kt);  // stages already issued after kt
+#ifdef MQK_TILE_TRACE2  // diagnostic build: per-wave timestamps around the wait, stages 8..22
+    if (g_tile_trace && lane == 0 && kt >= 8 && kt < 23)
+      g_tile_trace[blockIdx.x * 256 + (kt - 8) * 16 + wave * 2] = __builtin_amdgcn_s_memrealtime();
+#endif
     wait_stage<NS, S::kLoadsPerWave>(ahead);
-#ifdef MQK_TILE_TRACE  // diagnostic build: per-stage timestamps of wave 0 of each workgroup
+#ifdef MQK_TILE_TRACE2
+    if (g_tile_trace && lane == 0 && kt >= 8 && kt < 23)
+      g_tile_trace[blockIdx.x * 256 + (kt - 8) * 16 + wave * 2 + 1] = __builtin_amdgcn_s_memrealtime();
+#elif defined(MQK_TILE_TRACE)  // diagnostic build: per-stage timestamps of wave 0 of each workgroup
     if (g_tile_trace && tid == 0 && kt < 126) g_tile_trace[blockIdx.x * 256 + 2 * kt] = __builtin_amdgcn_s_memrealtime();
 #endif
     if (in_norm) {  // this wave's x chunks of stage kt have landed: normalise them in place
@@ -386,7 +393,7 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     barrier();
-#ifdef MQK_TILE_TRACE
+#if defined(MQK_TILE_TRACE) && !defined(MQK_TILE_TRACE2)
     if (g_tile_trace && tid == 0 && kt < 126) g_tile_trace[blockIdx.x * 256 + 2 * kt + 1] = __builtin_amdgcn_s_memrealtime();
 #endif
     if (kt + NS - 1 < nkt) issue(kt + NS - 1);
@@ -418,12 +425,12 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
     }
   }
   barrier();  // every wave is done with the ring; the epilogue reuses the LDS
-#ifdef MQK_TILE_TRACE
+#if defined(MQK_TILE_TRACE) && !defined(MQK_TILE_TRACE2)
   if (g_tile_trace && tid == 0) g_tile_trace[blockIdx.x * 256 + 252] = __builtin_amdgcn_s_memrealtime();
 #endif
 
   tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, cslot, ht, m0, p, e, smem);
-#ifdef MQK_TILE_TRACE
+#if defined(MQK_TILE_TRACE) && !defined(MQK_TILE_TRACE2)
   if (g_tile_trace && tid == 0) g_tile_trace[blockIdx.x * 256 + 253] = __builtin_amdgcn_s_memrealtime();
 #endif
 }
