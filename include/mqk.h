@@ -255,6 +255,9 @@ int mqk_fused_qkv_rope_ex_w4a16(const mqk_bf16* x, const int32_t* qw_q, const vo
  *   "decode_splits"  0 = auto, otherwise the split-K factor of the decode kernel (1..16,
  *                    at most 16 64-wide k tiles per split; otherwise the tile kernel runs)
  *   "group_m"        row tiles per tile-ordering group of the tile kernel (default 8)
+ *   "tail_split"     1 (default): when the last, partial row tile of a prefill holds at most 64
+ *                    rows and would cost a whole extra round of tiles over the CUs, those rows
+ *                    run on the split-K decode kernel in a second launch; 0: never
  *   "decode_force_recompute"  1: the decode kernel takes its recompute path (used when a
  *                    split ran on an unexpected XCD) for every head; for tests
  * Returns MQK_OK or MQK_ERR_BAD_OPTION.

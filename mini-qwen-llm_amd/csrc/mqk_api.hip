@@ -1,5 +1,6 @@
 // C ABI of libmqk.so: argument validation, kernel selection and launch.
 // Declarations and the contract of every entry point: include/mqk.h.
+#include <algorithm>
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -42,6 +43,7 @@ std::atomic<int64_t> g_prefill_tile{0};
 std::atomic<int64_t> g_decode_max_t{64};
 std::atomic<int64_t> g_decode_splits{0};
 std::atomic<int64_t> g_group_m{8};
+std::atomic<int64_t> g_tail_split{1};
 
 constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace (per head)
 
@@ -93,20 +95,64 @@ bool epilogue_aligned(const EpilogueArgs& e) {
   return aligned16(e.q_gamma) && aligned16(e.k_gamma) && aligned16(e.cos) && aligned16(e.sin);
 }
 
+constexpr int64_t kCus = 256;  // MI355X compute units: one pipelined tile per CU at a time
+
+// How a call's T tokens are split over kernels.  T <= 64: the split-K decode
+// kernel alone.  Otherwise a tile kernel; when the rows of its last, partial
+// row tile (at most 64) would cost a whole extra round of tiles over the CUs,
+// those rows go to the decode kernel in a second launch instead (e.g. 8214
+// tokens in 256-row tiles: three full rounds plus 22 rows).
+struct Plan {
+  const TileVariant* v = nullptr;  // tile variant (null: decode only)
+  int64_t tail = 0;                // rows run by the decode kernel after the tile rows
+  int splits = 0;                  // decode kernel split-K factor (0: no decode launch)
+};
+
+Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned) {
+  Plan pl;
+  if (use_decode(M) && aligned) {
+    pl.splits = decode_splits_for(M, K, n_tiles, int(g_decode_splits.load()));
+    if (pl.splits > 0) {
+      pl.tail = M;
+      return pl;
+    }
+  }
+  pl.v = choose_tile_variant(int(g_prefill_tile.load()), M, n_tiles, int4);
+  if (!pl.v || !g_tail_split.load() || !aligned || M <= 64) return pl;
+  const int64_t r = M % pl.v->bm;
+  if (r == 0 || r > 64 || !use_decode(r)) return pl;
+  const int64_t ct = n_tiles / pl.v->hpt;
+  const int64_t rounds_all = ((M + pl.v->bm - 1) / pl.v->bm * ct + kCus - 1) / kCus;
+  const int64_t rounds_main = ((M - r) / pl.v->bm * ct + kCus - 1) / kCus;
+  if (rounds_main >= rounds_all) return pl;
+  const int splits = decode_splits_for(r, K, n_tiles, int(g_decode_splits.load()));
+  if (splits > 0) {
+    pl.tail = r;
+    pl.splits = splits;
+  }
+  return pl;
+}
+
 // Common launcher of the fused op (bf16 or int4 weights).  With an input norm
 // (p.in_gamma set, epsilon in_eps), the per-token scales go to the workspace
 // after the decode kernel's region and are computed by a pre-pass first.
 int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& e, float in_eps,
               void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (p.M == 0) return ok();
-  const int splits = use_decode(p.M) && epilogue_aligned(e)
-                         ? decode_splits_for(p.M, p.K, p.n_tiles, int(g_decode_splits.load()))
-                         : 0;
+  Plan pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e));
+  if (!pl.v && pl.splits == 0)
+    return fail(MQK_ERR_BAD_OPTION, "prefill_tile variant %lld cannot run this problem (%d heads%s)",
+                (long long)g_prefill_tile.load(), p.n_tiles, int4 ? ", int4 weights" : "");
   // (the decode kernel's arrival counters open every workspace and must stay zero,
   // so the scales never start before them, whichever kernel runs this call)
-  const size_t base = splits > 0 ? decode_workspace_bytes(p.n_tiles, splits) : decode_counter_bytes();
+  size_t base = pl.splits > 0 ? decode_workspace_bytes(p.n_tiles, pl.splits) : decode_counter_bytes();
+  if (pl.v && pl.splits > 0 && (!workspace || ws_bytes < align_up(base, 256))) {
+    pl.tail = 0;  // a workspace sized without the tail launch: run the tile kernel on every row
+    pl.splits = 0;
+    base = decode_counter_bytes();
+  }
   const size_t scale_off = align_up(base, 256);
-  const size_t need = p.in_gamma ? scale_off + size_t(p.M) * sizeof(float) : (splits > 0 ? base : 0);
+  const size_t need = p.in_gamma ? scale_off + size_t(p.M) * sizeof(float) : (pl.splits > 0 ? base : 0);
   if (need > 0 && (!workspace || ws_bytes < need))
     return fail(MQK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given%s", need, ws_bytes,
                 workspace ? "" : " (NULL)");
@@ -116,17 +162,31 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
     if (st != MQK_OK) return st;
     p.in_scale = scale;
   }
-  if (splits > 0)
-    return hip_status(launch_decode(int4, p, w, e, splits, workspace, stream), "decode kernel launch");
-  const TileVariant* v = choose_tile_variant(int(g_prefill_tile.load()), p.M, p.n_tiles, int4);
-  if (!v) return fail(MQK_ERR_BAD_OPTION, "prefill_tile variant %lld cannot run this problem (%d heads%s)",
-                      (long long)g_prefill_tile.load(), p.n_tiles, int4 ? ", int4 weights" : "");
-  // The pipelined variants (ids >= 10) read every operand with 16-byte direct loads,
-  // and with an input norm hold gamma in LDS next to their ring.
-  if (v->id >= 10 && (!(epilogue_aligned(e) && (!int4 || int4_aligned(w))) ||
-                      (p.in_gamma && tile_dma_lds_bytes(v->id) + p.K * 2 > 160 * 1024)))
-    v = choose_tile_variant(p.n_tiles % 2 == 0 ? 4 : 1, p.M, p.n_tiles, int4);
-  return hip_status(launch_tile(*v, int4, p, w, e, int(g_group_m.load()), stream), "tile kernel launch");
+  if (pl.v) {
+    const TileVariant* v = pl.v;
+    // The pipelined variants (ids >= 10) read every operand with 16-byte direct loads,
+    // and with an input norm hold gamma in LDS next to their ring.
+    if (v->id >= 10 && (!(epilogue_aligned(e) && (!int4 || int4_aligned(w))) ||
+                        (p.in_gamma && tile_dma_lds_bytes(v->id) + p.K * 2 > 160 * 1024)))
+      v = choose_tile_variant(p.n_tiles % 2 == 0 ? 4 : 1, p.M, p.n_tiles, int4);
+    ProblemArgs pm = p;
+    pm.M = p.M - pl.tail;
+    const int st = hip_status(launch_tile(*v, int4, pm, w, e, int(g_group_m.load()), stream), "tile kernel launch");
+    if (st != MQK_OK || pl.tail == 0) return st;
+  }
+  // the decode kernel on the last pl.tail rows (all of them when there is no tile launch)
+  const int64_t t0 = p.M - pl.tail;
+  ProblemArgs pt = p;
+  pt.M = pl.tail;
+  pt.x = p.x + t0 * p.K;
+  if (p.in_scale) pt.in_scale = p.in_scale + t0;
+  EpilogueArgs et = e;
+  et.t0 = t0;
+  auto shift = [&](uint16_t* ptr, int heads) { return ptr ? ptr + t0 * heads * kHeadDim : ptr; };
+  et.q = shift(e.q, e.Hq);
+  et.k = shift(e.k, e.Hkv);
+  et.v = shift(e.v, e.Hkv);
+  return hip_status(launch_decode(int4, pt, w, et, pl.splits, workspace, stream), "decode kernel launch");
 }
 
 }  // namespace
@@ -152,10 +212,14 @@ const char* mqk_error_string(int status) {
 const char* mqk_last_error_detail(void) { return g_detail; }
 
 size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden) {
-  if (T <= 0 || Hq <= 0 || Hkv <= 0 || hidden <= 0 || hidden % kBK != 0 || !use_decode(T)) return 0;
+  if (T <= 0 || Hq <= 0 || Hkv <= 0 || hidden <= 0 || hidden % kBK != 0) return 0;
   const int tiles = Hq + 2 * Hkv;
-  const int splits = decode_splits_for(T, hidden, tiles, int(g_decode_splits.load()));
-  return splits > 0 ? decode_workspace_bytes(tiles, splits) : 0;
+  size_t n = 0;
+  for (int int4 = 0; int4 < 2; ++int4) {  // the same size serves both weight formats
+    const Plan pl = plan_fused(int4, T, hidden, tiles, true);
+    if (pl.splits > 0) n = std::max(n, decode_workspace_bytes(tiles, pl.splits));
+  }
+  return n;
 }
 
 size_t mqk_fused_qkv_rope_ex_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden,
@@ -481,6 +545,9 @@ int mqk_set_option(const char* name, int64_t value) {
   } else if (!strcmp(name, "tile_trace")) {  // diagnostic builds only
     set_tile_trace(reinterpret_cast<void*>(value));
 #endif
+  } else if (!strcmp(name, "tail_split")) {
+    if (value != 0 && value != 1) return fail(MQK_ERR_BAD_OPTION, "tail_split must be 0 or 1");
+    g_tail_split = value;
   } else if (!strcmp(name, "group_m")) {
     if (value < 1 || value > 1024) return fail(MQK_ERR_BAD_OPTION, "group_m must be in [1, 1024]");
     g_group_m = value;
@@ -496,6 +563,7 @@ int64_t mqk_get_option(const char* name) {
   if (!strcmp(name, "decode_max_t")) return g_decode_max_t.load();
   if (!strcmp(name, "decode_splits")) return g_decode_splits.load();
   if (!strcmp(name, "group_m")) return g_group_m.load();
+  if (!strcmp(name, "tail_split")) return g_tail_split.load();
   if (!strcmp(name, "decode_force_recompute")) return g_decode_force_recompute;
   return -1;
 }

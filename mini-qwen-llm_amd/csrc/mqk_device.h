@@ -122,6 +122,7 @@ __device__ __forceinline__ u32x4_t input_norm8(const u32x4_t& xv, float scale, c
 // (reference fused_qkv_rope.py:109), positions[t] (:107), or the varlen position.
 template <class E>
 __device__ __forceinline__ int64_t rope_row(const E& e, int64_t t) {
+  t += e.t0;  // the launch's first row is token t0 of the call
   int64_t p;
   if (e.cu_seqlens) {
     int64_t s;
@@ -140,6 +141,7 @@ __device__ __forceinline__ int64_t rope_row(const E& e, int64_t t) {
 template <class E>
 __device__ __forceinline__ int64_t paged_slot(const E& e, int64_t t) {
   if (!e.k_cache) return -1;
+  t += e.t0;
   int64_t seq, pos;
   if (e.cu_seqlens && !(e.kv_seq && e.kv_pos)) {
     varlen_locate(e, t, seq, pos);

@@ -55,6 +55,10 @@ struct EpilogueArgs {
   const int32_t* cu_seqlens;
   const int32_t* seq_pos0;
   int64_t n_seqs;
+  // Token index of the launch's row 0 within the call (a call's tokens may be
+  // split over two launches); positions, slots and varlen offsets are indexed by
+  // the call's token index, outputs and x by the launch's rows.
+  int64_t t0;
 };
 
 struct ProblemArgs {
