@@ -282,6 +282,22 @@ __device__ __forceinline__ void wait_vm_n(int n) {
   }
 }
 
+// Sum over each aligned group of 8 lanes, returned to all 8, with DPP lane
+// moves (no LDS round trip): the xor-1 and xor-2 butterflies as quad
+// permutations, then the other quad of the group via the half-row mirror.
+// Every lane adds the same pairs as the xor-1/2/4 butterfly, so the result is
+// the same bit for bit.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float sum8_lanes(float v) {
+  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_move<0x141>(v);  // row_half_mirror: lane i <-> 7 - i within 8
+  return v;
+}
+
 __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 }  // namespace mqk

@@ -516,9 +516,7 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss += lo[i] * lo[i] + hi[i] * hi[i];
-    ss += __shfl_xor(ss, 1);
-    ss += __shfl_xor(ss, 2);
-    ss += __shfl_xor(ss, 4);
+    ss = sum8_lanes(ss);
     const float rms = rsqrtf(ss * (1.0f / float(kHeadDim)) + e.eps);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {

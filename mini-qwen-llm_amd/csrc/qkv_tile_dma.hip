@@ -183,6 +183,19 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
     const int head = ht * NH + j;
     int proj, hh;
     split_head(head, e.Hq, e.Hkv, proj, hh);
+    // this head's gamma pairs in fp32, converted once for all its row passes
+    // (with up to two passes per head; with more, the 16 extra registers spill)
+    constexpr bool kHoistGamma = kPasses <= 2;
+    float g1[8], g2[8];
+    if constexpr (kHoistGamma) {
+      const u32x4_t* g = proj == 0 ? gq : gk;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int wd = i >> 1, sh = (i & 1) * 16;
+        g1[i] = bf16_to_f32((g[0][wd] >> sh) & 0xFFFFu);
+        g2[i] = bf16_to_f32((g[1][wd] >> sh) & 0xFFFFu);
+      }
+    }
 #pragma unroll
     for (int q = 0; q < kPasses; ++q) {
       const int r0 = (tid >> 3) + q * kRowStep;
@@ -201,9 +214,7 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) ss += lo[i] * lo[i] + hi[i] * hi[i];
-        ss += __shfl_xor(ss, 1);
-        ss += __shfl_xor(ss, 2);
-        ss += __shfl_xor(ss, 4);
+        ss = sum8_lanes(ss);
         const float rms = rsqrtf(ss * (1.0f / float(kHeadDim)) + e.eps);
         u32x4_t c2[2], s2[2];
         if constexpr (kPreload) {
@@ -215,8 +226,10 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int wd = i >> 1, sh = (i & 1) * 16;
-          const float x1n = lo[i] * rms * bf16_to_f32((g[0][wd] >> sh) & 0xFFFFu);
-          const float x2n = hi[i] * rms * bf16_to_f32((g[1][wd] >> sh) & 0xFFFFu);
+          const float gl = kHoistGamma ? g1[i] : bf16_to_f32((g[0][wd] >> sh) & 0xFFFFu);
+          const float gh = kHoistGamma ? g2[i] : bf16_to_f32((g[1][wd] >> sh) & 0xFFFFu);
+          const float x1n = lo[i] * rms * gl;
+          const float x2n = hi[i] * rms * gh;
           const float co1 = bf16_to_f32((c2[0][wd] >> sh) & 0xFFFFu);
           const float co2 = bf16_to_f32((c2[1][wd] >> sh) & 0xFFFFu);
           const float si1 = bf16_to_f32((s2[0][wd] >> sh) & 0xFFFFu);
