@@ -355,3 +355,19 @@ def test_config4_30b_a3b_long_prefill(device):
     ref = case.oracle(token_idx=idx)
     out = tuple(t.reshape(8192, *t.shape[2:])[torch.as_tensor(idx)] for t in (q, k, v))
     _check(out, tuple(r[0] for r in ref), "C4 30B-A3B S=8192")
+
+
+def test_large_t_64bit_offsets(device):
+    """Maximum-size addressing: T = 270000 tokens with 32 query heads puts q's
+    byte offsets past 2^31 (t * Hq * 128 * 2), so every output, x and table index
+    must be 64-bit.  Checked against the oracle on the first and last tokens."""
+    T, hidden, Hq, Hkv = 270000, 64, 32, 4
+    pos = (torch.arange(T) % 4096).to(torch.int32)
+    case = Case(1, T, hidden, Hq, Hkv, seed=11, rows=4096, positions=pos)
+    q, k, v = _run(case, device)
+    torch.cuda.synchronize()
+    assert q.numel() * q.element_size() > 2 ** 31
+    idx = np.concatenate([np.arange(0, 8), np.arange(T - 24, T)])
+    ref = case.oracle(token_idx=idx)
+    out = tuple(t.reshape(T, *t.shape[2:])[torch.as_tensor(idx)] for t in (q, k, v))
+    _check(out, tuple(r[0] for r in ref), "T=270000")
