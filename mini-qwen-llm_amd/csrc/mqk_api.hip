@@ -44,6 +44,7 @@ std::atomic<int64_t> g_decode_max_t{64};
 std::atomic<int64_t> g_decode_splits{0};
 std::atomic<int64_t> g_group_m{8};
 std::atomic<int64_t> g_tail_split{1};
+std::atomic<int64_t> g_decode_blocks{16};  // most 64-row decode launches for one call (T > 64)
 
 constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace (per head)
 
@@ -108,10 +109,28 @@ struct Plan {
   int splits = 0;                  // decode kernel split-K factor (0: no decode launch)
 };
 
-Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned) {
+Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, bool allow_blocks = true) {
   Plan pl;
   if (use_decode(M) && aligned) {
     pl.splits = decode_splits_for(M, K, n_tiles, int(g_decode_splits.load()));
+    if (pl.splits > 0) {
+      pl.tail = M;
+      return pl;
+    }
+  }
+  // A few 64-row blocks: consecutive decode launches, each streaming the weights
+  // over every CU, can beat a tile launch whose few tiles leave most CUs idle
+  // and stream their panels at a single CU's rate.  Measured at hidden 4096:
+  // a bf16 decode launch ~17.6 us against ~75 us for the best tile variant at
+  // T = 65..512; int4 ~16 us per launch against ~135 us.  The models below
+  // follow those measurements (and hidden 2048: ~12 us against ~42 us).
+  const int64_t nblk = (M + 63) / 64;
+  const double w_bytes = double(n_tiles) * kHeadDim * double(K) * (int4 ? 0.5 : 2.0);
+  const double dec_us = int4 ? 4.0 + 3.0 * double(K) / 1024.0 : 8.0 + w_bytes / 5.0e6;
+  const double tile_us = double(K) / 64.0 * (int4 ? 2.1 : 1.15) + 5.0;
+  if (allow_blocks && aligned && M > 64 && g_prefill_tile.load() == 0 && g_decode_max_t.load() >= 64 &&
+      nblk <= g_decode_blocks.load() && double(nblk) * dec_us <= tile_us) {
+    pl.splits = decode_splits_for(64, K, n_tiles, int(g_decode_splits.load()));
     if (pl.splits > 0) {
       pl.tail = M;
       return pl;
@@ -146,6 +165,11 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
   // (the decode kernel's arrival counters open every workspace and must stay zero,
   // so the scales never start before them, whichever kernel runs this call)
   size_t base = pl.splits > 0 ? decode_workspace_bytes(p.n_tiles, pl.splits) : decode_counter_bytes();
+  if (!pl.v && p.M > 64 && (!workspace || ws_bytes < align_up(base, 256))) {
+    // decode blocks planned, but a workspace sized without them: the tile kernel
+    pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), false);
+    base = pl.splits > 0 ? decode_workspace_bytes(p.n_tiles, pl.splits) : decode_counter_bytes();
+  }
   if (pl.v && pl.splits > 0 && (!workspace || ws_bytes < align_up(base, 256))) {
     pl.tail = 0;  // a workspace sized without the tail launch: run the tile kernel on every row
     pl.splits = 0;
@@ -174,19 +198,23 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
     const int st = hip_status(launch_tile(*v, int4, pm, w, e, int(g_group_m.load()), stream), "tile kernel launch");
     if (st != MQK_OK || pl.tail == 0) return st;
   }
-  // the decode kernel on the last pl.tail rows (all of them when there is no tile launch)
-  const int64_t t0 = p.M - pl.tail;
-  ProblemArgs pt = p;
-  pt.M = pl.tail;
-  pt.x = p.x + t0 * p.K;
-  if (p.in_scale) pt.in_scale = p.in_scale + t0;
-  EpilogueArgs et = e;
-  et.t0 = t0;
-  auto shift = [&](uint16_t* ptr, int heads) { return ptr ? ptr + t0 * heads * kHeadDim : ptr; };
-  et.q = shift(e.q, e.Hq);
-  et.k = shift(e.k, e.Hkv);
-  et.v = shift(e.v, e.Hkv);
-  return hip_status(launch_decode(int4, pt, w, et, pl.splits, workspace, stream), "decode kernel launch");
+  // the decode kernel on the last pl.tail rows (all of them when there is no tile
+  // launch), 64 rows per launch; the launches share the workspace in stream order
+  for (int64_t t0 = p.M - pl.tail; t0 < p.M; t0 += 64) {
+    ProblemArgs pt = p;
+    pt.M = std::min<int64_t>(64, p.M - t0);
+    pt.x = p.x + t0 * p.K;
+    if (p.in_scale) pt.in_scale = p.in_scale + t0;
+    EpilogueArgs et = e;
+    et.t0 = t0;
+    auto shift = [&](uint16_t* ptr, int heads) { return ptr ? ptr + t0 * heads * kHeadDim : ptr; };
+    et.q = shift(e.q, e.Hq);
+    et.k = shift(e.k, e.Hkv);
+    et.v = shift(e.v, e.Hkv);
+    const int st = hip_status(launch_decode(int4, pt, w, et, pl.splits, workspace, stream), "decode kernel launch");
+    if (st != MQK_OK) return st;
+  }
+  return ok();
 }
 
 }  // namespace
@@ -548,6 +576,9 @@ int mqk_set_option(const char* name, int64_t value) {
   } else if (!strcmp(name, "tail_split")) {
     if (value != 0 && value != 1) return fail(MQK_ERR_BAD_OPTION, "tail_split must be 0 or 1");
     g_tail_split = value;
+  } else if (!strcmp(name, "decode_blocks")) {
+    if (value < 0 || value > 64) return fail(MQK_ERR_BAD_OPTION, "decode_blocks must be in [0, 64]");
+    g_decode_blocks = value;
   } else if (!strcmp(name, "group_m")) {
     if (value < 1 || value > 1024) return fail(MQK_ERR_BAD_OPTION, "group_m must be in [1, 1024]");
     g_group_m = value;
@@ -564,6 +595,7 @@ int64_t mqk_get_option(const char* name) {
   if (!strcmp(name, "decode_splits")) return g_decode_splits.load();
   if (!strcmp(name, "group_m")) return g_group_m.load();
   if (!strcmp(name, "tail_split")) return g_tail_split.load();
+  if (!strcmp(name, "decode_blocks")) return g_decode_blocks.load();
   if (!strcmp(name, "decode_force_recompute")) return g_decode_force_recompute;
   return -1;
 }

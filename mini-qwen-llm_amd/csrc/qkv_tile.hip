@@ -434,10 +434,13 @@ const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles,
   struct Cand { int id; float speed; };
   // (per-tile rates measured on MI355X: 64-wide k stages (16, 17, 18) beat 32-wide
   // ones; 128x384 wins when its tiles fill the chip, 256x256 otherwise)
+  // The register-staged variants (1-5) are not candidates: with few tiles (small
+  // T) their per-tile rate collapses (T = 65..1024 measured 3-6x slower than the
+  // pipelined variants), so they serve only as the fallback for shapes no
+  // pipelined variant tiles and for explicit requests.
   static const Cand bf16_cands[] = {{16, 1.00f}, {18, 1.27f}, {17, 1.26f}, {11, 0.94f}, {10, 1.19f},
-                                    {13, 0.75f}, {12, 0.75f}, {1, 0.50f}};
-  static const Cand int4_cands[] = {{31, 1.00f}, {4, 0.94f}, {5, 0.78f}, {30, 0.75f}, {2, 0.63f},
-                                    {3, 0.61f}, {32, 0.54f}, {1, 0.51f}};
+                                    {13, 0.75f}, {12, 0.75f}};
+  static const Cand int4_cands[] = {{31, 1.00f}, {30, 0.75f}, {32, 0.54f}};
   const Cand* cands = int4 ? int4_cands : bf16_cands;
   const int ncand = int(int4 ? sizeof(int4_cands) / sizeof(int4_cands[0]) : sizeof(bf16_cands) / sizeof(bf16_cands[0]));
   const int64_t cus = 256;

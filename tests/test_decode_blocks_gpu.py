@@ -1,0 +1,117 @@
+"""GPU tests of the decode-block plan.
+
+A call of 64 < T tokens whose tile launch would leave most CUs idle (few row
+tiles, long K) runs instead as consecutive 64-row launches of the split-K decode
+kernel, each streaming the weights over every CU; row 0 of launch i is the call's
+token 64 i, so positions, cache slots and varlen offsets keep the call's token
+index.  Each block must equal the decode kernel run on those 64 rows alone, bit
+for bit; the whole call must match the oracle and, within the acceptance bar,
+the tile path (option decode_blocks = 0).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import HEAD_DIM, Case, f32
+from oracle import qkv_rope_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+D = HEAD_DIM
+MAX_ABS, REL_L2 = 2e-2, 1e-2
+
+
+def _with_option(name, value, fn):
+    import mqk
+    old = mqk.get_option(name)
+    try:
+        mqk.set_option(name, value)
+        out = fn()
+        torch.cuda.synchronize()
+        return out
+    finally:
+        mqk.set_option(name, old)
+
+
+def _close(a, b, label):
+    for name, x, y in zip("qkv", a, b):
+        x, y = f32(x), f32(y)
+        ma, rl = orc.max_abs(x, y), orc.rel_l2(x, y)
+        assert ma <= MAX_ABS and rl <= REL_L2, f"{label} {name}: {ma} {rl}"
+
+
+@pytest.mark.parametrize("T", [65, 128, 200, 256])
+def test_decode_blocks_bf16(T, device):
+    import mqk
+    pos = torch.randint(0, 8192, (T,), generator=torch.Generator().manual_seed(T), dtype=torch.int32)
+    case = Case(1, T, 4096, 32, 8, seed=1100 + T, rows=8192, positions=pos)
+    x, wq, wk, wv, gq, gk, cos, sin, p = case.args(device)
+    out = mqk.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin, p)
+    torch.cuda.synchronize()
+    for t0 in range(0, T, 64):
+        alone = mqk.fused_qkv_rope(x[:, t0:t0 + 64].contiguous(), wq, wk, wv, gq, gk, cos, sin, p[t0:t0 + 64])
+        torch.cuda.synchronize()
+        for a, b in zip(out, alone):
+            assert torch.equal(a[:, t0:t0 + 64], b), f"T={T}: block at {t0} differs from the decode kernel alone"
+    tile = _with_option("decode_blocks", 0, lambda: mqk.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin, p))
+    _close(out, tile, f"T={T} blocks vs tile")
+    idx = np.unique(np.concatenate([np.arange(0, 4), np.arange(60, 70), np.arange(T - 4, T)]).clip(0, T - 1))
+    ref = case.oracle(token_idx=idx)
+    for name, o, r in zip("qkv", out, ref):
+        o = f32(o)[0, idx].reshape(r.shape)
+        assert orc.max_abs(o, r) <= MAX_ABS and orc.rel_l2(o, r) <= REL_L2, f"T={T} {name} vs oracle"
+
+
+def test_decode_blocks_w4a16(device):
+    import mqk
+    from test_w4a16_gpu import _check_w4, _int4_case
+    T, hidden, Hq, Hkv = 200, 1024, 16, 8
+    x, projs, gq, gk = _int4_case(1, T, hidden, Hq, Hkv, seed=1201, scale_dtype=torch.float16)
+    c, s = mqk.rope_tables(D, 4096)
+    cos, sin = c.bfloat16(), s.bfloat16()
+    pos = torch.randint(0, 4096, (T,), generator=torch.Generator().manual_seed(7), dtype=torch.int32)
+    dp = [tuple(t.to(device) for t in pr) for pr in projs]
+    xd, args = x.to(device), (gq.to(device), gk.to(device), cos.to(device), sin.to(device))
+    out = mqk.fused_qkv_rope_w4a16(xd, *dp, *args, pos.to(device))
+    torch.cuda.synchronize()
+    for t0 in range(0, T, 64):
+        alone = mqk.fused_qkv_rope_w4a16(xd[:, t0:t0 + 64].contiguous(), *dp, *args, pos[t0:t0 + 64].to(device))
+        torch.cuda.synchronize()
+        for a, b in zip(out, alone):
+            assert torch.equal(a[:, t0:t0 + 64], b), f"int4 block at {t0} differs from the decode kernel alone"
+    _check_w4(out, x, projs, gq, gk, cos, sin, Hq, Hkv, pos.numpy(), "w4a16 decode blocks")
+
+
+def test_decode_blocks_varlen_paged_input_norm(device):
+    """Varlen offsets, paged-cache slots and the input-norm scales follow the
+    call's token index across block launches: equal to the tile path within the
+    bar, with every cache slot holding the returned K/V."""
+    import mqk
+    from test_paged_gpu import _block_table, _caches, _check_cache, _expected_slots
+    lens = np.array([70, 0, 45, 35])
+    T, hidden, Hq, Hkv, bs = int(lens.sum()), 4096, 32, 8, 16
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    start = np.array([5, 0, 300, 17])
+    seq, posv = orc.varlen_positions(cu, start)
+    case = Case(1, T, hidden, Hq, Hkv, seed=1300, rows=4096)
+    x, wq, wk, wv, gq, gk, cos, sin, _ = case.args(device)
+    x = x.reshape(T, hidden)
+    g_in = (1 + 0.3 * torch.randn(hidden, generator=torch.Generator().manual_seed(9))).bfloat16().to(device)
+    bt = _block_table(len(lens), 32, 256, seed=3)
+    cu_d, st_d = torch.from_numpy(cu).to(device), torch.from_numpy(start.astype(np.int32)).to(device)
+
+    def run():
+        kc, vc = _caches(256, bs, Hkv, device)
+        out = mqk.fused_qkv_rope_ex(x, wq, wk, wv, gq, gk, cos, sin, cu_seqlens=cu_d, seq_pos0=st_d,
+                                    input_norm_w=g_in, k_cache=kc, v_cache=vc, block_table=bt.to(device))
+        return out, kc, vc
+
+    (q, k, v), kc, vc = run()
+    torch.cuda.synchronize()
+    (qt, kt, vt), _, _ = _with_option("decode_blocks", 0, run)
+    _close((q, k, v), (qt, kt, vt), "varlen + paged + input norm, blocks vs tile")
+    slots = _expected_slots(seq, posv, bt.numpy(), bs)
+    _check_cache(kc, k, slots, "k cache")
+    _check_cache(vc, v, slots, "v cache")

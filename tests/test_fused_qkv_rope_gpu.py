@@ -123,12 +123,20 @@ def test_decode_mode_full_table(B, device):
     _check((q, k, v), case.oracle(), f"decode full-table B={B}")
 
 
+@pytest.mark.parametrize("blocks", [16, 0])
 @pytest.mark.parametrize("T", [63, 64, 65, 129, 200])
-def test_tile_boundaries(T, device):
-    """Token counts around the decode/tile-kernel switch and the 128-row tile."""
+def test_tile_boundaries(T, blocks, device):
+    """Token counts around the decode/tile-kernel switch and the 128-row tile,
+    with 64-row decode blocks allowed (the default) and off (tile kernel)."""
+    import mqk
     case = Case(1, T, 2048, 16, 4, seed=400 + T)
-    q, k, v = _run(case, device)
-    _check((q, k, v), case.oracle(), f"T={T}")
+    old = mqk.get_option("decode_blocks")
+    try:
+        mqk.set_option("decode_blocks", blocks)
+        q, k, v = _run(case, device)
+    finally:
+        mqk.set_option("decode_blocks", old)
+    _check((q, k, v), case.oracle(), f"T={T} decode_blocks={blocks}")
 
 
 def test_decode_and_tile_paths_agree(device):

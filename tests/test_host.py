@@ -117,10 +117,21 @@ def test_decode_needs_workspace(lib):
 
 
 def test_workspace_size(lib):
-    assert lib.mqk_fused_qkv_rope_workspace_size(512, 32, 8, 4096) == 0      # tile kernel
+    assert lib.mqk_fused_qkv_rope_workspace_size(2048, 32, 8, 4096) == 0     # tile kernel only
     assert lib.mqk_fused_qkv_rope_workspace_size(0, 32, 8, 4096) == 0
     n = lib.mqk_fused_qkv_rope_workspace_size(64, 32, 8, 4096)
     assert n >= 4096 + 48 * 64 * 128 * 4  # counters + at least one fp32 partial per head
+    # 64 < T: 64-row decode launches (bf16 up to T = 256 here, int4 up to 512) share one
+    # decode region; past them, the tile kernel needs none
+    assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == n
+    assert lib.mqk_fused_qkv_rope_workspace_size(512, 32, 8, 4096) == n     # the int4 plan
+    assert lib.mqk_fused_qkv_rope_workspace_size(1024, 32, 8, 4096) == 0
+    from mqk import _native
+    _native.set_option("decode_blocks", 0)
+    try:
+        assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == 0
+    finally:
+        _native.set_option("decode_blocks", 16)
 
 
 def test_w4a16_validation(lib):
@@ -149,7 +160,7 @@ def test_options_roundtrip(lib):
     from mqk import _native
     assert _native.get_option("decode_max_t") == 64
     for name, val in (("prefill_tile", 11), ("decode_max_t", 16), ("decode_splits", 4), ("group_m", 8),
-                      ("decode_force_recompute", 1)):
+                      ("decode_force_recompute", 1), ("decode_blocks", 3), ("tail_split", 0)):
         old = _native.get_option(name)
         _native.set_option(name, val)
         assert _native.get_option(name) == val
