@@ -163,6 +163,61 @@ def test_fused_w4a16(B, S, positions_mode, scale_dtype, device):
               f"w4a16 B={B} S={S}")
 
 
+def test_config5_w4a16_ragged_full_size(device):
+    """BASELINE config 5 at full size: Qwen3-8B dims (hidden 4096, 32/8 heads), AWQ
+    int4 weights with random nibbles U{0..15}, fp16 scales U(0.005, 0.02), random
+    zeros; 16 packed sequences of lengths U[1, 1024] starting at positions
+    U[0, 4096), read from an 8192-row table.  The tile launch and the decode-kernel
+    tail launch both run (T is not a multiple of 256).  Checked against the oracle
+    on 192 tokens: each sequence's first and last token plus a seeded sample."""
+    import mqk
+    hidden, Hq, Hkv = 4096, 32, 8
+    g = torch.Generator().manual_seed(4)
+    lens = torch.randint(1, 1025, (16,), generator=g)
+    starts = torch.randint(0, 4096, (16,), generator=g)
+    pos = torch.cat([s + torch.arange(int(n)) for s, n in zip(starts, lens)]).to(torch.int32)
+    T = int(lens.sum())
+    projs = []
+    for h in (Hq, Hkv, Hkv):
+        N = h * D
+        qw = torch.randint(-2**31, 2**31 - 1, (hidden // 8, N), generator=g, dtype=torch.int64).to(torch.int32)
+        sc = (0.005 + 0.015 * torch.rand(hidden // 128, N, generator=g)).half()
+        qz = torch.randint(-2**31, 2**31 - 1, (hidden // 128, N // 8), generator=g,
+                           dtype=torch.int64).to(torch.int32)
+        projs.append((qw, sc, qz))
+    x = torch.randn(1, T, hidden, generator=g).bfloat16()
+    gq = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    gk = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    c, s = mqk.rope_tables(D, 8192)
+    cos, sin = c.bfloat16(), s.bfloat16()
+    dp = [tuple(t.to(device) for t in p) for p in projs]
+    q, k, v = mqk.fused_qkv_rope_w4a16(x.to(device), *dp, gq.to(device), gk.to(device), cos.to(device),
+                                       sin.to(device), pos.to(device))
+    torch.cuda.synchronize()
+    assert q.shape == (1, T, Hq, D) and k.shape == (1, T, Hkv, D) and v.shape == (1, T, Hkv, D)
+    ends = torch.cumsum(lens, 0)
+    edge = torch.cat([ends - lens, ends - 1]).numpy()
+    rest = np.random.default_rng(4).choice(T, size=160, replace=False)
+    idx = np.unique(np.concatenate([edge, rest]))
+    ti = torch.as_tensor(idx)
+    out = tuple(t[0, ti].cpu()[None] for t in (q, k, v))
+    # q / k are normalised (rms ~ 1): the absolute bar of the other tests.  v is
+    # the plain projection, which with these int4 weights has rms ~ 5.5 and
+    # reaches |v| ~ 30, where one bf16 ulp is 0.125: its max-abs bar is the same
+    # one in units of rms(ref).
+    from oracle import qkv_rope_oracle as orc
+    for round_weight, bound in ((True, 2e-2), (False, 4e-2)):
+        ref = _oracle_w4a16(x[:, ti], projs, gq, gk, cos, sin, Hq, Hkv, pos.numpy()[idx], round_weight)
+        for name, o, r in zip("qkv", out, ref):
+            o = f32(o).reshape(r.shape).astype(np.float64)
+            scale = float(np.sqrt(np.mean(r ** 2))) if name == "v" else 1.0
+            ma, rl = orc.max_abs(o, r), orc.rel_l2(o, r)
+            print(f"  C5 T={T} {name} (bf16 weight ref={round_weight}): max_abs={ma:.5f} "
+                  f"(bar scale {scale:.2f}) rel_l2={rl:.2e}")
+            assert np.isfinite(o).all()
+            assert ma <= bound * scale and rl <= 1e-2, f"C5 {name}: {ma} {rl}"
+
+
 def test_fused_w4a16_accepts_modules(device):
     import mqk
     hidden, Hq, Hkv = 512, 4, 2
