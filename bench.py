@@ -19,6 +19,9 @@ fp32, numpy/BLAS) on the host for a bounded sample of the same workload.
 ``secondary`` reports the other BASELINE configurations (decode, long prefill,
 W4A16) with their own roofline fractions; the decode step rotates 8 copies of
 the weights (400 MB, more than the 256 MB Infinity Cache) so it reads HBM.
+Config 1 (the Qwen3-0.6B-shaped layer, B=1 x S=128, which the reference runs
+on the CPU in fp32) is reported as the op's bf16 GPU time next to the oracle's
+fp32 composition timed on the host.
 
 Synthetic data, seeded: x ~ N(0,1), W ~ N(0, 0.02), gammas 1 + N(0, 0.1),
 theta = 1e6 RoPE tables.  One GPU only (--gpus N>1 exits with a message).
@@ -175,6 +178,31 @@ def cpu_baseline(budget_s=12.0):
                       f"{med * 1e3:.1f} ms/rep"}
 
 
+def cpu_config1(reps=20):
+    """BASELINE config 1 on the host: the Qwen3-0.6B-shaped layer (hidden 1024,
+    16/8 heads, B=1, S=128) through the oracle's unfused fp32 composition, the
+    reference's own CPU-runnable case.  Returns (tokens/s, ms per call)."""
+    import numpy as np
+    from oracle import qkv_rope_oracle as orc
+    rng = np.random.default_rng(0)
+    S, hidden, Hq, Hkv = 128, 1024, 16, 8
+    x = rng.standard_normal((1, S, hidden), dtype=np.float32)
+    wq = rng.standard_normal((Hq * D, hidden), dtype=np.float32) * 0.02
+    wk = rng.standard_normal((Hkv * D, hidden), dtype=np.float32) * 0.02
+    wv = rng.standard_normal((Hkv * D, hidden), dtype=np.float32) * 0.02
+    gq = 1 + 0.1 * rng.standard_normal(D, dtype=np.float32)
+    gk = 1 + 0.1 * rng.standard_normal(D, dtype=np.float32)
+    cos, sin = orc.rope_tables(D, S)
+    orc.unfused_composition(x, wq, wk, wv, gq, gk, cos, sin)  # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        orc.unfused_composition(x, wq, wk, wv, gq, gk, cos, sin)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    return S / med, med * 1e3
+
+
 def load_traffic(name):
     f = ROOT / "profiles" / f"{name}.json"
     if f.exists():
@@ -309,6 +337,17 @@ def main(argv=None) -> int:
                                        "ms_per_step": round(ms5, 6), "bound": "mfma", "achieved_TFLOPs": round(a5, 2),
                                        "frac": round(a5 / PEAK_BF16_TFLOPS, 4)}
         log(f"[bench] config 5 W4A16 T={T5}: {ms5 * 1e3:.1f} us/step, {a5:.0f} TFLOP/s")
+        # config 1: the Qwen3-0.6B-shaped layer, B=1 x S=128 (the reference runs it on
+        # the CPU in fp32; here on the GPU in bf16, and the oracle's fp32 composition on the host)
+        ms1, _ = bench_prefill(128, 1, 128, 1024, 16, 8, 0, 200, 200, dev)
+        c1 = {"gpu_tokens_per_s": round(128 / (ms1 * 1e-3), 1), "gpu_ms_per_step": round(ms1, 6),
+              "gpu_dtype": "bf16"}
+        if not args.no_cpu:
+            ctps, cms = cpu_config1()
+            c1.update({"cpu_fp32_tokens_per_s": round(ctps, 1), "cpu_ms_per_call": round(cms, 3),
+                       "cpu_kind": "port (oracle unfused composition, numpy/BLAS)"})
+        sec["config1_qwen3_0p6b_s128"] = c1
+        log(f"[bench] config 1: {ms1 * 1e3:.1f} us/step on the GPU")
         result["secondary"] = sec
 
     if not args.no_cpu:
