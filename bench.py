@@ -13,9 +13,9 @@ stream the op launches on, bracketed by device synchronisation.
 ``roofline`` prices the dominant (only) kernel of a step: 2*T*hidden*N FLOP per
 launch / average launch duration, against the bf16 dense MFMA peak (2.5
 PFLOP/s).  ``traffic`` is filled from the committed rocprofv3 PMC summary in
-profiles/ when present.  ``cpu_baseline`` times the oracle's restatement of the
-reference's unfused composition (3 projections -> per-head RMSNorm -> RoPE,
-fp32, numpy/BLAS) on the host for a bounded sample of the same workload.
+profiles/ when present.  ``cpu_baseline`` times a torch fp32 restatement of the
+reference's unfused composition (3 projections -> per-head RMSNorm -> RoPE) on
+the host's cores for a bounded sample of the same workload.
 ``secondary`` reports the other BASELINE configurations (decode, long prefill,
 W4A16) with their own roofline fractions; the decode step rotates 8 copies of
 the weights (400 MB, more than the 256 MB Infinity Cache) so it reads HBM.
@@ -143,62 +143,71 @@ def bench_w4a16(hidden, Hq, Hkv, seed, steps, warmup, dev):
 
 
 def cpu_baseline(budget_s=12.0):
-    """Oracle restatement of the reference's unfused composition on the host, fp32.
+    """The reference's unfused composition on the host in fp32, with PyTorch.
 
-    Sample: one sequence of the headline workload (B=1, S=512 of the B=4 x S=512
-    batch; hidden 4096, 32/8 heads), repeated until ~budget_s of CPU time."""
+    oracle/torch_baseline.py restates tests/test_fused_qkv_rope.py:244-259 (three
+    projections -> per-head RMSNorm -> rotate-half RoPE) with torch CPU tensors,
+    on torch's intra-op thread pool (OMP_NUM_THREADS when set).  Sample: one
+    sequence of the headline workload (B=1, S=512 of the B=4 x S=512 batch; hidden
+    4096, 32/8 heads), repeated until ~budget_s of wall time, median reported."""
     import numpy as np
-    from threadpoolctl import threadpool_info
+    import torch
     from oracle import qkv_rope_oracle as orc
+    from oracle.torch_baseline import unfused_composition_torch
     rng = np.random.default_rng(0)
     S, hidden, Hq, Hkv = 512, 4096, 32, 8
-    x = orc.round_bf16(rng.standard_normal((1, S, hidden), dtype=np.float32))
-    wq = orc.round_bf16(rng.standard_normal((Hq * D, hidden), dtype=np.float32) * 0.02)
-    wk = orc.round_bf16(rng.standard_normal((Hkv * D, hidden), dtype=np.float32) * 0.02)
-    wv = orc.round_bf16(rng.standard_normal((Hkv * D, hidden), dtype=np.float32) * 0.02)
-    gq = orc.round_bf16(1 + 0.1 * rng.standard_normal(D, dtype=np.float32))
-    gk = orc.round_bf16(1 + 0.1 * rng.standard_normal(D, dtype=np.float32))
-    cos, sin = orc.rope_tables(D, S)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+    x = t(orc.round_bf16(rng.standard_normal((1, S, hidden), dtype=np.float32)))
+    wq = t(orc.round_bf16(rng.standard_normal((Hq * D, hidden), dtype=np.float32) * 0.02))
+    wk = t(orc.round_bf16(rng.standard_normal((Hkv * D, hidden), dtype=np.float32) * 0.02))
+    wv = t(orc.round_bf16(rng.standard_normal((Hkv * D, hidden), dtype=np.float32) * 0.02))
+    gq = t(orc.round_bf16(1 + 0.1 * rng.standard_normal(D, dtype=np.float32)))
+    gk = t(orc.round_bf16(1 + 0.1 * rng.standard_normal(D, dtype=np.float32)))
+    cos, sin = (t(a) for a in orc.rope_tables(D, S))
     times = []
-    t_start = time.perf_counter()
-    orc.unfused_composition(x, wq, wk, wv, gq, gk, cos, sin)  # warm-up
-    while True:
-        t0 = time.perf_counter()
-        orc.unfused_composition(x, wq, wk, wv, gq, gk, cos, sin)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s and len(times) >= 5:
-            break
+    with torch.inference_mode():
+        unfused_composition_torch(x, wq, wk, wv, gq, gk, cos, sin)  # warm-up
+        t_start = time.perf_counter()
+        while True:
+            t0 = time.perf_counter()
+            unfused_composition_torch(x, wq, wk, wv, gq, gk, cos, sin)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - t_start > budget_s and len(times) >= 5:
+                break
     med = sorted(times)[len(times) // 2]
-    threads = max([i.get("num_threads", 1) for i in threadpool_info()
-                   if i.get("user_api") == "blas"] or [1])
-    return {"value": round(S / med, 1), "unit": "tokens/s", "cores": int(threads),
+    return {"value": round(S / med, 1), "unit": "tokens/s", "cores": int(torch.get_num_threads()),
             "kind": "port",
-            "sample": f"oracle unfused fp32 composition (numpy/BLAS), B=1 x S=512 of the "
-                      f"B=4 x S=512 Qwen3-8B prefill, median of {len(times)} reps, "
-                      f"{med * 1e3:.1f} ms/rep"}
+            "sample": f"torch fp32 CPU restatement of the reference's unfused composition "
+                      f"(test_fused_qkv_rope.py:244-259), B=1 x S=512 of the B=4 x S=512 Qwen3-8B "
+                      f"prefill, median of {len(times)} reps, {med * 1e3:.1f} ms/rep"}
 
 
 def cpu_config1(reps=20):
     """BASELINE config 1 on the host: the Qwen3-0.6B-shaped layer (hidden 1024,
-    16/8 heads, B=1, S=128) through the oracle's unfused fp32 composition, the
-    reference's own CPU-runnable case.  Returns (tokens/s, ms per call)."""
+    16/8 heads, B=1, S=128) through the torch fp32 restatement of the reference's
+    unfused composition, the reference's own CPU-runnable case.  Returns
+    (tokens/s, ms per call)."""
     import numpy as np
+    import torch
     from oracle import qkv_rope_oracle as orc
+    from oracle.torch_baseline import unfused_composition_torch
     rng = np.random.default_rng(0)
     S, hidden, Hq, Hkv = 128, 1024, 16, 8
-    x = rng.standard_normal((1, S, hidden), dtype=np.float32)
-    wq = rng.standard_normal((Hq * D, hidden), dtype=np.float32) * 0.02
-    wk = rng.standard_normal((Hkv * D, hidden), dtype=np.float32) * 0.02
-    wv = rng.standard_normal((Hkv * D, hidden), dtype=np.float32) * 0.02
-    gq = 1 + 0.1 * rng.standard_normal(D, dtype=np.float32)
-    gk = 1 + 0.1 * rng.standard_normal(D, dtype=np.float32)
-    cos, sin = orc.rope_tables(D, S)
-    orc.unfused_composition(x, wq, wk, wv, gq, gk, cos, sin)  # warm-up
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+    x = t(rng.standard_normal((1, S, hidden), dtype=np.float32))
+    wq = t(rng.standard_normal((Hq * D, hidden), dtype=np.float32) * 0.02)
+    wk = t(rng.standard_normal((Hkv * D, hidden), dtype=np.float32) * 0.02)
+    wv = t(rng.standard_normal((Hkv * D, hidden), dtype=np.float32) * 0.02)
+    gq = t(1 + 0.1 * rng.standard_normal(D, dtype=np.float32))
+    gk = t(1 + 0.1 * rng.standard_normal(D, dtype=np.float32))
+    cos, sin = (t(a) for a in orc.rope_tables(D, S))
     times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        orc.unfused_composition(x, wq, wk, wv, gq, gk, cos, sin)
-        times.append(time.perf_counter() - t0)
+    with torch.inference_mode():
+        unfused_composition_torch(x, wq, wk, wv, gq, gk, cos, sin)  # warm-up
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            unfused_composition_torch(x, wq, wk, wv, gq, gk, cos, sin)
+            times.append(time.perf_counter() - t0)
     med = sorted(times)[len(times) // 2]
     return S / med, med * 1e3
 
@@ -345,7 +354,7 @@ def main(argv=None) -> int:
         if not args.no_cpu:
             ctps, cms = cpu_config1()
             c1.update({"cpu_fp32_tokens_per_s": round(ctps, 1), "cpu_ms_per_call": round(cms, 3),
-                       "cpu_kind": "port (oracle unfused composition, numpy/BLAS)"})
+                       "cpu_kind": "port (torch fp32 unfused composition)"})
         sec["config1_qwen3_0p6b_s128"] = c1
         log(f"[bench] config 1: {ms1 * 1e3:.1f} us/step on the GPU")
         result["secondary"] = sec

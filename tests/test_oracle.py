@@ -192,6 +192,25 @@ def test_fused_equals_unfused_composition():
         np.testing.assert_allclose(u, w_, rtol=1e-10, atol=1e-12)
 
 
+def test_torch_cpu_baseline_equals_fused_oracle():
+    """The torch restatement bench.py times as the CPU baseline computes the same
+    function as the fused oracle (float64 on both sides), GQA shapes and S > 1."""
+    import torch
+    from oracle.torch_baseline import unfused_composition_torch
+    rng = np.random.default_rng(17)
+    B, S, H, Hq, Hkv = 2, 7, 256, 4, 2
+    x = rng.standard_normal((B, S, H))
+    wq, wk, wv = (rng.standard_normal((h * D, H)) * 0.05 for h in (Hq, Hkv, Hkv))
+    gq, gk = rng.uniform(0.8, 1.2, D), rng.uniform(0.8, 1.2, D)
+    cos, sin = _tables64(S)
+    a = orc.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin)
+    t = lambda v: torch.from_numpy(np.ascontiguousarray(v))
+    b = unfused_composition_torch(t(x), t(wq), t(wk), t(wv), t(gq), t(gk), t(cos), t(sin))
+    for u, w_ in zip(a, b):
+        assert tuple(w_.shape) == u.shape
+        np.testing.assert_allclose(w_.numpy(), u, rtol=1e-10, atol=1e-12)
+
+
 def test_round_projection_changes_only_by_bf16_rounding():
     rng = np.random.default_rng(8)
     x = orc.round_bf16(rng.standard_normal((1, 4, 256)).astype(np.float32))
