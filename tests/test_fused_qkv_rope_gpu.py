@@ -216,6 +216,27 @@ def test_gqa_ratios(Hq, Hkv, device):
     _check(_run(case, device), case.oracle(), f"Hq={Hq} Hkv={Hkv}")
 
 
+# Attention shapes of the other Qwen3 models (hidden, Q heads, KV heads), each as a
+# prefill (tile kernel, a partial last row tile) and as a decode step (split-K
+# kernel, random positions into an 8192-row table).
+QWEN3_FAMILY = [
+    ("Qwen3-1.7B", 2048, 16, 8),
+    ("Qwen3-4B", 2560, 32, 8),
+    ("Qwen3-14B", 5120, 40, 8),
+    ("Qwen3-32B", 5120, 64, 8),
+    ("Qwen3-235B-A22B", 4096, 64, 4),
+]
+
+
+@pytest.mark.parametrize("name,hidden,Hq,Hkv", QWEN3_FAMILY)
+def test_qwen3_family_shapes(name, hidden, Hq, Hkv, device):
+    case = Case(1, 200, hidden, Hq, Hkv, seed=hidden + Hq)
+    _check(_run(case, device), case.oracle(), f"{name} prefill T=200")
+    pos = torch.randint(0, 8192, (48,), generator=torch.Generator().manual_seed(Hq), dtype=torch.int32)
+    case = Case(48, 1, hidden, Hq, Hkv, seed=hidden + Hq + 1, rows=8192, positions=pos)
+    _check(_run(case, device), case.oracle(), f"{name} decode B=48")
+
+
 def test_theta_and_scale(device):
     """theta != 1e6 and larger activations (checks no hidden theta/scale assumption).
 
