@@ -13,7 +13,7 @@ import os
 import threading
 from pathlib import Path
 
-import torch  # noqa: F401  (must be imported before the HIP library is mapped)
+import torch  # (imported before the HIP library is mapped)
 
 LIB_PATH = Path(os.environ.get("MQK_LIBRARY", Path(__file__).with_name("libmqk.so")))
 
@@ -152,6 +152,17 @@ def library() -> ctypes.CDLL:
                 fn.argtypes = args
             _lib = lib
     return _lib
+
+
+def call(device: torch.device, fn, *args) -> int:
+    """Run one native entry point with ``device`` as the current HIP device.
+
+    libmqk launches on the calling thread's current device, so a caller whose
+    tensors live on another GPU than the current one (one process driving
+    several GPUs) still gets the kernels on the tensors' device, next to the
+    stream and workspace that belong to it."""
+    with torch.cuda.device(device):
+        return fn(*args)
 
 
 def check(status: int, what: str) -> None:

@@ -117,7 +117,8 @@ def fused_qkv_rope(
     stream = torch.cuda.current_stream(device)
     nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, H_Q, H_KV, H))
     ws = _native.workspace(device, stream, nbytes)
-    status = lib.mqk_fused_qkv_rope_bf16(
+    status = _native.call(
+        device, lib.mqk_fused_qkv_rope_bf16,
         x.data_ptr(), w_q.data_ptr(), w_k.data_ptr(), w_v.data_ptr(),
         q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), _native.ptr(pos),
         T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
@@ -214,7 +215,7 @@ def fused_qkv_rope_paged(
     stream = torch.cuda.current_stream(device)
     nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, H_Q, H_KV, H))
     ws = _native.workspace(device, stream, nbytes)
-    status = lib.mqk_fused_qkv_rope_paged_bf16(
+    status = _native.call(device, lib.mqk_fused_qkv_rope_paged_bf16,
         x.data_ptr(), w_q.data_ptr(), w_k.data_ptr(), w_v.data_ptr(),
         q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), _native.ptr(pos),
         T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
@@ -350,7 +351,7 @@ def fused_qkv_rope_ex(
     stream = torch.cuda.current_stream(device)
     nbytes = int(lib.mqk_fused_qkv_rope_ex_workspace_size(T, H_Q, H_KV, H, ctypes.byref(ext)))
     ws = _native.workspace(device, stream, nbytes)
-    status = lib.mqk_fused_qkv_rope_ex_bf16(
+    status = _native.call(device, lib.mqk_fused_qkv_rope_ex_bf16,
         x.data_ptr(), w_q.data_ptr(), w_k.data_ptr(), w_v.data_ptr(),
         q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), _native.ptr(pos),
         T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
@@ -405,7 +406,7 @@ def qk_norm_rope(
     if T == 0:
         return q_out, k_out
     stream = torch.cuda.current_stream(device)
-    status = _native.library().mqk_qk_norm_rope_bf16(
+    status = _native.call(device, _native.library().mqk_qk_norm_rope_bf16,
         q_raw.data_ptr(), k_raw.data_ptr(), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
         cos.data_ptr(), sin.data_ptr(), _native.ptr(pos), T, S, H_Q, H_KV, D, cos.shape[0],
         float(eps), q_out.data_ptr(), k_out.data_ptr(), stream.cuda_stream)

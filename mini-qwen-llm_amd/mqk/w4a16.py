@@ -70,7 +70,7 @@ def w4a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
     if M == 0:
         return out
     stream = torch.cuda.current_stream(device)
-    status = _native.library().mqk_w4a16_gemm(
+    status = _native.call(device, _native.library().mqk_w4a16_gemm,
         x.data_ptr(), qweight.data_ptr(), scales.data_ptr(), qzeros.data_ptr(), M, K, N,
         group_size, st, out.data_ptr(), stream.cuda_stream)
     _native.check(status, "mqk_w4a16_gemm")
@@ -285,13 +285,13 @@ def _fused_w4a16(x, q_proj, k_proj, v_proj, q_norm_w, k_norm_w, cos, sin, positi
             q.data_ptr(), _native.ptr(k), _native.ptr(v))
     tail = (_native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
     if ext is not None:
-        status = lib.mqk_fused_qkv_rope_ex_w4a16(*head, ctypes.byref(ext), *tail)
+        status = _native.call(device, lib.mqk_fused_qkv_rope_ex_w4a16, *head, ctypes.byref(ext), *tail)
         _native.check(status, "mqk_fused_qkv_rope_ex_w4a16")
     elif desc is None:
-        status = lib.mqk_fused_qkv_rope_w4a16(*head, *tail)
+        status = _native.call(device, lib.mqk_fused_qkv_rope_w4a16, *head, *tail)
         _native.check(status, "mqk_fused_qkv_rope_w4a16")
     else:
-        status = lib.mqk_fused_qkv_rope_paged_w4a16(*head, ctypes.byref(desc), *tail)
+        status = _native.call(device, lib.mqk_fused_qkv_rope_paged_w4a16, *head, ctypes.byref(desc), *tail)
         _native.check(status, "mqk_fused_qkv_rope_paged_w4a16")
     del keep
     return q, k, v

@@ -348,3 +348,41 @@ def test_ext_validation(lib):
     normed = lib.mqk_fused_qkv_rope_ex_workspace_size(1000, 32, 8, 4096,
                                                        ctypes.byref(_native.FusedExt(in_gamma=fake)))
     assert normed >= plain + 4000
+
+
+def test_native_call_makes_the_tensor_device_current(monkeypatch):
+    """libmqk launches on the current HIP device: every launch goes through
+    _native.call, which enters torch.cuda.device(<the tensors' device>) around it."""
+    from mqk import _native
+    seen = []
+
+    class Recorder:
+        def __init__(self, dev):
+            self.dev = dev
+
+        def __enter__(self):
+            seen.append(("enter", str(self.dev)))
+
+        def __exit__(self, *exc):
+            seen.append(("exit", str(self.dev)))
+
+    monkeypatch.setattr(torch.cuda, "device", Recorder)
+    r = _native.call(torch.device("cuda", 1), lambda a, b: seen.append(("launch", a, b)) or 7, 3, 4)
+    assert r == 7
+    assert seen == [("enter", "cuda:1"), ("launch", 3, 4), ("exit", "cuda:1")]
+
+
+def test_every_launch_goes_through_native_call():
+    """No entry point that launches kernels is called directly from the package."""
+    import re
+    pkg = ROOT / "mini-qwen-llm_amd" / "mqk"
+    launching = re.compile(r"\.(mqk_fused_qkv_rope(_paged|_ex)?_(bf16|w4a16)|mqk_w4a16_gemm|mqk_qk_norm_rope_bf16)\b")
+    launches = 0
+    for f in pkg.glob("*.py"):
+        if f.name == "_native.py":  # the ctypes signature table names every entry point
+            continue
+        for ln in f.read_text().splitlines():
+            if launching.search(ln) and not ln.strip().startswith(("#", '"')):
+                launches += 1
+                assert "_native.call(device, " in ln or ln.strip().startswith("device, lib."), f"{f.name}: {ln.strip()}"
+    assert launches >= 8  # bf16 / paged / ex / qk-norm, int4 GEMM / plain / paged / ex
