@@ -7,10 +7,12 @@
  * passed as `mqk_bf16*` (the raw 16-bit pattern).  All tensors are dense and
  * row-major ("contiguous" in PyTorch terms).  Calls are asynchronous on the
  * given stream, never synchronize, never allocate device memory, and may be
- * made from any host thread.  Return value: MQK_OK (0) or a negative mqk
- * error code; mqk_error_string() turns it into text and
- * mqk_last_error_detail() names the argument or HIP error involved (per host
- * thread).
+ * made from any host thread.  Kernels launch on the calling thread's current
+ * HIP device: every pointer, the workspace and the stream must belong to it
+ * (a process driving several GPUs calls hipSetDevice first).  Return value:
+ * MQK_OK (0) or a negative mqk error code; mqk_error_string() turns it into
+ * text and mqk_last_error_detail() names the argument or HIP error involved
+ * (per host thread).
  *
  * Reference interface each entry point replaces (mini-qwen-llm):
  *   mqk_fused_qkv_rope_bf16   <- fused_qkv_rope()      mini_qwen/kernels/fused_qkv_rope.py:130-195
