@@ -82,3 +82,73 @@ def test_two_streams_concurrently(device):
     for i in range(2):
         for o in outs[i]:
             assert all(torch.equal(a, b) for a, b in zip(o, want[i]))
+
+
+def _replay_checks(graph, outs, want, rerun):
+    """Three replays, each compared with the eager result, eager work in between."""
+    for _ in range(3):
+        for t in outs:
+            t.fill_(0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(outs, want))
+        rerun()  # eager work between replays
+        torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("T", [32, 200])
+def test_graph_replay_w4a16(T, device):
+    """The W4A16 front (decode kernel at T = 32, tile + tail launches at T = 200)."""
+    import mqk
+    hidden, Hq, Hkv, D = 1024, 16, 8, 128
+    g = torch.Generator().manual_seed(T)
+    projs = []
+    for h in (Hq, Hkv, Hkv):
+        w = torch.randn(hidden, h * D, generator=g) * 0.02
+        projs.append(tuple(t.to(device) for t in mqk.per_group_minmax_quantize(w, 128, torch.float16)))
+    x = torch.randn(1, T, hidden, generator=g).bfloat16().to(device)
+    gq = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16().to(device)
+    gk = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16().to(device)
+    c, s = mqk.rope_tables(D, 4096)
+    cos, sin = c.bfloat16().to(device), s.bfloat16().to(device)
+    pos = torch.randint(0, 4096, (T,), generator=g, dtype=torch.int32).to(device)
+    run = lambda: mqk.fused_qkv_rope_w4a16(x, *projs, gq, gk, cos, sin, pos)
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        eager = run()
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = run()
+    _replay_checks(graph, out, eager, run)
+
+
+def test_graph_replay_paged_input_norm_decode(device):
+    """Decode step with the fused input RMSNorm (a pre-pass kernel writing the
+    workspace) and the paged-KV-cache write: outputs and cache contents replay."""
+    import mqk
+    B, hidden, Hq, Hkv, D, bs = 24, 1024, 16, 8, 128, 16
+    g = torch.Generator().manual_seed(77)
+    case = Case(B, 1, hidden, Hq, Hkv, seed=77, rows=4096,
+                positions=torch.randint(0, 4096, (B,), generator=g, dtype=torch.int32))
+    x, wq, wk, wv, gq, gk, cos, sin, pos = case.args(device)
+    in_w = (1 + 0.1 * torch.randn(hidden, generator=g)).bfloat16().to(device)
+    nblocks = B * 4096 // bs
+    kc = torch.zeros(nblocks, bs, Hkv, D, dtype=torch.bfloat16, device=device)
+    vc = torch.zeros_like(kc)
+    bt = torch.arange(nblocks, dtype=torch.int32, device=device).view(B, 4096 // bs)
+    kv_seq = torch.arange(B, dtype=torch.int32, device=device)
+
+    def run():
+        return mqk.fused_qkv_rope_ex(x, wq, wk, wv, gq, gk, cos, sin, pos, input_norm_w=in_w,
+                                     k_cache=kc, v_cache=vc, block_table=bt, kv_seq=kv_seq, kv_pos=pos)
+
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        eager = run()
+        stream.synchronize()
+        eager_caches = (kc.clone(), vc.clone())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = run()
+    _replay_checks(graph, tuple(out) + (kc, vc), tuple(eager) + eager_caches, run)
