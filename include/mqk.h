@@ -260,10 +260,12 @@ int mqk_fused_qkv_rope_ex_w4a16(const mqk_bf16* x, const int32_t* qw_q, const vo
  *   "tail_split"     1 (default): when the last, partial row tile of a prefill holds at most 64
  *                    rows and would cost a whole extra round of tiles over the CUs, those rows
  *                    run on the split-K decode kernel in a second launch; 0: never
- *   "decode_blocks"  16 (default): most 64-row split-K decode launches one call with
- *                    64 < T tokens may run as (instead of a tile launch whose few tiles leave
- *                    most CUs idle), used where a cost model of both paths says the launches
- *                    are faster; 0: never
+ *   "decode_blocks"  16 (default): most 64-row blocks of split-K decode launches one call
+ *                    with 64 < T tokens may run as (instead of a tile launch whose few tiles
+ *                    leave most CUs idle), used where a cost model of both paths says the
+ *                    launches are faster; 0: never
+ *   "decode_passes"  4 (default): most 64-row blocks one decode launch covers, streaming
+ *                    the weights once for all of them (1..4; the workspace size grows with it)
  *   "decode_force_recompute"  1: the decode kernel takes its recompute path (used when a
  *                    split ran on an unexpected XCD) for every head; for tests
  * Returns MQK_OK or MQK_ERR_BAD_OPTION.

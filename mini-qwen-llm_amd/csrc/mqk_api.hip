@@ -44,7 +44,8 @@ std::atomic<int64_t> g_decode_max_t{64};
 std::atomic<int64_t> g_decode_splits{0};
 std::atomic<int64_t> g_group_m{8};
 std::atomic<int64_t> g_tail_split{1};
-std::atomic<int64_t> g_decode_blocks{16};  // most 64-row decode launches for one call (T > 64)
+std::atomic<int64_t> g_decode_blocks{16};  // most 64-row decode blocks for one call (T > 64)
+std::atomic<int64_t> g_decode_passes{4};   // most 64-row blocks one decode launch covers (1..4)
 
 constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace (per head)
 
@@ -107,6 +108,7 @@ struct Plan {
   const TileVariant* v = nullptr;  // tile variant (null: decode only)
   int64_t tail = 0;                // rows run by the decode kernel after the tile rows
   int splits = 0;                  // decode kernel split-K factor (0: no decode launch)
+  int passes = 1;                  // 64-row blocks per decode launch
 };
 
 Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, bool allow_blocks = true) {
@@ -118,21 +120,29 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, bool 
       return pl;
     }
   }
-  // A few 64-row blocks: consecutive decode launches, each streaming the weights
-  // over every CU, can beat a tile launch whose few tiles leave most CUs idle
-  // and stream their panels at a single CU's rate.  Measured at hidden 4096:
-  // a bf16 decode launch ~17.6 us against ~75 us for the best tile variant at
-  // T = 65..512; int4 ~16 us per launch against ~135 us.  The models below
-  // follow those measurements (and hidden 2048: ~12 us against ~42 us).
+  // A few 64-row blocks: decode launches, each streaming the weights over every
+  // CU once for up to four blocks, can beat a tile launch whose few tiles leave
+  // most CUs idle and stream their panels at a single CU's rate.  Measured at
+  // hidden 4096: a bf16 decode launch ~18 us against ~80 us for the best tile
+  // variant at T = 65..1024; int4 ~16 us per launch against ~136 us.  Each
+  // further block of a launch (x re-staged, its rows finished) adds ~7 us at
+  // hidden 4096 (bf16 T = 128 / 192 / 256 in one launch: 26.6 / 33 / 40.5 us).
+  // The models below follow those measurements (and hidden 2048: ~12 us per
+  // launch against ~42 us for the tile kernel).
   const int64_t nblk = (M + 63) / 64;
+  const int64_t per_launch = std::max<int64_t>(1, std::min<int64_t>(g_decode_passes.load(), 4));
+  const int64_t launches = (nblk + per_launch - 1) / per_launch;
   const double w_bytes = double(n_tiles) * kHeadDim * double(K) * (int4 ? 0.5 : 2.0);
   const double dec_us = int4 ? 4.0 + 3.0 * double(K) / 1024.0 : 8.0 + w_bytes / 5.0e6;
+  const double pass_us = 3.0 + double(K) / 4096.0 * 4.0;
+  const double blocks_us = double(launches) * dec_us + double(nblk - launches) * pass_us;
   const double tile_us = double(K) / 64.0 * (int4 ? 2.1 : 1.15) + 5.0;
   if (allow_blocks && aligned && M > 64 && g_prefill_tile.load() == 0 && g_decode_max_t.load() >= 64 &&
-      nblk <= g_decode_blocks.load() && double(nblk) * dec_us <= tile_us) {
+      nblk <= g_decode_blocks.load() && blocks_us <= tile_us) {
     pl.splits = decode_splits_for(64, K, n_tiles, int(g_decode_splits.load()));
     if (pl.splits > 0) {
       pl.tail = M;
+      pl.passes = int(std::min<int64_t>(per_launch, nblk));
       return pl;
     }
   }
@@ -164,7 +174,11 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
                 (long long)g_prefill_tile.load(), p.n_tiles, int4 ? ", int4 weights" : "");
   // (the decode kernel's arrival counters open every workspace and must stay zero,
   // so the scales never start before them, whichever kernel runs this call)
-  size_t base = pl.splits > 0 ? decode_workspace_bytes(p.n_tiles, pl.splits) : decode_counter_bytes();
+  size_t base = pl.splits > 0 ? decode_workspace_bytes(p.n_tiles, pl.splits, pl.passes) : decode_counter_bytes();
+  if (!pl.v && pl.passes > 1 && (!workspace || ws_bytes < align_up(base, 256))) {
+    pl.passes = 1;  // a workspace sized for one block per launch
+    base = decode_workspace_bytes(p.n_tiles, pl.splits, 1);
+  }
   if (!pl.v && p.M > 64 && (!workspace || ws_bytes < align_up(base, 256))) {
     // decode blocks planned, but a workspace sized without them: the tile kernel
     pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), false);
@@ -199,10 +213,12 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
     if (st != MQK_OK || pl.tail == 0) return st;
   }
   // the decode kernel on the last pl.tail rows (all of them when there is no tile
-  // launch), 64 rows per launch; the launches share the workspace in stream order
-  for (int64_t t0 = p.M - pl.tail; t0 < p.M; t0 += 64) {
+  // launch), pl.passes blocks of 64 rows per launch; the launches share the
+  // workspace in stream order
+  const int64_t rows_per_launch = 64 * int64_t(pl.passes);
+  for (int64_t t0 = p.M - pl.tail; t0 < p.M; t0 += rows_per_launch) {
     ProblemArgs pt = p;
-    pt.M = std::min<int64_t>(64, p.M - t0);
+    pt.M = std::min<int64_t>(rows_per_launch, p.M - t0);
     pt.x = p.x + t0 * p.K;
     if (p.in_scale) pt.in_scale = p.in_scale + t0;
     EpilogueArgs et = e;
@@ -245,7 +261,7 @@ size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hid
   size_t n = 0;
   for (int int4 = 0; int4 < 2; ++int4) {  // the same size serves both weight formats
     const Plan pl = plan_fused(int4, T, hidden, tiles, true);
-    if (pl.splits > 0) n = std::max(n, decode_workspace_bytes(tiles, pl.splits));
+    if (pl.splits > 0) n = std::max(n, decode_workspace_bytes(tiles, pl.splits, pl.passes));
   }
   return n;
 }
@@ -579,6 +595,9 @@ int mqk_set_option(const char* name, int64_t value) {
   } else if (!strcmp(name, "decode_blocks")) {
     if (value < 0 || value > 64) return fail(MQK_ERR_BAD_OPTION, "decode_blocks must be in [0, 64]");
     g_decode_blocks = value;
+  } else if (!strcmp(name, "decode_passes")) {
+    if (value < 1 || value > 4) return fail(MQK_ERR_BAD_OPTION, "decode_passes must be in [1, 4]");
+    g_decode_passes = value;
   } else if (!strcmp(name, "group_m")) {
     if (value < 1 || value > 1024) return fail(MQK_ERR_BAD_OPTION, "group_m must be in [1, 1024]");
     g_group_m = value;
@@ -596,6 +615,7 @@ int64_t mqk_get_option(const char* name) {
   if (!strcmp(name, "group_m")) return g_group_m.load();
   if (!strcmp(name, "tail_split")) return g_tail_split.load();
   if (!strcmp(name, "decode_blocks")) return g_decode_blocks.load();
+  if (!strcmp(name, "decode_passes")) return g_decode_passes.load();
   if (!strcmp(name, "decode_force_recompute")) return g_decode_force_recompute;
   return -1;
 }

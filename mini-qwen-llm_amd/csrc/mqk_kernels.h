@@ -106,8 +106,11 @@ hipError_t launch_row_scale(const uint16_t* x, int64_t M, int64_t K, float eps, 
                             hipStream_t stream);
 
 int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested);
-size_t decode_workspace_bytes(int n_tiles, int splits);
+size_t decode_workspace_bytes(int n_tiles, int splits, int passes = 1);
 size_t decode_counter_bytes();  // the arrival counters at the start of every workspace
+// The split-K decode kernel on the launch's p.M <= 256 rows: ceil(M / 64) blocks of
+// 64 rows share one stream of the weights; the workspace holds
+// decode_workspace_bytes(n_tiles, splits, blocks).
 hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                          int splits, void* workspace, hipStream_t stream);
 

@@ -58,7 +58,8 @@ void set_decode_trace(void* ptr) {
 
 namespace {
 
-constexpr int kDecRows = 64;            // token rows per call (T <= 64)
+constexpr int kDecRows = 64;            // token rows per block (one block per call when T <= 64)
+constexpr int kDecMaxPasses = 4;        // most 64-row blocks one launch streams the weights for
 constexpr int kDecThreads = 512;        // 8 waves; wave w owns columns [16w, 16w+16) of the head
 constexpr int kDecWaves = kDecThreads / 64;
 constexpr int kDecMaxNK = 16;           // largest k-range of one split, in 64-wide tiles
@@ -97,16 +98,17 @@ __device__ __forceinline__ void split_range(int s, int S, int nkt, int& kt0, int
   nk = int((int64_t(s + 1) * nkt) / S) - kt0;
 }
 
-// One direct L2 -> LDS load per wave stages k tile t of the x slice: wave w
-// fills rows [8w, 8w+8) (1 KB, contiguous in LDS); lane L takes row 8w + L/8 and
-// LDS slot L % 8, i.e. global chunk (L % 8) ^ ((row >> 1) & 7).  Rows >= M
-// re-read row M-1; those LDS rows only feed output rows that are never stored.
-__device__ __forceinline__ void stage_x_tile(const ProblemArgs& p, int64_t kbeg, int t, uint32_t xs_lds) {
+// One direct L2 -> LDS load per wave stages k tile t of the x slice of the
+// 64-row block starting at launch row r0: wave w fills rows [8w, 8w+8) (1 KB,
+// contiguous in LDS); lane L takes row 8w + L/8 and LDS slot L % 8, i.e. global
+// chunk (L % 8) ^ ((row >> 1) & 7).  Rows >= M re-read row M-1; those LDS rows
+// only feed output rows that are never stored.
+__device__ __forceinline__ void stage_x_tile(const ProblemArgs& p, int64_t kbeg, int t, uint32_t xs_lds, int r0 = 0) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = wave * 8 + (lane >> 3);
   const int gq = (lane & 7) ^ ((row >> 1) & 7);
-  const int grow = row < int(p.M) ? row : int(p.M) - 1;
+  const int grow = r0 + row < int(p.M) ? r0 + row : int(p.M) - 1;
   dma16(p.x + int64_t(grow) * p.K + kbeg + t * kBK + gq * 8,
         xs_lds + uint32_t(t * kDecRows * 128 + wave * 1024));
 }
@@ -137,12 +139,12 @@ __device__ __forceinline__ void gamma_to_lds(const ProblemArgs& p, const u32x4_t
 
 // Normalise this wave's chunks of x tiles [0, nk) of the slice starting at k = kbeg
 // (gamma must be in LDS); ends with this wave's LDS writes complete.
-__device__ __forceinline__ void norm_x_tiles(const ProblemArgs& p, uint16_t* xs, int64_t kbeg, int nk) {
+__device__ __forceinline__ void norm_x_tiles(const ProblemArgs& p, uint16_t* xs, int64_t kbeg, int nk, int r0 = 0) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = wave * 8 + (lane >> 3);
   const int gq = (lane & 7) ^ ((row >> 1) & 7);
-  const float scale = p.in_scale[row < int(p.M) ? row : int(p.M) - 1];
+  const float scale = p.in_scale[r0 + row < int(p.M) ? r0 + row : int(p.M) - 1];
   unsigned char* base = reinterpret_cast<unsigned char*>(xs) + wave * 1024 + lane * 16;
   for (int t = 0; t < nk; ++t) {
     u32x4_t* q = reinterpret_cast<u32x4_t*>(base + t * kDecRows * 128);
@@ -220,16 +222,34 @@ __device__ __forceinline__ void dequant_tile(const Int4Col& ic, const uint32_t (
 // in every wave (own wait: the 3*(NK-1-t)+2 later loads may still be pending;
 // then a barrier) and its weight fragments have arrived (the compiler's per-use
 // waits), so the MFMAs run under the rest of the stream.
-template <bool INT4, bool INORM, int NK>
+// With NP > 1 the launch covers NP blocks of 64 rows: block 0 as above, then
+// for each later block the x slice of its rows is staged in the same LDS and
+// multiplied by the weight fragments this wave still holds in registers, so the
+// weights are streamed from HBM once for all NP * 64 rows (accs[pp] = block pp).
+template <bool INT4, bool INORM, int NK, int NP>
 __device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const WeightArgs& w, int proj, int hh,
-                                              int kt0, const uint16_t* xs, uint32_t xs_lds, f32x4_t (&acc)[4]) {
+                                              int kt0, const uint16_t* xs, uint32_t xs_lds,
+                                              f32x4_t (&accs)[NP][4]) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int c16 = lane & 15, g4 = lane >> 4;
   const int64_t kbeg = int64_t(kt0) * kBK;
   const int64_t col = int64_t(hh) * kHeadDim + wave * 16 + c16;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4_t{};
+  for (int pp = 0; pp < NP; ++pp)
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) accs[pp][mb] = f32x4_t{};
+  f32x4_t(&acc)[4] = accs[0];
+  // rows [64 pp, 64 pp + 64): stage their x slice once every wave is done with the
+  // previous block's (the normalising gamma, if any, is already in LDS)
+  auto stage_block = [&](int pp) {
+    barrier();
+#pragma unroll
+    for (int t = 0; t < NK; ++t) stage_x_tile(p, kbeg, t, xs_lds, pp * kDecRows);
+    wait_vm<0>();
+    if (INORM) norm_x_tiles(p, const_cast<uint16_t*>(xs), kbeg, NK, pp * kDecRows);
+    barrier();
+  };
   if constexpr (!INT4) {
     // The x slice (L2-resident) is requested first, then the first kLook weight
     // tiles; each later tile is requested one tile before the MFMAs that free
@@ -267,6 +287,12 @@ __device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const Weight
       }
       mma_tile(xs, t, b[t], acc);
     }
+#pragma unroll
+    for (int pp = 1; pp < NP; ++pp) {
+      stage_block(pp);
+#pragma unroll
+      for (int t = 0; t < NK; ++t) mma_tile(xs, t, b[t], accs[pp]);
+    }
   } else {
     // int4 weights are 4x smaller: load them with their scales and zeros, then
     // the x slice, and wait for everything
@@ -299,6 +325,16 @@ __device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const Weight
       dequant_tile(ic, q[t], sraw[t], zw[t], b);
       mma_tile(xs, t, b, acc);
     }
+#pragma unroll
+    for (int pp = 1; pp < NP; ++pp) {
+      stage_block(pp);
+#pragma unroll
+      for (int t = 0; t < NK; ++t) {
+        u32x4_t b[2];
+        dequant_tile(ic, q[t], sraw[t], zw[t], b);
+        mma_tile(xs, t, b, accs[pp]);
+      }
+    }
   }
 }
 
@@ -307,7 +343,7 @@ __device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const Weight
 // its result is bit-identical.  Used by the recompute path only.
 template <bool INT4, bool INORM>
 __device__ void partial_any(const ProblemArgs& p, const WeightArgs& w, int proj, int hh, int kt0, int nk,
-                            const uint16_t* xs, uint32_t xs_lds, f32x4_t (&acc)[4]) {
+                            const uint16_t* xs, uint32_t xs_lds, f32x4_t (&acc)[4], int r0) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int c16 = lane & 15, g4 = lane >> 4;
@@ -315,9 +351,9 @@ __device__ void partial_any(const ProblemArgs& p, const WeightArgs& w, int proj,
   const int64_t col = int64_t(hh) * kHeadDim + wave * 16 + c16;
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4_t{};
-  for (int t = 0; t < nk; ++t) stage_x_tile(p, kbeg, t, xs_lds);
+  for (int t = 0; t < nk; ++t) stage_x_tile(p, kbeg, t, xs_lds, r0);
   wait_vm<0>();
-  if (INORM) norm_x_tiles(p, const_cast<uint16_t*>(xs), kbeg, nk);  // gamma is in LDS already
+  if (INORM) norm_x_tiles(p, const_cast<uint16_t*>(xs), kbeg, nk, r0);  // gamma is in LDS already
   barrier();
   for (int t = 0; t < nk; ++t) {
     const int64_t k0 = kbeg + int64_t(t) * kBK;
@@ -337,13 +373,13 @@ __device__ void partial_any(const ProblemArgs& p, const WeightArgs& w, int proj,
   }
 }
 
-template <bool INT4, bool INORM>
+template <bool INT4, bool INORM, int NP>
 __device__ __forceinline__ void partial_dispatch(const ProblemArgs& p, const WeightArgs& w, int proj, int hh,
                                                  int kt0, int nk, const uint16_t* xs, uint32_t xs_lds,
-                                                 f32x4_t (&acc)[4]) {
+                                                 f32x4_t (&acc)[NP][4]) {
   switch (nk) {
 #define MQK_DEC_CASE(n) \
-  case n: partial_fixed<INT4, INORM, n>(p, w, proj, hh, kt0, xs, xs_lds, acc); break;
+  case n: partial_fixed<INT4, INORM, n, NP>(p, w, proj, hh, kt0, xs, xs_lds, acc); break;
     MQK_DEC_CASE(1) MQK_DEC_CASE(2) MQK_DEC_CASE(3) MQK_DEC_CASE(4)
     MQK_DEC_CASE(5) MQK_DEC_CASE(6) MQK_DEC_CASE(7) MQK_DEC_CASE(8)
     MQK_DEC_CASE(9) MQK_DEC_CASE(10) MQK_DEC_CASE(11) MQK_DEC_CASE(12)
@@ -353,7 +389,7 @@ __device__ __forceinline__ void partial_dispatch(const ProblemArgs& p, const Wei
   }
 }
 
-template <bool INT4, bool INORM>
+template <bool INT4, bool INORM, int NP>
 __global__ void __launch_bounds__(kDecThreads, 1)
 decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __restrict__ part,
               uint32_t* __restrict__ counters, int force_recompute) {
@@ -377,21 +413,30 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   split_head(head, e.Hq, e.Hkv, proj, hh);
   DECODE_TRACE(0)
 
-  // RoPE table row of this thread's finisher row (tid / 8), read now: a
-  // positions[] load here is off every critical path
-  const int64_t prow = (proj != 2 && (tid >> 3) < M) ? rope_row(e, tid >> 3) * kHeadDim : 0;
-  const int64_t cslot = (proj != 0 && (tid >> 3) < M) ? paged_slot(e, tid >> 3) : -1;  // paged-KV-cache slot
+  // RoPE table row of this thread's finisher row (tid / 8) of each 64-row block,
+  // read now: a positions[] load here is off every critical path
+  int64_t prow[NP], cslot[NP];  // cslot: paged-KV-cache slot
+#pragma unroll
+  for (int pp = 0; pp < NP; ++pp) {
+    const int rr = pp * kDecRows + (tid >> 3);
+    prow[pp] = (proj != 2 && rr < M) ? rope_row(e, rr) * kHeadDim : 0;
+    cslot[pp] = (proj != 0 && rr < M) ? paged_slot(e, rr) : -1;
+  }
 
   int kt0, nk;
   split_range(split, splits, nkt, kt0, nk);
-  f32x4_t acc[4];
-  partial_dispatch<INT4, INORM>(p, w, proj, hh, kt0, nk, xs, xs_lds, acc);
+  f32x4_t acc[NP][4];
+  partial_dispatch<INT4, INORM, NP>(p, w, proj, hh, kt0, nk, xs, xs_lds, acc);
   DECODE_TRACE(1)
 
-  // ---- publish the partial in fragment order: part[split][head][wave][mb][lane] ----
-  f32x4_t* mine = reinterpret_cast<f32x4_t*>(part) + ((int64_t(split) * n_tiles + head) * kDecWaves + wave) * 4 * 64 + lane;
+  // ---- publish the partials in fragment order: part[split][block][head][wave][mb][lane] ----
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) mine[mb * 64] = acc[mb];
+  for (int pp = 0; pp < NP; ++pp) {
+    f32x4_t* mine = reinterpret_cast<f32x4_t*>(part) +
+                    (((int64_t(split) * NP + pp) * n_tiles + head) * kDecWaves + wave) * 4 * 64 + lane;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) mine[mb * 64] = acc[pp][mb];
+  }
   __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have reached the L2
   __syncthreads();                // ... and every thread's
   if (tid == 0) {
@@ -413,16 +458,20 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   // no dependent load stalls the finisher.
   const int r = tid >> 3;
   const int c = tid & 7;
+#pragma unroll
+  for (int pp = 0; pp < NP; ++pp) {
+  if (pp > 0) __syncthreads();  // the previous block's epilogue is done with the LDS
+  const int rr = pp * kDecRows + r;  // this thread's row of the launch
   u32x4_t g_lo{}, g_hi{}, c_lo{}, c_hi{}, s_lo{}, s_hi{};
   auto load_operands = [&]() {
-    if (proj != 2 && r < M) {
+    if (proj != 2 && rr < M) {
       const uint16_t* gamma = proj == 0 ? e.q_gamma : e.k_gamma;
       g_lo = load8_bf16(gamma + 8 * c);
       g_hi = load8_bf16(gamma + kHalfDim + 8 * c);
-      c_lo = load8_bf16(e.cos + prow + 8 * c);
-      c_hi = load8_bf16(e.cos + prow + kHalfDim + 8 * c);
-      s_lo = load8_bf16(e.sin + prow + 8 * c);
-      s_hi = load8_bf16(e.sin + prow + kHalfDim + 8 * c);
+      c_lo = load8_bf16(e.cos + prow[pp] + 8 * c);
+      c_hi = load8_bf16(e.cos + prow[pp] + kHalfDim + 8 * c);
+      s_lo = load8_bf16(e.sin + prow[pp] + 8 * c);
+      s_hi = load8_bf16(e.sin + prow[pp] + kHalfDim + 8 * c);
     }
   };
 
@@ -437,8 +486,8 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
     // wave reads back only the 4 KB regions it loaded itself, so its own vmcnt
     // wait is the only synchronisation.  Summation is in split order.
     const char* frag = reinterpret_cast<const char*>(part) +
-                       ((int64_t(head) * kDecWaves + wave) * 4 * 64) * sizeof(f32x4_t);
-    const int64_t split_stride = int64_t(n_tiles) * kTileFloats * sizeof(float);
+                       (((int64_t(pp) * n_tiles + head) * kDecWaves + wave) * 4 * 64) * sizeof(f32x4_t);
+    const int64_t split_stride = int64_t(NP) * n_tiles * kTileFloats * sizeof(float);
     const uint32_t slot0 = xs_lds + uint32_t(wave * 4096);
     const char* slot0_ptr = reinterpret_cast<const char*>(xs) + wave * 4096;
     load_operands();
@@ -459,7 +508,7 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
         for (int u = first; u <= q; ++u) {
           if (u == split) {
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) sum[mb] += acc[mb];
+            for (int mb = 0; mb < 4; ++mb) sum[mb] += acc[pp][mb];
           } else {
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb)
@@ -480,9 +529,10 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
       int s_kt0, s_nk;
       split_range(s, splits, nkt, s_kt0, s_nk);
       __syncthreads();  // every wave is done with the x slice of the previous split
-      partial_any<INT4, INORM>(p, w, proj, hh, s_kt0, s_nk, xs, xs_lds, acc);
+      f32x4_t part_s[4];
+      partial_any<INT4, INORM>(p, w, proj, hh, s_kt0, s_nk, xs, xs_lds, part_s, pp * kDecRows);
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) sum[mb] += acc[mb];
+      for (int mb = 0; mb < 4; ++mb) sum[mb] += part_s[mb];
     }
   }
 
@@ -528,7 +578,7 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
       hi[i] = t2;
     }
   }
-  if (r < M) {
+  if (rr < M) {
     const int H = proj == 0 ? e.Hq : e.Hkv;
     u32x4_t o1, o2;
     o1.x = pack_bf16x2(lo[0], lo[1]);
@@ -541,16 +591,17 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
     o2.w = pack_bf16x2(hi[6], hi[7]);
     uint16_t* base = proj == 0 ? e.q : (proj == 1 ? e.k : e.v);  // k / v may be null (cache only)
     if (base) {
-      uint16_t* dst = base + (int64_t(r) * H + hh) * kHeadDim;
+      uint16_t* dst = base + (int64_t(rr) * H + hh) * kHeadDim;
       *reinterpret_cast<u32x4_t*>(dst + 8 * c) = o1;
       *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c) = o2;
     }
-    if (cslot >= 0) {
-      uint16_t* crow = paged_row(e, cslot, proj, hh);
+    if (cslot[pp] >= 0) {
+      uint16_t* crow = paged_row(e, cslot[pp], proj, hh);
       *reinterpret_cast<u32x4_t*>(crow + 8 * c) = o1;
       *reinterpret_cast<u32x4_t*>(crow + kHalfDim + 8 * c) = o2;
     }
   }
+  }  // 64-row blocks
   if (tid == 0) __hip_atomic_store(counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #ifdef MQK_DECODE_TRACE
   __builtin_amdgcn_s_waitcnt(0);
@@ -596,15 +647,16 @@ int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested) {
 
 size_t decode_counter_bytes() { return size_t(kCounterBytes); }
 
-size_t decode_workspace_bytes(int n_tiles, int splits) {
-  return size_t(kCounterBytes) + size_t(splits) * n_tiles * kTileFloats * sizeof(float);
+size_t decode_workspace_bytes(int n_tiles, int splits, int passes) {
+  return size_t(kCounterBytes) + size_t(splits) * passes * n_tiles * kTileFloats * sizeof(float);
 }
 
 hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                          int splits, void* workspace, hipStream_t stream) {
   const int nkt = int(p.K / kBK);
+  const int passes = int((p.M + kDecRows - 1) / kDecRows);  // 64-row blocks of this launch
   if (splits < 1 || splits > kDecMaxNK || splits > nkt || (nkt + splits - 1) / splits > kDecMaxNK ||
-      p.n_tiles > kMaxHeads)
+      p.n_tiles > kMaxHeads || passes < 1 || passes > kDecMaxPasses)
     return hipErrorInvalidValue;
   uint32_t* counters = static_cast<uint32_t*>(workspace);
   float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
@@ -616,9 +668,16 @@ hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, co
   if (p.in_gamma && (p.K / 8 > int64_t(kGamPerThread) * kDecThreads ||
                      kDecRows * kDecKc * 2 + 16 + dyn > 160 * 1024 || !a16(p.in_gamma)))
     return hipErrorInvalidValue;
-  // (the input norm is a template switch: the plain kernels carry none of its code)
-  auto* kernel = int4 ? (p.in_gamma ? decode_kernel<true, true> : decode_kernel<true, false>)
-                      : (p.in_gamma ? decode_kernel<false, true> : decode_kernel<false, false>);
+  // (the input norm and the block count are template switches: the plain one-block
+  // kernels carry none of their code)
+  using Kernel = void (*)(ProblemArgs, WeightArgs, EpilogueArgs, int, float*, uint32_t*, int);
+#define MQK_DEC_KERNELS(NP)                                                                   \
+  {decode_kernel<false, false, NP>, decode_kernel<false, true, NP>, decode_kernel<true, false, NP>, \
+   decode_kernel<true, true, NP>}
+  static const Kernel kernels[kDecMaxPasses][4] = {MQK_DEC_KERNELS(1), MQK_DEC_KERNELS(2), MQK_DEC_KERNELS(3),
+                                                   MQK_DEC_KERNELS(4)};
+#undef MQK_DEC_KERNELS
+  Kernel kernel = kernels[passes - 1][(int4 ? 2 : 0) + (p.in_gamma ? 1 : 0)];
   hipLaunchKernelGGL(kernel, grid, dim3(kDecThreads), dyn, stream, p, w, e, splits, part, counters, fr);
   return hipGetLastError();
 }

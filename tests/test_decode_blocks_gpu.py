@@ -1,12 +1,13 @@
 """GPU tests of the decode-block plan.
 
 A call of 64 < T tokens whose tile launch would leave most CUs idle (few row
-tiles, long K) runs instead as consecutive 64-row launches of the split-K decode
-kernel, each streaming the weights over every CU; row 0 of launch i is the call's
-token 64 i, so positions, cache slots and varlen offsets keep the call's token
-index.  Each block must equal the decode kernel run on those 64 rows alone, bit
-for bit; the whole call must match the oracle and, within the acceptance bar,
-the tile path (option decode_blocks = 0).
+tiles, long K) runs instead as launches of the split-K decode kernel, each
+streaming the weights over every CU once for up to four 64-row blocks (option
+decode_passes); row 0 of a launch is the call's token 64 * (blocks before it),
+so positions, cache slots and varlen offsets keep the call's token index.  Each
+block must equal the decode kernel run on those 64 rows alone, bit for bit; the
+whole call must match the oracle and, within the acceptance bar, the tile path
+(option decode_blocks = 0).
 """
 from __future__ import annotations
 
@@ -36,13 +37,17 @@ def _with_option(name, value, fn):
 
 
 def _close(a, b, label):
+    """Two kernel families against each other (each is held to the oracle bar
+    separately): they may round an element to neighbouring bf16 values, one ulp
+    apart, which above |v| = 4 exceeds 2e-2; the bound is the larger of the two."""
     for name, x, y in zip("qkv", a, b):
         x, y = f32(x), f32(y)
         ma, rl = orc.max_abs(x, y), orc.rel_l2(x, y)
-        assert ma <= MAX_ABS and rl <= REL_L2, f"{label} {name}: {ma} {rl}"
+        excess = np.abs(x - y) - np.maximum(MAX_ABS, 2.0 ** -7 * np.abs(y))
+        assert float(excess.max()) <= 0 and rl <= REL_L2, f"{label} {name}: {ma} {rl}"
 
 
-@pytest.mark.parametrize("T", [65, 128, 200, 256])
+@pytest.mark.parametrize("T", [65, 128, 200, 256, 300, 448])  # 300, 448: two launches
 def test_decode_blocks_bf16(T, device):
     import mqk
     pos = torch.randint(0, 8192, (T,), generator=torch.Generator().manual_seed(T), dtype=torch.int32)
@@ -115,3 +120,37 @@ def test_decode_blocks_varlen_paged_input_norm(device):
     slots = _expected_slots(seq, posv, bt.numpy(), bs)
     _check_cache(kc, k, slots, "k cache")
     _check_cache(vc, v, slots, "v cache")
+
+
+def test_decode_blocks_recompute_path(device):
+    """The recompute fallback (a split on an unexpected XCD) over a four-block
+    launch: every block recomputed by the last arrival, bit-identical."""
+    import mqk
+    T = 256
+    pos = torch.randint(0, 8192, (T,), generator=torch.Generator().manual_seed(3), dtype=torch.int32)
+    case = Case(1, T, 4096, 32, 8, seed=1400, rows=8192, positions=pos)
+    args = case.args(device)
+    out = mqk.fused_qkv_rope(*args)
+    torch.cuda.synchronize()
+    again = _with_option("decode_force_recompute", 1, lambda: mqk.fused_qkv_rope(*args))
+    for a, b in zip(out, again):
+        assert torch.equal(a, b)
+
+
+def test_decode_blocks_input_norm_four_blocks(device):
+    """The fused input RMSNorm across a four-block launch: each block equals the
+    same op on its 64 rows alone."""
+    import mqk
+    T, hidden = 256, 4096
+    pos = torch.randint(0, 8192, (T,), generator=torch.Generator().manual_seed(4), dtype=torch.int32)
+    case = Case(1, T, hidden, 32, 8, seed=1500, rows=8192, positions=pos)
+    x, wq, wk, wv, gq, gk, cos, sin, p = case.args(device)
+    g_in = (1 + 0.3 * torch.randn(hidden, generator=torch.Generator().manual_seed(5))).bfloat16().to(device)
+    out = mqk.fused_qkv_rope_ex(x, wq, wk, wv, gq, gk, cos, sin, p, input_norm_w=g_in)
+    torch.cuda.synchronize()
+    for t0 in range(0, T, 64):
+        alone = mqk.fused_qkv_rope_ex(x[:, t0:t0 + 64].contiguous(), wq, wk, wv, gq, gk, cos, sin,
+                                      p[t0:t0 + 64], input_norm_w=g_in)
+        torch.cuda.synchronize()
+        for a, b in zip(out, alone):
+            assert torch.equal(a[:, t0:t0 + 64], b), f"input-norm block at {t0} differs"

@@ -121,12 +121,15 @@ def test_workspace_size(lib):
     assert lib.mqk_fused_qkv_rope_workspace_size(0, 32, 8, 4096) == 0
     n = lib.mqk_fused_qkv_rope_workspace_size(64, 32, 8, 4096)
     assert n >= 4096 + 48 * 64 * 128 * 4  # counters + at least one fp32 partial per head
-    # 64 < T: 64-row decode launches (bf16 up to T = 256 here, int4 up to 512) share one
-    # decode region; past them, the tile kernel needs none
-    assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == n
-    assert lib.mqk_fused_qkv_rope_workspace_size(512, 32, 8, 4096) == n     # the int4 plan
-    assert lib.mqk_fused_qkv_rope_workspace_size(1024, 32, 8, 4096) == 0
     from mqk import _native
+    # 64 < T: decode launches of up to four 64-row blocks; each block of a launch
+    # has its own partials, so four blocks need four times the partial region
+    assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == 4096 + 4 * (n - 4096)
+    _native.set_option("decode_passes", 1)
+    try:  # one block per launch: the launches share one block's region
+        assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == n
+    finally:
+        _native.set_option("decode_passes", 4)
     _native.set_option("decode_blocks", 0)
     try:
         assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == 0
