@@ -1,4 +1,5 @@
-// Split-K projection for small token counts (decode steps, T <= 64) with the
+// Split-K projection for small token counts (decode steps, T <= 64, and up to
+// four 64-row blocks per launch at mid T) with the
 // per-head norm + RoPE applied once the split partial sums are combined.
 //
 // At decode the op is weight-read bound: Qwen3-8B's 50 MB of projection
