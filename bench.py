@@ -2,7 +2,7 @@
 """Benchmark of the fused QKV + QK-Norm + RoPE op on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
-    python bench.py --only {c2,c3,c4,c5,copy} --steps K   # one workload, for profiler runs
+    python bench.py --only {c2,c3,c4,c5,mid,copy} --steps K   # one workload, for profiler runs
 
 Headline (``value``): BASELINE config 2, Qwen3-8B prefill B=4 x S=512 (2048
 tokens, hidden 4096, 32 Q heads, 8 KV heads, head_dim 128, bf16), tokens/s of
@@ -239,7 +239,7 @@ def copy_kernel(nbytes, steps, dev):
     torch.cuda.synchronize()
 
 
-WORKLOADS = ("c2", "c3", "c4", "c5", "copy")
+WORKLOADS = ("c2", "c3", "c4", "c5", "mid", "copy")
 
 
 def run_only(name, steps, warmup, dev):
@@ -253,6 +253,8 @@ def run_only(name, steps, warmup, dev):
         ms, _ = bench_prefill(8192, 1, 8192, 2048, 32, 4, 3, steps, warmup, dev)
     elif name == "c5":
         ms, _ = bench_w4a16(hidden, Hq, Hkv, 4, steps, warmup, dev)
+    elif name == "mid":  # a 256-token decode step: one decode launch covering four 64-row blocks
+        ms, _ = bench_decode(256, hidden, Hq, Hkv, 2, steps, warmup, dev)
     else:
         copy_kernel(256 << 20, steps, dev)
         ms = float("nan")
