@@ -461,147 +461,147 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   const int c = tid & 7;
 #pragma unroll
   for (int pp = 0; pp < NP; ++pp) {
-  if (pp > 0) __syncthreads();  // the previous block's epilogue is done with the LDS
-  const int rr = pp * kDecRows + r;  // this thread's row of the launch
-  u32x4_t g_lo{}, g_hi{}, c_lo{}, c_hi{}, s_lo{}, s_hi{};
-  auto load_operands = [&]() {
-    if (proj != 2 && rr < M) {
-      const uint16_t* gamma = proj == 0 ? e.q_gamma : e.k_gamma;
-      g_lo = load8_bf16(gamma + 8 * c);
-      g_hi = load8_bf16(gamma + kHalfDim + 8 * c);
-      c_lo = load8_bf16(e.cos + prow[pp] + 8 * c);
-      c_hi = load8_bf16(e.cos + prow[pp] + kHalfDim + 8 * c);
-      s_lo = load8_bf16(e.sin + prow[pp] + 8 * c);
-      s_hi = load8_bf16(e.sin + prow[pp] + kHalfDim + 8 * c);
-    }
-  };
-
-  // ---- last arrival: sum the partials in split order ---------------------------------
-  f32x4_t sum[4];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) sum[mb] = f32x4_t{};
-  if (!recompute) {
-    // The other splits' fragments of this wave are pulled into LDS with direct
-    // L2 -> LDS loads (a CU fetches faster that way than into VGPRs), up to four
-    // splits per batch in the x slice's space, which no wave reads any more; each
-    // wave reads back only the 4 KB regions it loaded itself, so its own vmcnt
-    // wait is the only synchronisation.  Summation is in split order.
-    const char* frag = reinterpret_cast<const char*>(part) +
-                       (((int64_t(pp) * n_tiles + head) * kDecWaves + wave) * 4 * 64) * sizeof(f32x4_t);
-    const int64_t split_stride = int64_t(NP) * n_tiles * kTileFloats * sizeof(float);
-    const uint32_t slot0 = xs_lds + uint32_t(wave * 4096);
-    const char* slot0_ptr = reinterpret_cast<const char*>(xs) + wave * 4096;
-    load_operands();
-    int slot = 0, first = 0;
-#pragma unroll 1
-    for (int q = 0; q < splits; ++q) {
-      if (q != split) {
-        const char* src = frag + q * split_stride + lane * 16;
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
-          dma16(src + mb * 1024, slot0 + uint32_t(slot * kDecWaves * 4096 + mb * 1024));
-        ++slot;
+    if (pp > 0) __syncthreads();  // the previous block's epilogue is done with the LDS
+    const int rr = pp * kDecRows + r;  // this thread's row of the launch
+    u32x4_t g_lo{}, g_hi{}, c_lo{}, c_hi{}, s_lo{}, s_hi{};
+    auto load_operands = [&]() {
+      if (proj != 2 && rr < M) {
+        const uint16_t* gamma = proj == 0 ? e.q_gamma : e.k_gamma;
+        g_lo = load8_bf16(gamma + 8 * c);
+        g_hi = load8_bf16(gamma + kHalfDim + 8 * c);
+        c_lo = load8_bf16(e.cos + prow[pp] + 8 * c);
+        c_hi = load8_bf16(e.cos + prow[pp] + kHalfDim + 8 * c);
+        s_lo = load8_bf16(e.sin + prow[pp] + 8 * c);
+        s_hi = load8_bf16(e.sin + prow[pp] + kHalfDim + 8 * c);
       }
-      if (slot == 4 || q == splits - 1) {  // four slots filled, or the last split: add in split order
-        wait_vm<0>();
-        int u_slot = 0;
+    };
+
+    // ---- last arrival: sum the partials in split order ---------------------------------
+    f32x4_t sum[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) sum[mb] = f32x4_t{};
+    if (!recompute) {
+      // The other splits' fragments of this wave are pulled into LDS with direct
+      // L2 -> LDS loads (a CU fetches faster that way than into VGPRs), up to four
+      // splits per batch in the x slice's space, which no wave reads any more; each
+      // wave reads back only the 4 KB regions it loaded itself, so its own vmcnt
+      // wait is the only synchronisation.  Summation is in split order.
+      const char* frag = reinterpret_cast<const char*>(part) +
+                         (((int64_t(pp) * n_tiles + head) * kDecWaves + wave) * 4 * 64) * sizeof(f32x4_t);
+      const int64_t split_stride = int64_t(NP) * n_tiles * kTileFloats * sizeof(float);
+      const uint32_t slot0 = xs_lds + uint32_t(wave * 4096);
+      const char* slot0_ptr = reinterpret_cast<const char*>(xs) + wave * 4096;
+      load_operands();
+      int slot = 0, first = 0;
 #pragma unroll 1
-        for (int u = first; u <= q; ++u) {
-          if (u == split) {
+      for (int q = 0; q < splits; ++q) {
+        if (q != split) {
+          const char* src = frag + q * split_stride + lane * 16;
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) sum[mb] += acc[pp][mb];
-          } else {
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
-              sum[mb] += *reinterpret_cast<const f32x4_t*>(slot0_ptr + u_slot * kDecWaves * 4096 + mb * 1024 + lane * 16);
-            ++u_slot;
-          }
+          for (int mb = 0; mb < 4; ++mb)
+            dma16(src + mb * 1024, slot0 + uint32_t(slot * kDecWaves * 4096 + mb * 1024));
+          ++slot;
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next batch overwrites
-        slot = 0;
-        first = q + 1;
+        if (slot == 4 || q == splits - 1) {  // four slots filled, or the last split: add in split order
+          wait_vm<0>();
+          int u_slot = 0;
+#pragma unroll 1
+          for (int u = first; u <= q; ++u) {
+            if (u == split) {
+#pragma unroll
+              for (int mb = 0; mb < 4; ++mb) sum[mb] += acc[pp][mb];
+            } else {
+#pragma unroll
+              for (int mb = 0; mb < 4; ++mb)
+                sum[mb] += *reinterpret_cast<const f32x4_t*>(slot0_ptr + u_slot * kDecWaves * 4096 + mb * 1024 + lane * 16);
+              ++u_slot;
+            }
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next batch overwrites
+          slot = 0;
+          first = q + 1;
+        }
+      }
+    } else {
+      // Some split ran on another XCD: its partial may not be visible through this
+      // L2.  Recompute every split here (same arithmetic, same order).
+      load_operands();
+      for (int s = 0; s < splits; ++s) {
+        int s_kt0, s_nk;
+        split_range(s, splits, nkt, s_kt0, s_nk);
+        __syncthreads();  // every wave is done with the x slice of the previous split
+        f32x4_t part_s[4];
+        partial_any<INT4, INORM>(p, w, proj, hh, s_kt0, s_nk, xs, xs_lds, part_s, pp * kDecRows);
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) sum[mb] += part_s[mb];
       }
     }
-  } else {
-    // Some split ran on another XCD: its partial may not be visible through this
-    // L2.  Recompute every split here (same arithmetic, same order).
-    load_operands();
-    for (int s = 0; s < splits; ++s) {
-      int s_kt0, s_nk;
-      split_range(s, splits, nkt, s_kt0, s_nk);
-      __syncthreads();  // every wave is done with the x slice of the previous split
-      f32x4_t part_s[4];
-      partial_any<INT4, INORM>(p, w, proj, hh, s_kt0, s_nk, xs, xs_lds, part_s, pp * kDecRows);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) sum[mb] += part_s[mb];
-    }
-  }
 
-  // ---- head tile to LDS (fp32 [64][kPitch]); the x slice is no longer read ----------
-  DECODE_TRACE(7)
-  __syncthreads();
-  {
-    const int c16 = lane & 15, g4 = lane >> 4;
+    // ---- head tile to LDS (fp32 [64][kPitch]); the x slice is no longer read ----------
+    DECODE_TRACE(7)
+    __syncthreads();
+    {
+      const int c16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+      for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) tile[(mb * 16 + g4 * 4 + j) * kPitch + wave * 16 + c16] = sum[mb][j];
-  }
-  __syncthreads();
-  DECODE_TRACE(3)
+        for (int j = 0; j < 4; ++j) tile[(mb * 16 + g4 * 4 + j) * kPitch + wave * 16 + c16] = sum[mb][j];
+    }
+    __syncthreads();
+    DECODE_TRACE(3)
 
-  float lo[8], hi[8];
-  {
-    const float* src = tile + r * kPitch;
-    const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(src + 8 * c);
-    const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(src + 8 * c + 4);
-    const f32x4_t b0 = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + 8 * c);
-    const f32x4_t b1 = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + 8 * c + 4);
-    lo[0] = a0.x; lo[1] = a0.y; lo[2] = a0.z; lo[3] = a0.w;
-    lo[4] = a1.x; lo[5] = a1.y; lo[6] = a1.z; lo[7] = a1.w;
-    hi[0] = b0.x; hi[1] = b0.y; hi[2] = b0.z; hi[3] = b0.w;
-    hi[4] = b1.x; hi[5] = b1.y; hi[6] = b1.z; hi[7] = b1.w;
-  }
+    float lo[8], hi[8];
+    {
+      const float* src = tile + r * kPitch;
+      const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(src + 8 * c);
+      const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(src + 8 * c + 4);
+      const f32x4_t b0 = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + 8 * c);
+      const f32x4_t b1 = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + 8 * c + 4);
+      lo[0] = a0.x; lo[1] = a0.y; lo[2] = a0.z; lo[3] = a0.w;
+      lo[4] = a1.x; lo[5] = a1.y; lo[6] = a1.z; lo[7] = a1.w;
+      hi[0] = b0.x; hi[1] = b0.y; hi[2] = b0.z; hi[3] = b0.w;
+      hi[4] = b1.x; hi[5] = b1.y; hi[6] = b1.z; hi[7] = b1.w;
+    }
 
-  if (proj != 2) {
-    float ss = 0.f;
+    if (proj != 2) {
+      float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss += lo[i] * lo[i] + hi[i] * hi[i];
-    ss = sum8_lanes(ss);
-    const float rms = rsqrtf(ss * (1.0f / float(kHeadDim)) + e.eps);
+      for (int i = 0; i < 8; ++i) ss += lo[i] * lo[i] + hi[i] * hi[i];
+      ss = sum8_lanes(ss);
+      const float rms = rsqrtf(ss * (1.0f / float(kHeadDim)) + e.eps);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float x1n = lo[i] * rms * bf16_lane(g_lo, i);
-      const float x2n = hi[i] * rms * bf16_lane(g_hi, i);
-      const float t1 = x1n * bf16_lane(c_lo, i) - x2n * bf16_lane(s_lo, i);
-      const float t2 = x2n * bf16_lane(c_hi, i) + x1n * bf16_lane(s_hi, i);
-      lo[i] = t1;
-      hi[i] = t2;
+      for (int i = 0; i < 8; ++i) {
+        const float x1n = lo[i] * rms * bf16_lane(g_lo, i);
+        const float x2n = hi[i] * rms * bf16_lane(g_hi, i);
+        const float t1 = x1n * bf16_lane(c_lo, i) - x2n * bf16_lane(s_lo, i);
+        const float t2 = x2n * bf16_lane(c_hi, i) + x1n * bf16_lane(s_hi, i);
+        lo[i] = t1;
+        hi[i] = t2;
+      }
     }
-  }
-  if (rr < M) {
-    const int H = proj == 0 ? e.Hq : e.Hkv;
-    u32x4_t o1, o2;
-    o1.x = pack_bf16x2(lo[0], lo[1]);
-    o1.y = pack_bf16x2(lo[2], lo[3]);
-    o1.z = pack_bf16x2(lo[4], lo[5]);
-    o1.w = pack_bf16x2(lo[6], lo[7]);
-    o2.x = pack_bf16x2(hi[0], hi[1]);
-    o2.y = pack_bf16x2(hi[2], hi[3]);
-    o2.z = pack_bf16x2(hi[4], hi[5]);
-    o2.w = pack_bf16x2(hi[6], hi[7]);
-    uint16_t* base = proj == 0 ? e.q : (proj == 1 ? e.k : e.v);  // k / v may be null (cache only)
-    if (base) {
-      uint16_t* dst = base + (int64_t(rr) * H + hh) * kHeadDim;
-      *reinterpret_cast<u32x4_t*>(dst + 8 * c) = o1;
-      *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c) = o2;
+    if (rr < M) {
+      const int H = proj == 0 ? e.Hq : e.Hkv;
+      u32x4_t o1, o2;
+      o1.x = pack_bf16x2(lo[0], lo[1]);
+      o1.y = pack_bf16x2(lo[2], lo[3]);
+      o1.z = pack_bf16x2(lo[4], lo[5]);
+      o1.w = pack_bf16x2(lo[6], lo[7]);
+      o2.x = pack_bf16x2(hi[0], hi[1]);
+      o2.y = pack_bf16x2(hi[2], hi[3]);
+      o2.z = pack_bf16x2(hi[4], hi[5]);
+      o2.w = pack_bf16x2(hi[6], hi[7]);
+      uint16_t* base = proj == 0 ? e.q : (proj == 1 ? e.k : e.v);  // k / v may be null (cache only)
+      if (base) {
+        uint16_t* dst = base + (int64_t(rr) * H + hh) * kHeadDim;
+        *reinterpret_cast<u32x4_t*>(dst + 8 * c) = o1;
+        *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c) = o2;
+      }
+      if (cslot[pp] >= 0) {
+        uint16_t* crow = paged_row(e, cslot[pp], proj, hh);
+        *reinterpret_cast<u32x4_t*>(crow + 8 * c) = o1;
+        *reinterpret_cast<u32x4_t*>(crow + kHalfDim + 8 * c) = o2;
+      }
     }
-    if (cslot[pp] >= 0) {
-      uint16_t* crow = paged_row(e, cslot[pp], proj, hh);
-      *reinterpret_cast<u32x4_t*>(crow + 8 * c) = o1;
-      *reinterpret_cast<u32x4_t*>(crow + kHalfDim + 8 * c) = o2;
-    }
-  }
   }  // 64-row blocks
   if (tid == 0) __hip_atomic_store(counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #ifdef MQK_DECODE_TRACE
