@@ -513,7 +513,8 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
             } else {
 #pragma unroll
               for (int mb = 0; mb < 4; ++mb)
-                sum[mb] += *reinterpret_cast<const f32x4_t*>(slot0_ptr + u_slot * kDecWaves * 4096 + mb * 1024 + lane * 16);
+                sum[mb] += *reinterpret_cast<const f32x4_t*>(slot0_ptr + u_slot * kDecWaves * 4096 + mb * 1024 +
+                                                             lane * 16);
               ++u_slot;
             }
           }
