@@ -137,6 +137,19 @@ def test_workspace_size(lib):
         _native.set_option("decode_blocks", 16)
 
 
+def test_decode_block_crossovers(lib):
+    """The plan's cost model reproduces the crossovers measured on MI355X at hidden
+    4096 (Qwen3-8B heads).  A workspace is needed exactly when decode launches run:
+    bf16 and int4 use decode blocks up to T = 512, int4 alone up to T = 768 (four-block
+    launches 76 / 113 us against 136 us for its tile kernel), and neither at T = 1024
+    (tile kernels 83 / 137 us against 155 us for four int4 launches)."""
+    size = lambda T: lib.mqk_fused_qkv_rope_workspace_size(T, 32, 8, 4096)
+    n4 = 4096 + 4 * (size(64) - 4096)  # counters + four blocks of partials
+    assert size(512) == n4
+    assert size(768) == n4   # the int4 plan
+    assert size(1024) == 0
+
+
 def test_w4a16_validation(lib):
     fake = 1 << 20
     call = lambda M=4, K=256, N=64, g=128, st=0, qw=fake: lib.mqk_w4a16_gemm(
