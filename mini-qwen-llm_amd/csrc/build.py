@@ -49,9 +49,9 @@ def _filter(text: str) -> str:
     return "\n".join(keep)
 
 
-def _compile(src: str, verbose: bool, defines=()) -> Path:
+def _compile(src: str, verbose: bool) -> Path:
     obj = BUILD_DIR / (Path(src).stem + ".o")
-    cmd = [_hipcc(), *COMMON_FLAGS, *[f"-D{d}" for d in defines], "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [_hipcc(), *COMMON_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -63,10 +63,10 @@ def _compile(src: str, verbose: bool, defines=()) -> Path:
     return obj
 
 
-def build(verbose: bool = False, defines=()) -> Path:
+def build(verbose: bool = False) -> Path:
     BUILD_DIR.mkdir(exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose, defines), SOURCES))
+        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
     tmp = OUT.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     if verbose:
@@ -81,10 +81,8 @@ def build(verbose: bool = False, defines=()) -> Path:
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--verbose", action="store_true")
-    ap.add_argument("-D", dest="defines", action="append", default=[],
-                    help="extra preprocessor define, e.g. -D MQK_DECODE_TRACE (diagnostic build)")
     args = ap.parse_args(argv)
-    out = build(args.verbose, args.defines)
+    out = build(args.verbose)
     print(f"built {out}")
     return 0
 

@@ -581,14 +581,6 @@ int mqk_set_option(const char* name, int64_t value) {
   } else if (!strcmp(name, "decode_force_recompute")) {
     if (value != 0 && value != 1) return fail(MQK_ERR_BAD_OPTION, "decode_force_recompute must be 0 or 1");
     g_decode_force_recompute = int(value);
-#ifdef MQK_DECODE_TRACE
-  } else if (!strcmp(name, "decode_trace")) {  // diagnostic builds only
-    set_decode_trace(reinterpret_cast<void*>(value));
-#endif
-#ifdef MQK_TILE_TRACE
-  } else if (!strcmp(name, "tile_trace")) {  // diagnostic builds only
-    set_tile_trace(reinterpret_cast<void*>(value));
-#endif
   } else if (!strcmp(name, "tail_split")) {
     if (value != 0 && value != 1) return fail(MQK_ERR_BAD_OPTION, "tail_split must be 0 or 1");
     g_tail_split = value;

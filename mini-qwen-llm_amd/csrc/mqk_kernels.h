@@ -118,13 +118,6 @@ hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, co
 // taken when a split ran on an unexpected XCD); for tests.
 extern int g_decode_force_recompute;
 
-#ifdef MQK_TILE_TRACE
-void set_tile_trace(void* ptr);
-#endif
-#ifdef MQK_DECODE_TRACE
-void set_decode_trace(void* ptr);  // diagnostic builds only
-#endif
-
 // Standalone QK-norm + RoPE.
 hipError_t launch_norm_rope(const uint16_t* q_raw, const uint16_t* k_raw, const EpilogueArgs& e,
                             int64_t T, hipStream_t stream);

@@ -41,22 +41,6 @@
 
 namespace mqk {
 
-#ifdef MQK_DECODE_TRACE
-// Diagnostic build only: per-workgroup phase timestamps (100 MHz s_memrealtime)
-// written to a device buffer set with mqk_set_option("decode_trace", ptr).
-// (a __constant__ pointer: read with a scalar load, so a trace point never waits
-// for the kernel's outstanding vector loads)
-__constant__ int64_t* g_decode_trace = nullptr;
-void set_decode_trace(void* ptr) {
-  (void)hipMemcpyToSymbol(HIP_SYMBOL(g_decode_trace), &ptr, sizeof(ptr));
-}
-#define DECODE_TRACE(i)                                                   \
-  if (g_decode_trace && threadIdx.x == 0)                                 \
-    g_decode_trace[blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memrealtime();
-#else
-#define DECODE_TRACE(i)
-#endif
-
 namespace {
 
 constexpr int kDecRows = 64;            // token rows per block (one block per call when T <= 64)
@@ -64,10 +48,7 @@ constexpr int kDecMaxPasses = 4;        // most 64-row blocks one launch streams
 constexpr int kDecThreads = 512;        // 8 waves; wave w owns columns [16w, 16w+16) of the head
 constexpr int kDecWaves = kDecThreads / 64;
 constexpr int kDecMaxNK = 16;           // largest k-range of one split, in 64-wide tiles
-#ifndef MQK_DEC_LOOK
-#define MQK_DEC_LOOK 6
-#endif
-constexpr int kDecLookahead = MQK_DEC_LOOK;  // weight tiles in flight per wave
+constexpr int kDecLookahead = 6;        // weight tiles in flight per wave
 constexpr int kDecKc = kDecMaxNK * kBK;     // LDS row length of the x slice (bf16), 2 KB
 constexpr int kMaxHeads = 1024;
 constexpr int kCounterBytes = kMaxHeads * 4;
@@ -186,11 +167,7 @@ __device__ __forceinline__ float bf16_lane(const u32x4_t& v, int i) {
 // Weight fragment load: non-temporal, so the weight stream does not evict the
 // split partials and the x slice from the L2.
 __device__ __forceinline__ u32x4_t wload(const uint16_t* ptr) {
-#ifdef MQK_DEC_TEMPORAL
-  return *reinterpret_cast<const u32x4_t*>(ptr);
-#else
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(ptr));
-#endif
 }
 
 struct Int4Col {  // this lane's column of an int4 projection
@@ -277,7 +254,6 @@ __device__ __forceinline__ void partial_fixed(const ProblemArgs& p, const Weight
       norm_x_tiles(p, const_cast<uint16_t*>(xs), kbeg, NK);
     }
     barrier();             // ... in every wave
-    DECODE_TRACE(5)
 #pragma unroll
     for (int t = 0; t < NK; ++t) {
       if (t + kLook < NK) {
@@ -412,7 +388,6 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   const int nkt = int(p.K / kBK);
   int proj, hh;
   split_head(head, e.Hq, e.Hkv, proj, hh);
-  DECODE_TRACE(0)
 
   // RoPE table row of this thread's finisher row (tid / 8) of each 64-row block,
   // read now: a positions[] load here is off every critical path
@@ -428,7 +403,6 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   split_range(split, splits, nkt, kt0, nk);
   f32x4_t acc[NP][4];
   partial_dispatch<INT4, INORM, NP>(p, w, proj, hh, kt0, nk, xs, xs_lds, acc);
-  DECODE_TRACE(1)
 
   // ---- publish the partials in fragment order: part[split][block][head][wave][mb][lane] ----
 #pragma unroll
@@ -446,11 +420,9 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
     arrival = __hip_atomic_fetch_add(counters + head, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
   }
   __syncthreads();
-  DECODE_TRACE(2)
   const uint32_t seen = arrival;
   if ((seen & (kForeignUnit - 1)) != uint32_t(splits)) return;  // not the last split to arrive
   const bool recompute = (seen >> 16) != 0;
-  DECODE_TRACE(8)
 
   // thread -> row r = tid / 8, c = tid % 8 of the head tile: columns [8c, 8c+8)
   // and [64+8c, 64+8c+8), so every RoPE pair (d, d+64) is thread-local.  Its
@@ -539,7 +511,6 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
     }
 
     // ---- head tile to LDS (fp32 [64][kPitch]); the x slice is no longer read ----------
-    DECODE_TRACE(7)
     __syncthreads();
     {
       const int c16 = lane & 15, g4 = lane >> 4;
@@ -549,7 +520,6 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
         for (int j = 0; j < 4; ++j) tile[(mb * 16 + g4 * 4 + j) * kPitch + wave * 16 + c16] = sum[mb][j];
     }
     __syncthreads();
-    DECODE_TRACE(3)
 
     float lo[8], hi[8];
     {
@@ -605,10 +575,6 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
     }
   }  // 64-row blocks
   if (tid == 0) __hip_atomic_store(counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#ifdef MQK_DECODE_TRACE
-  __builtin_amdgcn_s_waitcnt(0);
-  DECODE_TRACE(4)
-#endif
 }
 
 int g_cus_per_xcd = 0;  // queried once (single-device processes)

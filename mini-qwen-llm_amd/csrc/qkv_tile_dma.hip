@@ -33,11 +33,6 @@
 
 namespace mqk {
 
-#ifdef MQK_TILE_TRACE
-__constant__ int64_t* g_tile_trace = nullptr;
-void set_tile_trace(void* ptr) { (void)hipMemcpyToSymbol(HIP_SYMBOL(g_tile_trace), &ptr, sizeof(ptr)); }
-#endif
-
 namespace {
 
 constexpr int kEpiPitch = kHeadDim + 4;     // fp32 pitch of the epilogue head tile
@@ -360,9 +355,6 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
     const uint32_t base = lds0 + uint32_t((kt % NS) * S::kStageBytes);
 #pragma unroll
     for (int i = 0; i < S::kLoadsPerWave; ++i) {
-#ifdef MQK_DIAG_NOLOAD  // diagnostic build: K loop without global loads (timing only, wrong results)
-      if (kt >= NS) break;
-#endif
       dma16(src[i] + int64_t(kt) * SBK, base + dst_off[i]);
     }
   };
@@ -376,28 +368,14 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
 
   const int c32 = lane & 31;
   const int khalf = lane >> 5;
-#ifdef MQK_DIAG_NOLOOP  // diagnostic build: epilogue only (timing only, wrong results)
-  const int nkt = 0;
-#else
   const int nkt = int(K / SBK);
-#endif
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
     if (s < nkt) issue(s);
 
   for (int kt = 0; kt < nkt; ++kt) {
     const int ahead = min(NS - 2, nkt - 1 - kt);  // stages already issued after kt
-#ifdef MQK_TILE_TRACE2  // diagnostic build: per-wave timestamps around the wait, stages 8..22
-    if (g_tile_trace && lane == 0 && kt >= 8 && kt < 23)
-      g_tile_trace[blockIdx.x * 256 + (kt - 8) * 16 + wave * 2] = __builtin_amdgcn_s_memrealtime();
-#endif
     wait_stage<NS, S::kLoadsPerWave>(ahead);
-#ifdef MQK_TILE_TRACE2
-    if (g_tile_trace && lane == 0 && kt >= 8 && kt < 23)
-      g_tile_trace[blockIdx.x * 256 + (kt - 8) * 16 + wave * 2 + 1] = __builtin_amdgcn_s_memrealtime();
-#elif defined(MQK_TILE_TRACE)  // diagnostic build: per-stage timestamps of wave 0 of each workgroup
-    if (g_tile_trace && tid == 0 && kt < 126) g_tile_trace[blockIdx.x * 256 + 2 * kt] = __builtin_amdgcn_s_memrealtime();
-#endif
     if (in_norm) {  // this wave's x chunks of stage kt have landed: normalise them in place
 #pragma unroll
       for (int i = 0; i < S::kALoads; ++i)
@@ -406,9 +384,6 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     barrier();
-#if defined(MQK_TILE_TRACE) && !defined(MQK_TILE_TRACE2)
-    if (g_tile_trace && tid == 0 && kt < 126) g_tile_trace[blockIdx.x * 256 + 2 * kt + 1] = __builtin_amdgcn_s_memrealtime();
-#endif
     if (kt + NS - 1 < nkt) issue(kt + NS - 1);
     const unsigned char* st = smem + (kt % NS) * S::kStageBytes;
 #pragma unroll
@@ -429,23 +404,13 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
       for (int mb = 0; mb < S::kMB; ++mb)
 #pragma unroll
         for (int nb = 0; nb < S::kNB; ++nb) {
-#ifdef MQK_DIAG_NOMFMA  // diagnostic build: K loop without MFMAs (timing only, wrong results)
-          acc[mb][nb][0] += __builtin_bit_cast(float, af[mb][0] ^ bf[nb][0]);
-#else
           acc[mb][nb] = mfma_32x32x16(af[mb], bf[nb], acc[mb][nb]);
-#endif
         }
     }
   }
   barrier();  // every wave is done with the ring; the epilogue reuses the LDS
-#if defined(MQK_TILE_TRACE) && !defined(MQK_TILE_TRACE2)
-  if (g_tile_trace && tid == 0) g_tile_trace[blockIdx.x * 256 + 252] = __builtin_amdgcn_s_memrealtime();
-#endif
 
   tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, cslot, ht, m0, p, e, smem);
-#if defined(MQK_TILE_TRACE) && !defined(MQK_TILE_TRACE2)
-  if (g_tile_trace && tid == 0) g_tile_trace[blockIdx.x * 256 + 253] = __builtin_amdgcn_s_memrealtime();
-#endif
 }
 
 template <int BM, int NH, int WM, int WN, int NS, int SBK = 32>

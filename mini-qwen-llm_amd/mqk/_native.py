@@ -194,11 +194,22 @@ def version() -> int:
 # ---------------------------------------------------------------------------
 # Workspace: one zero-initialised device buffer per (device, stream).  The
 # kernels leave its arrival counters at zero after each call, so it is zeroed
-# only when (re)allocated.  Keyed by stream because calls that may overlap must
-# not share a workspace.
+# only when allocated.  Keyed by stream because calls that may overlap must not
+# share a workspace.
+#
+# A HIP graph captured on a stream keeps the workspace address it was captured
+# with and writes partials and counters there on every replay.  A buffer is
+# therefore never released once a launch has used it: when a call needs more,
+# the stream gets a new, larger buffer (at least twice the old size, so this
+# happens a few times per stream at most) and the old one is retired, kept
+# allocated and zero-countered for the life of the process, where graphs
+# captured earlier still find it.  A buffer cannot be created during capture
+# (its zero fill would run only at replay), so that raises instead: run the op
+# once eagerly at the largest size before capturing.
 # ---------------------------------------------------------------------------
 _ws_lock = threading.Lock()
 _workspaces: dict = {}
+_retired: list = []
 
 
 def workspace(device: torch.device, stream, nbytes: int):
@@ -208,11 +219,23 @@ def workspace(device: torch.device, stream, nbytes: int):
     with _ws_lock:
         buf = _workspaces.get(key)
         if buf is None or buf.numel() < nbytes:
-            size = max(nbytes, 1 << 20)
+            if torch.cuda.is_current_stream_capturing():
+                raise MqkNativeError(
+                    f"the mqk workspace of this stream must grow to {nbytes} bytes during HIP-graph "
+                    "capture; run the op once eagerly on this stream at the largest size before capturing")
+            old = 0 if buf is None else buf.numel()
+            size = max(nbytes, 2 * old, 1 << 20)
             with torch.cuda.stream(stream):
-                buf = torch.zeros(size, dtype=torch.uint8, device=device)
-            _workspaces[key] = buf
+                new = torch.zeros(size, dtype=torch.uint8, device=device)
+            if buf is not None:
+                _retired.append(buf)  # graphs captured earlier may still point at it
+            _workspaces[key] = buf = new
         return buf
+
+
+def retired_workspaces() -> int:
+    """Number of superseded workspaces kept alive for graphs captured earlier."""
+    return len(_retired)
 
 
 def ptr(t) -> int | None:

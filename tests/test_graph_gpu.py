@@ -96,9 +96,21 @@ def _replay_checks(graph, outs, want, rerun):
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("T", [32, 200])
-def test_graph_replay_w4a16(T, device):
-    """The W4A16 front (decode kernel at T = 32, tile + tail launches at T = 200)."""
+@pytest.mark.parametrize("T,plan", [(32, ["decode<1>"]), (200, ["decode<4>"]),
+                                    (4128, ["tile_w4", "decode<1>"])])
+def test_graph_replay_w4a16(T, plan, device):
+    """The W4A16 front under capture, one case per launch plan: the decode kernel
+    (T = 32), one four-block decode launch (T = 200), and the tile launch plus
+    the decode-kernel tail launch (T = 4128 = 16 row tiles of 256 + 32 rows,
+    whose 17th row tile would cost a second round over the CUs).  The plan is
+    checked from the kernels the eager call launches."""
+    from conftest import launched_kernels
+    run = _w4a16_case(T, device)
+    assert launched_kernels(run) == plan
+    _graph_replay(run, device)
+
+
+def _w4a16_case(T, device):
     import mqk
     hidden, Hq, Hkv, D = 1024, 16, 8, 128
     g = torch.Generator().manual_seed(T)
@@ -112,7 +124,10 @@ def test_graph_replay_w4a16(T, device):
     c, s = mqk.rope_tables(D, 4096)
     cos, sin = c.bfloat16().to(device), s.bfloat16().to(device)
     pos = torch.randint(0, 4096, (T,), generator=g, dtype=torch.int32).to(device)
-    run = lambda: mqk.fused_qkv_rope_w4a16(x, *projs, gq, gk, cos, sin, pos)
+    return lambda: mqk.fused_qkv_rope_w4a16(x, *projs, gq, gk, cos, sin, pos)
+
+
+def _graph_replay(run, device):
     stream = torch.cuda.Stream(device)
     with torch.cuda.stream(stream):
         eager = run()
@@ -121,6 +136,70 @@ def test_graph_replay_w4a16(T, device):
         with torch.cuda.graph(graph, stream=stream):
             out = run()
     _replay_checks(graph, out, eager, run)
+
+
+def test_graph_survives_workspace_growth(device):
+    """A graph captured with a small workspace replays correctly after a later
+    eager call on the same stream needed a larger one.
+
+    The decode step (T = 64) is captured with the one-block workspace; an eager
+    T = 256 call (one four-block decode launch) then needs four times the
+    partials.  The stream gets a new workspace and the old one stays allocated,
+    so the replayed decode kernel still writes its partials and counters into
+    memory nothing else owns.  Freed and refilled allocator blocks would expose a
+    replay into released memory: stale counters would leave no finisher, and the
+    outputs would keep the zeros written before each replay."""
+    import mqk
+    from mqk import _native
+    hidden, Hq, Hkv = 1024, 16, 8
+    small = Case(64, 1, hidden, Hq, Hkv, seed=4242, rows=4096,
+                 positions=torch.randint(0, 4096, (64,), generator=torch.Generator().manual_seed(1),
+                                         dtype=torch.int32))
+    big = Case(1, 256, hidden, Hq, Hkv, seed=4243)
+    lib = _native.library()
+    assert lib.mqk_fused_qkv_rope_workspace_size(256, Hq, Hkv, hidden) > \
+        2 * lib.mqk_fused_qkv_rope_workspace_size(64, Hq, Hkv, hidden)
+    a_small, a_big = small.args(device), big.args(device)
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        eager = mqk.fused_qkv_rope(*a_small)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = mqk.fused_qkv_rope(*a_small)
+        retired = _native.retired_workspaces()
+        want_big = mqk.fused_qkv_rope(*a_big)  # grows this stream's workspace
+        stream.synchronize()
+    assert _native.retired_workspaces() == retired + 1
+    torch.cuda.empty_cache()
+    junk = [torch.full((1 << 22,), -1, dtype=torch.int32, device=device) for _ in range(16)]
+    for rep in range(3):
+        for t in out:
+            t.fill_(0)
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(out, eager)), f"replay {rep}"
+        with torch.cuda.stream(stream):
+            again = mqk.fused_qkv_rope(*a_big)  # eager work on the grown workspace between replays
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(again, want_big))
+    del junk
+
+
+def test_workspace_growth_during_capture_raises(device):
+    """A stream whose workspace would have to grow inside a capture raises (its
+    zero fill would only run at replay) instead of capturing a wrong launch."""
+    import mqk
+    case = Case(48, 1, 1024, 16, 8, seed=4244, rows=4096,
+                positions=torch.arange(48, dtype=torch.int32))
+    args = case.args(device)
+    stream = torch.cuda.Stream(device)  # fresh stream: no workspace yet
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(mqk.MqkNativeError, match="before capturing"):
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                mqk.fused_qkv_rope(*args)
 
 
 def test_graph_replay_paged_input_norm_decode(device):

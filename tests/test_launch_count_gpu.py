@@ -1,0 +1,86 @@
+"""Kernel launches per call, counted with torch.profiler.
+
+The reference counts device kernels of the unfused and the fused front the
+same way (tests/test_fused_qkv_rope.py:287-311; 33 unfused against 6 fused,
+docs/02_fused_qkv_rope.md:65-67).  Here the whole front is one launch in the
+common cases; a split-off tail adds a decode launch, the fused input RMSNorm
+adds its pre-pass, and mid token counts run as decode launches of up to four
+64-row blocks each.  Each case names the plan it expects, so a change of the
+planner shows up here as well as in the timings.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import Case, launched_kernels
+
+pytestmark = pytest.mark.gpu
+
+HID, HQ, HKV = 4096, 32, 8  # Qwen3-8B attention shapes (BASELINE configs 2 and 3)
+
+
+def _bf16_call(case, device, **ext):
+    import mqk
+    args = case.args(device)
+    if ext:
+        return lambda: mqk.fused_qkv_rope_ex(*args, **ext)
+    return lambda: mqk.fused_qkv_rope(*args)
+
+
+def test_prefill_c2_is_one_tile_launch(device):
+    case = Case(4, 512, HID, HQ, HKV, seed=11)
+    assert launched_kernels(_bf16_call(case, device)) == ["tile"]
+
+
+def test_decode_c3_is_one_decode_launch(device):
+    pos = torch.randint(0, 8192, (64,), generator=torch.Generator().manual_seed(3), dtype=torch.int32)
+    case = Case(64, 1, HID, HQ, HKV, seed=12, rows=8192, positions=pos)
+    assert launched_kernels(_bf16_call(case, device)) == ["decode<1>"]
+
+
+@pytest.mark.parametrize("T,plan", [(128, ["decode<2>"]), (256, ["decode<4>"]),
+                                    (448, ["decode<4>", "decode<3>"])])
+def test_mid_t_decode_block_launches(T, plan, device):
+    case = Case(1, T, HID, HQ, HKV, seed=13 + T)
+    assert launched_kernels(_bf16_call(case, device)) == plan
+
+
+def test_tail_split_adds_one_decode_launch(device):
+    """2080 tokens in 128 x 384 tiles: 16 full row tiles fill the 256 CUs once,
+    and the last 32 rows go to the decode kernel instead of a second round."""
+    import mqk
+    case = Case(1, 2080, HID, HQ, HKV, seed=14)
+    mqk.set_option("prefill_tile", 16)
+    try:
+        assert launched_kernels(_bf16_call(case, device)) == ["tile", "decode<1>"]
+        mqk.set_option("tail_split", 0)
+        assert launched_kernels(_bf16_call(case, device)) == ["tile"]
+    finally:
+        mqk.set_option("tail_split", 1)
+        mqk.set_option("prefill_tile", 0)
+
+
+@pytest.mark.parametrize("B,S,plan", [(64, 1, ["row_scale", "decode<1>"]), (4, 512, ["row_scale", "tile"])])
+def test_input_norm_adds_its_pre_pass(B, S, plan, device):
+    g = torch.Generator().manual_seed(15)
+    pos = torch.randint(0, 4096, (B * S,), generator=g, dtype=torch.int32) if S == 1 else None
+    case = Case(B, S, HID, HQ, HKV, seed=15, rows=4096 if S == 1 else S, positions=pos)
+    in_w = (1 + 0.1 * torch.randn(HID, generator=g)).bfloat16().to(device)
+    assert launched_kernels(_bf16_call(case, device, input_norm_w=in_w)) == plan
+
+
+def test_w4a16_front_is_one_launch(device):
+    import mqk
+    g = torch.Generator().manual_seed(16)
+    hidden, Hq, Hkv, D, T = 1024, 16, 8, 128, 2048
+    projs = []
+    for h in (Hq, Hkv, Hkv):
+        w = torch.randn(hidden, h * D, generator=g) * 0.02
+        projs.append(tuple(t.to(device) for t in mqk.per_group_minmax_quantize(w, 128, torch.float16)))
+    x = torch.randn(1, T, hidden, generator=g).bfloat16().to(device)
+    gq = torch.ones(D, dtype=torch.bfloat16, device=device)
+    c, s = mqk.rope_tables(D, T)
+    cos, sin = c.bfloat16().to(device), s.bfloat16().to(device)
+    run = lambda: mqk.fused_qkv_rope_w4a16(x, *projs, gq, gq, cos, sin)
+    assert launched_kernels(run) == ["tile_w4"]
