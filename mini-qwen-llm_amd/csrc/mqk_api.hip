@@ -174,17 +174,22 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
                 (long long)g_prefill_tile.load(), p.n_tiles, int4 ? ", int4 weights" : "");
   // (the decode kernel's arrival counters open every workspace and must stay zero,
   // so the scales never start before them, whichever kernel runs this call)
+  // (the four-block decode kernel with the input norm would spill registers)
+  if (p.in_gamma && pl.passes > 3) pl.passes = 3;
   size_t base = pl.splits > 0 ? decode_workspace_bytes(p.n_tiles, pl.splits, pl.passes) : decode_counter_bytes();
-  if (!pl.v && pl.passes > 1 && (!workspace || ws_bytes < align_up(base, 256))) {
+  // bytes the plan needs: the decode region, then (input norm) the per-token scales
+  const size_t scale_bytes = p.in_gamma ? align_up(size_t(p.M) * sizeof(float), 256) : 0;
+  auto fits = [&](size_t b) { return workspace && ws_bytes >= align_up(b, 256) + scale_bytes; };
+  if (!pl.v && pl.passes > 1 && !fits(base)) {
     pl.passes = 1;  // a workspace sized for one block per launch
     base = decode_workspace_bytes(p.n_tiles, pl.splits, 1);
   }
-  if (!pl.v && p.M > 64 && (!workspace || ws_bytes < align_up(base, 256))) {
+  if (!pl.v && p.M > 64 && !fits(base)) {
     // decode blocks planned, but a workspace sized without them: the tile kernel
     pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), false);
     base = pl.splits > 0 ? decode_workspace_bytes(p.n_tiles, pl.splits) : decode_counter_bytes();
   }
-  if (pl.v && pl.splits > 0 && (!workspace || ws_bytes < align_up(base, 256))) {
+  if (pl.v && pl.splits > 0 && !fits(base)) {
     pl.tail = 0;  // a workspace sized without the tail launch: run the tile kernel on every row
     pl.splits = 0;
     base = decode_counter_bytes();

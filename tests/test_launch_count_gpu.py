@@ -4,7 +4,8 @@ The reference counts device kernels of the unfused and the fused front the
 same way (tests/test_fused_qkv_rope.py:287-311; 33 unfused against 6 fused,
 docs/02_fused_qkv_rope.md:65-67).  Here the whole front is one launch in the
 common cases; a split-off tail adds a decode launch, the fused input RMSNorm
-adds its pre-pass, and mid token counts run as decode launches of up to four
+adds its pre-pass (and caps a decode launch at three blocks, whose
+four-block form would spill registers), and mid token counts run as decode launches of up to four
 64-row blocks each.  Each case names the plan it expects, so a change of the
 planner shows up here as well as in the timings.
 """
@@ -61,7 +62,8 @@ def test_tail_split_adds_one_decode_launch(device):
         mqk.set_option("prefill_tile", 0)
 
 
-@pytest.mark.parametrize("B,S,plan", [(64, 1, ["row_scale", "decode<1>"]), (4, 512, ["row_scale", "tile"])])
+@pytest.mark.parametrize("B,S,plan", [(64, 1, ["row_scale", "decode<1>"]), (4, 512, ["row_scale", "tile"]),
+                                      (1, 256, ["row_scale", "decode<3>", "decode<1>"])])
 def test_input_norm_adds_its_pre_pass(B, S, plan, device):
     g = torch.Generator().manual_seed(15)
     pos = torch.randint(0, 4096, (B * S,), generator=g, dtype=torch.int32) if S == 1 else None
