@@ -100,6 +100,25 @@ int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
 size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden);
 
 /*
+ * mqk_fused_qkv_rope_bf16 without a workspace argument: allocates nothing, for
+ * callers that cannot call hipMalloc (code under HIP-graph capture, tight
+ * serving loops, harnesses that forbid allocation).  It has no counterpart in
+ * the reference.  The decode kernel's counters and partials live in a fixed
+ * device array of 4 KiB + 8 MiB per GPU, held until the process ends; calls
+ * whose decode launch needs more (e.g. T <= 64 with more than 256 heads x
+ * splits) return MQK_ERR_WORKSPACE before launching anything, and larger T run
+ * with fewer 64-row blocks per decode launch (bit-identical results).  Every
+ * call on a GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller.
+ */
+int mqk_fused_qkv_rope_bf16_noalloc(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
+                                    const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                                    const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                                    int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                                    int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                                    void* stream);
+
+/*
  * QK-Norm + RoPE alone on already-projected q/k (bf16), the functional twin
  * of _qk_norm_rope_kernel (mini_qwen/kernels/fused_qkv_rope.py:46-127):
  *   q_raw [T, Hq, D] -> q_out, k_raw [T, Hkv, D] -> k_out.

@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/mqk.h"
 #include "mqk_device.h"
@@ -387,6 +388,88 @@ int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
                             void* workspace, size_t ws_bytes, void* stream) {
   return fused_bf16_impl(x, w_q, w_k, w_v, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D,
                          cos_rows, eps, q, k, v, nullptr, workspace, ws_bytes, stream);
+}
+
+// ---- allocation-free variant of mqk_fused_qkv_rope_bf16 ---------------------------------
+// The decode kernel's scratch (its arrival counters, then its fp32 split partials)
+// lives in this file-scope device array instead of a caller workspace: 4 KiB of
+// counters plus 8 MiB of partials, enough for one 64-row block of any head count
+// up to one split per CU (e.g. 48 heads x 5 splits at hidden 4096: 7.5 MiB).
+// Each GPU holds its own copy for the life of the process.  Host code never
+// passes `scratch` itself to a kernel (in host code the name is a stand-in, not a
+// device address): the device address comes from hipGetSymbolAddress, once per
+// device, and only that address is used.
+}  // extern "C"
+
+static __device__ __align__(256) unsigned char scratch[4096 + (size_t(8) << 20)];
+
+namespace {
+
+constexpr size_t kScratchBytes = sizeof(scratch);
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+__global__ void clear_words_kernel(uint32_t* words, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) words[i] = 0u;
+}
+
+// Device address of this device's scratch (set up on the first call on a device).
+int scratch_address(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return hip_status(err, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(MQK_ERR_UNSUPPORTED, "device %d beyond %d devices", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr) return hip_status(err != hipSuccess ? err : hipErrorInvalidSymbol,
+                                                     "hipGetSymbolAddress(scratch)");
+    // The counters must start at zero (every call leaves them so).  Device
+    // globals are zero when the code object loads; they are cleared once more
+    // here with a fill kernel, unless the stream is being captured (the fill
+    // would then run only at replay).
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    err = hipStreamIsCapturing(stream, &cs);
+    if (err != hipSuccess) return hip_status(err, "hipStreamIsCapturing");
+    if (cs == hipStreamCaptureStatusNone) {
+      const int words = int(decode_counter_bytes() / 4);
+      hipLaunchKernelGGL(clear_words_kernel, dim3((words + 255) / 256), dim3(256), 0, stream,
+                         static_cast<uint32_t*>(ptr), words);
+      err = hipGetLastError();
+      if (err != hipSuccess) return hip_status(err, "scratch clear launch");
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MQK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mqk_fused_qkv_rope_bf16_noalloc(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
+                                    const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                                    const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                                    int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                                    int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                                    void* stream) {
+  void* ws = nullptr;
+  if (T > 0) {
+    const int st = scratch_address(static_cast<hipStream_t>(stream), &ws);
+    if (st != MQK_OK) return st;
+  }
+  const int st = fused_bf16_impl(x, w_q, w_k, w_v, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv,
+                                 D, cos_rows, eps, q, k, v, nullptr, ws, kScratchBytes, stream);
+  if (st == MQK_ERR_WORKSPACE)
+    return fail(MQK_ERR_WORKSPACE,
+                "T=%lld with %d heads at hidden %lld needs more than the %zu-byte fixed scratch of "
+                "mqk_fused_qkv_rope_bf16_noalloc (use mqk_fused_qkv_rope_bf16 with a workspace)",
+                (long long)T, Hq + 2 * Hkv, (long long)hidden, kScratchBytes);
+  return st;
 }
 
 int mqk_fused_qkv_rope_paged_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
