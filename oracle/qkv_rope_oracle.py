@@ -23,7 +23,11 @@ Pinning (what checks each function against something other than itself):
   * row selection       -- prefill ``t % S`` vs positions mode, sentinel tables.
   * varlen_positions    -- hand-worked offsets with an empty sequence, and a
                            brute-force scan of cu_seqlens for every token.
+  * paged_slot          -- hand-worked slots of a small block table, and a
+                           brute-force scan of every slot of the cache.
   * int4 pack/unpack    -- hand-packed 0x76543210 known answer, round trips.
+  * awq_unpack          -- hand-packed 0x75316420 known answer (AutoAWQ's
+                           nibble order), brute-force per-nibble decode.
   * minmax quantizer    -- hand-computed group, error <= scale/2, zero exact.
   * dequant / w4a16     -- brute-force nibble-by-nibble restatement.
 There is no function here marked "parity unpinned"; the GEMM's bf16 bit pattern
@@ -296,6 +300,34 @@ def unpack_int4(packed: np.ndarray) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
+# Paged KV cache addressing  (paged_attn_prefill.py:45-56, kv_cache.py:3-6)
+# ---------------------------------------------------------------------------
+
+def paged_slot(block_table, seq, pos, block_size: int = 16, num_blocks=None) -> np.ndarray:
+    """Flat cache slot of each token: ``block_table[seq, pos // bs] * bs + pos % bs``.
+
+    The cache is ``[num_blocks, block_size, H_kv, D]`` (kv_cache.py:3-6), so a
+    token's K/V row of head h sits at row ``slot * H_kv + h`` of the flattened
+    cache.  The scatter kernel computes ``page_idx = pos // PAGE_SIZE``,
+    ``slot = pos % PAGE_SIZE``, ``phys = Block_table[batch_id, page_idx]``
+    (paged_attn_prefill.py:47-51).  The reference does not bound-check; here a
+    token whose sequence, page or block falls outside the table (or outside
+    ``num_blocks``) gets -1: nothing is written for it.
+    """
+    bt = np.asarray(block_table, dtype=np.int64)
+    seq = np.asarray(seq, dtype=np.int64)
+    pos = np.asarray(pos, dtype=np.int64)
+    rows, cols = bt.shape
+    page = np.where(pos >= 0, pos // block_size, -1)
+    ok = (seq >= 0) & (seq < rows) & (pos >= 0) & (page < cols)
+    blk = np.where(ok, bt[np.clip(seq, 0, rows - 1), np.clip(page, 0, cols - 1)], -1)
+    if num_blocks is not None:
+        ok &= (blk >= 0) & (blk < num_blocks)
+    ok &= blk >= 0
+    return np.where(ok, blk * block_size + pos % block_size, -1)
+
+
+# ---------------------------------------------------------------------------
 # Per-group min-max quantizer  (mini_qwen/quantization/awq.py:14-58)
 # ---------------------------------------------------------------------------
 
@@ -333,6 +365,34 @@ def dequant(qweight, scales_f32, qzeros, group_size: int = 128) -> np.ndarray:
     G = K // group_size
     qg = q.reshape(G, group_size, N)
     return ((qg - z[:, None, :]) * s[:, None, :]).reshape(K, N)
+
+
+# AutoAWQ checkpoints (the "GEMM" layout, AutoAWQ 0.2.x, awq/modules/linear/gemm.py,
+# WQLinear_GEMM.from_linear; not vendored in the reference) pack 8 values along N
+# into each int32 with the order map (0, 2, 4, 6, 1, 3, 5, 7): nibble i of word
+# [r, j] holds column 8*j + AWQ_ORDER[i].  qweight is [K, N/8], qzeros [K/g, N/8],
+# scales [K/g, N] fp16; the weight is (q - z) * s as in the reference's format.
+AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
+
+
+def awq_unpack(words: np.ndarray) -> np.ndarray:
+    """AutoAWQ words ``[R, N/8]`` int32 -> values ``[R, N]`` in column order."""
+    p = np.asarray(words).astype(np.int32).view(np.uint32)
+    R, n8 = p.shape
+    out = np.empty((R, n8, 8), dtype=np.int32)
+    for i, c in enumerate(AWQ_ORDER):
+        out[:, :, c] = ((p >> np.uint32(4 * i)) & np.uint32(0xF)).astype(np.int32)
+    return out.reshape(R, n8 * 8)
+
+
+def dequant_awq(qweight_awq, qzeros_awq, scales_f32, group_size: int = 128) -> np.ndarray:
+    """fp32 ``[K, N]`` = ``(q - z) * s`` read straight from AutoAWQ words."""
+    q = awq_unpack(qweight_awq).astype(np.float32)
+    z = awq_unpack(qzeros_awq).astype(np.float32)
+    s = np.asarray(scales_f32, dtype=np.float32)
+    K, N = q.shape
+    G = K // group_size
+    return ((q.reshape(G, group_size, N) - z[:, None, :]) * s[:, None, :]).reshape(K, N)
 
 
 def gptq_zero_fix(qzeros: np.ndarray) -> np.ndarray:

@@ -350,3 +350,67 @@ def test_varlen_positions_brute_force():
     for t in range(int(cu[-1])):
         s = [i for i in range(13) if cu[i] <= t < cu[i + 1]]
         assert len(s) == 1 and b[t] == s[0] and p[t] == t - cu[s[0]] + start[s[0]]
+
+
+# ── paged-cache slots (paged_attn_prefill.py:45-56, kv_cache.py:3-6) ─────────
+
+def test_paged_slot_known_answer():
+    """Block size 4, two sequences: seq 0 owns blocks (5, 2), seq 1 owns (0, 7).
+    pos 0 of seq 0 -> block 5, slot 0 -> 20; pos 6 of seq 0 -> page 1 = block 2,
+    slot 2 -> 10; pos 3 of seq 1 -> block 0, slot 3 -> 3; pos 5 of seq 1 ->
+    block 7, slot 1 -> 29.  Out of the table: pos 8 (page 2), seq 2, pos -1,
+    and a block id beyond num_blocks."""
+    bt = np.array([[5, 2], [0, 7]])
+    got = orc.paged_slot(bt, [0, 0, 1, 1, 0, 2, 1], [0, 6, 3, 5, 8, 0, -1], block_size=4, num_blocks=8)
+    assert got.tolist() == [20, 10, 3, 29, -1, -1, -1]
+    assert orc.paged_slot(np.array([[9]]), [0], [1], 4, num_blocks=8).tolist() == [-1]
+
+
+def test_paged_slot_brute_force():
+    """Every (seq, pos) of a random table: the slot is the unique cache position
+    whose (block, offset) pair the table assigns to that token."""
+    rng = np.random.default_rng(8)
+    bs, rows, cols = 16, 3, 5
+    nb = rows * cols + 4
+    bt = rng.permutation(nb)[: rows * cols].reshape(rows, cols)
+    owner = {}  # cache slot -> (seq, pos), by walking the cache
+    for blk in range(nb):
+        for off in range(bs):
+            hit = [(s, c) for s in range(rows) for c in range(cols) if bt[s, c] == blk]
+            if hit:
+                s, c = hit[0]
+                owner[blk * bs + off] = (s, c * bs + off)
+    seqs, poss = np.meshgrid(np.arange(rows), np.arange(cols * bs), indexing="ij")
+    got = orc.paged_slot(bt, seqs.ravel(), poss.ravel(), bs, nb)
+    for slot, s, p in zip(got, seqs.ravel(), poss.ravel()):
+        assert owner[int(slot)] == (s, p)
+    assert len(set(got.tolist())) == got.size
+
+
+# ── AutoAWQ words (AWQ order 0,2,4,6,1,3,5,7) ─────────────────────────────────
+
+def test_awq_unpack_known_answer():
+    """Column c of an 8-column group holding value c packs to 0x75316420: nibble
+    i holds column (0,2,4,6,1,3,5,7)[i], so nibbles read 0,2,4,6,1,3,5,7."""
+    w = np.array([[0x75316420, 0x00000000, 0x11111111]], dtype=np.uint32).view(np.int32)
+    got = orc.awq_unpack(w)
+    assert got[0, :8].tolist() == list(range(8))
+    assert got[0, 8:16].tolist() == [0] * 8 and got[0, 16:].tolist() == [1] * 8
+    hi = np.array([[np.uint32(0xF0000000)]]).view(np.int32)   # top nibble = nibble 7 -> column 7
+    assert orc.awq_unpack(hi)[0].tolist() == [0] * 7 + [15]
+
+
+def test_dequant_awq_brute_force():
+    rng = np.random.default_rng(9)
+    K, N, g = 256, 16, 128
+    words = rng.integers(0, 2**32, (K, N // 8), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    zw = rng.integers(0, 2**32, (K // g, N // 8), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    s = rng.uniform(0.005, 0.02, (K // g, N)).astype(np.float32)
+    got = orc.dequant_awq(words, zw, s, g)
+    order = (0, 2, 4, 6, 1, 3, 5, 7)
+    for k in range(0, K, 37):
+        for n in range(N):
+            i = order.index(n % 8)  # nibble holding column n
+            q = (int(words.view(np.uint32)[k, n // 8]) >> (4 * i)) & 0xF
+            z = (int(zw.view(np.uint32)[k // g, n // 8]) >> (4 * i)) & 0xF
+            assert got[k, n] == np.float32((q - z) * s[k // g, n])

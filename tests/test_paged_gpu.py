@@ -34,9 +34,11 @@ def _block_table(n_seq, blocks_per_seq, num_blocks, seed):
     return perm.view(n_seq, blocks_per_seq).to(torch.int32)
 
 
-def _expected_slots(seq, pos, bt, block_size):
-    blk = bt[seq, pos // block_size]
-    return blk * block_size + pos % block_size
+def _expected_slots(seq, pos, bt, block_size, num_blocks=None):
+    """Flat cache slot of every token, from the oracle's restatement of the
+    reference scatter (paged_attn_prefill.py:47-51); -1 = not written."""
+    from oracle import qkv_rope_oracle as orc
+    return orc.paged_slot(bt, seq, pos, block_size, num_blocks)
 
 
 def _check_cache(cache, rows, slots, label):
@@ -111,15 +113,17 @@ def test_paged_out_of_range_entries_skipped(device):
     q, k, v = mqk.fused_qkv_rope_paged(x, wq, wk, wv, gq, gk, cos, sin, kc, vc, bt.to(device))
     torch.cuda.synchronize()
     t = np.arange(S)
-    ok = (t // bs == 0) | (t // bs == 3)
-    slots = _expected_slots(np.zeros(ok.sum(), dtype=np.int64), t[ok], bt.numpy(), bs)
-    _check_cache(kc, k.reshape(S, Hkv, D)[torch.from_numpy(ok)], slots, "partial table k")
+    all_slots = _expected_slots(np.zeros(S, dtype=np.int64), t, bt.numpy(), bs, nb)
+    ok = all_slots >= 0
+    assert np.array_equal(ok, (t // bs == 0) | (t // bs == 3))  # pages 0 and 3 only
+    _check_cache(kc, k.reshape(S, Hkv, D)[torch.from_numpy(ok)], all_slots[ok], "partial table k")
     # a sequence index past the table
     seq = torch.full((S,), 5, dtype=torch.int32)
     kc2, vc2 = _caches(nb, bs, Hkv, device)
     mqk.fused_qkv_rope_paged(x, wq, wk, wv, gq, gk, cos, sin, kc2, vc2, bt.to(device),
                              kv_seq=seq.to(device))
     torch.cuda.synchronize()
+    assert (_expected_slots(seq.numpy(), t, bt.numpy(), bs, nb) == -1).all()
     assert bool((kc2.view(torch.int16) == SENTINEL).all())
 
 
