@@ -17,8 +17,9 @@ profiles/ when present.  ``cpu_baseline`` times a torch fp32 restatement of the
 reference's unfused composition (3 projections -> per-head RMSNorm -> RoPE) on
 the host's cores for a bounded sample of the same workload.
 ``secondary`` reports the other BASELINE configurations (decode, long prefill,
-W4A16) with their own roofline fractions; the decode step rotates 8 copies of
-the weights (400 MB, more than the 256 MB Infinity Cache) so it reads HBM.
+W4A16) with their own roofline fractions; every step rotates over several copies
+of its inputs (decode: 8 weight sets, 400 MB; prefill and W4A16: 6 sets of x and
+weights, 300-480 MB), more than the 256 MB Infinity Cache, so it reads HBM.
 Config 1 (the Qwen3-0.6B-shaped layer, B=1 x S=128, which the reference runs
 on the CPU in fp32) is reported as the op's bf16 GPU time next to the oracle's
 fp32 composition timed on the host.
@@ -91,12 +92,21 @@ def time_steps(fn, steps, warmup):
     return e0.elapsed_time(e1) / steps, wall
 
 
-def bench_prefill(S_total, B, S, hidden, Hq, Hkv, seed, steps, warmup, dev):
+def bench_prefill(S_total, B, S, hidden, Hq, Hkv, seed, steps, warmup, dev, copies=6):
+    """Steps rotate over `copies` sets of (x, weights), more bytes than the 256 MB
+    Infinity Cache for the BASELINE prefill configs, so each step reads its
+    inputs from HBM instead of finding the previous step's in the cache."""
     import mqk
-    x, ws, gq, gk, cos, sin = make_inputs(S_total, hidden, Hq, Hkv, S, seed, dev)
-    x = x.reshape(B, S, hidden)
-    wq, wk, wv = ws[0]
-    return time_steps(lambda i: mqk.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin), steps, warmup)
+    x, ws, gq, gk, cos, sin = make_inputs(S_total, hidden, Hq, Hkv, S, seed, dev, copies)
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed + 7)
+    xs = [x.reshape(B, S, hidden)] + [torch.randn(B, S, hidden, generator=g, device=dev).bfloat16()
+                                      for _ in range(copies - 1)]
+
+    def step(i):
+        wq, wk, wv = ws[i % copies]
+        return mqk.fused_qkv_rope(xs[i % copies], wq, wk, wv, gq, gk, cos, sin)
+    return time_steps(step, steps, warmup)
 
 
 def bench_decode(B, hidden, Hq, Hkv, seed, steps, warmup, dev, copies=8):
@@ -113,9 +123,10 @@ def bench_decode(B, hidden, Hq, Hkv, seed, steps, warmup, dev, copies=8):
     return time_steps(step, steps, warmup)
 
 
-def bench_w4a16(hidden, Hq, Hkv, seed, steps, warmup, dev):
+def bench_w4a16(hidden, Hq, Hkv, seed, steps, warmup, dev, copies=6):
     """Config 5: 16 packed sequences, lengths U[1,1024], starts U[0,4096), int4
-    weights (group 128, fp16 scales U(0.005, 0.02), zeros U{0..15})."""
+    weights (group 128, fp16 scales U(0.005, 0.02), zeros U{0..15}).  Steps
+    rotate over `copies` sets of (x, weights), more than the Infinity Cache holds."""
     import torch
     import mqk
     g = torch.Generator().manual_seed(seed)
@@ -124,21 +135,26 @@ def bench_w4a16(hidden, Hq, Hkv, seed, steps, warmup, dev):
     pos = torch.cat([s + torch.arange(int(n)) for s, n in zip(starts, lens)]).to(torch.int32)
     T = int(lens.sum())
     gd = torch.Generator(device=dev).manual_seed(seed)
-    x = torch.randn(1, T, hidden, generator=gd, device=dev).bfloat16()
-    projs = []
-    for h in (Hq, Hkv, Hkv):
-        N = h * D
-        qw = torch.randint(-2**31, 2**31 - 1, (hidden // 8, N), generator=gd, device=dev,
-                           dtype=torch.int64).to(torch.int32)
-        sc = (0.005 + 0.015 * torch.rand(hidden // 128, N, generator=gd, device=dev)).half()
-        qz = torch.randint(-2**31, 2**31 - 1, (hidden // 128, N // 8), generator=gd, device=dev,
-                           dtype=torch.int64).to(torch.int32)
-        projs.append((qw, sc, qz))
+    xs = [torch.randn(1, T, hidden, generator=gd, device=dev).bfloat16() for _ in range(copies)]
+
+    def int4_set():
+        projs = []
+        for h in (Hq, Hkv, Hkv):
+            N = h * D
+            qw = torch.randint(-2**31, 2**31 - 1, (hidden // 8, N), generator=gd, device=dev,
+                               dtype=torch.int64).to(torch.int32)
+            sc = (0.005 + 0.015 * torch.rand(hidden // 128, N, generator=gd, device=dev)).half()
+            qz = torch.randint(-2**31, 2**31 - 1, (hidden // 128, N // 8), generator=gd, device=dev,
+                               dtype=torch.int64).to(torch.int32)
+            projs.append((qw, sc, qz))
+        return projs
+    sets = [int4_set() for _ in range(copies)]
     gq = (1 + 0.1 * torch.randn(D, generator=gd, device=dev)).bfloat16()
     gk = (1 + 0.1 * torch.randn(D, generator=gd, device=dev)).bfloat16()
     cos, sin = (t.to(dev).bfloat16() for t in mqk.rope_tables(D, 8192))
     pos = pos.to(dev)
-    ms, _ = time_steps(lambda i: mqk.fused_qkv_rope_w4a16(x, *projs, gq, gk, cos, sin, pos), steps, warmup)
+    ms, _ = time_steps(lambda i: mqk.fused_qkv_rope_w4a16(xs[i % copies], *sets[i % copies], gq, gk, cos, sin, pos),
+                       steps, warmup)
     return ms, T
 
 
@@ -147,7 +163,9 @@ def cpu_baseline(budget_s=12.0):
 
     oracle/torch_baseline.py restates tests/test_fused_qkv_rope.py:244-259 (three
     projections -> per-head RMSNorm -> rotate-half RoPE) with torch CPU tensors,
-    on torch's intra-op thread pool (OMP_NUM_THREADS when set).  Sample: one
+    on torch's intra-op thread pool: one thread per core this process may run
+    on (sched_getaffinity), capped by OMP_NUM_THREADS when that is set (the
+    GPU box's CPU share).  Sample: one
     sequence of the headline workload (B=1, S=512 of the B=4 x S=512 batch; hidden
     4096, 32/8 heads), repeated until ~budget_s of wall time, median reported."""
     import numpy as np
@@ -164,6 +182,9 @@ def cpu_baseline(budget_s=12.0):
     gq = t(orc.round_bf16(1 + 0.1 * rng.standard_normal(D, dtype=np.float32)))
     gk = t(orc.round_bf16(1 + 0.1 * rng.standard_normal(D, dtype=np.float32)))
     cos, sin = (t(a) for a in orc.rope_tables(D, S))
+    affinity = len(os.sched_getaffinity(0))
+    threads = min(affinity, int(os.environ.get("OMP_NUM_THREADS", affinity) or affinity))
+    torch.set_num_threads(threads)
     times = []
     with torch.inference_mode():
         unfused_composition_torch(x, wq, wk, wv, gq, gk, cos, sin)  # warm-up
@@ -176,7 +197,7 @@ def cpu_baseline(budget_s=12.0):
                 break
     med = sorted(times)[len(times) // 2]
     return {"value": round(S / med, 1), "unit": "tokens/s", "cores": int(torch.get_num_threads()),
-            "kind": "port",
+            "affinity_cores": affinity, "kind": "port",
             "sample": f"torch fp32 CPU restatement of the reference's unfused composition "
                       f"(test_fused_qkv_rope.py:244-259), B=1 x S=512 of the B=4 x S=512 Qwen3-8B "
                       f"prefill, median of {len(times)} reps, {med * 1e3:.1f} ms/rep"}

@@ -104,7 +104,7 @@ size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hid
  * callers that cannot call hipMalloc (code under HIP-graph capture, tight
  * serving loops, harnesses that forbid allocation).  It has no counterpart in
  * the reference.  The decode kernel's counters and partials live in a fixed
- * device array of 4 KiB + 8 MiB per GPU, held until the process ends; calls
+ * device array of 4.25 KiB + 8 MiB per GPU, held until the process ends; calls
  * whose decode launch needs more (e.g. T <= 64 with more than 256 heads x
  * splits) return MQK_ERR_WORKSPACE before launching anything, and larger T run
  * with fewer 64-row blocks per decode launch (bit-identical results).  Every
@@ -287,7 +287,11 @@ int mqk_fused_qkv_rope_ex_w4a16(const mqk_bf16* x, const int32_t* qw_q, const vo
  *                    the weights once for all of them (1..4; the workspace size grows with it)
  *   "decode_force_recompute"  1: the decode kernel takes its recompute path (used when a
  *                    split ran on an unexpected XCD) for every head; for tests
- * Returns MQK_OK or MQK_ERR_BAD_OPTION.
+ * Returns MQK_OK or MQK_ERR_BAD_OPTION.  mqk_get_option also reads "device_cus" and
+ * "device_xcds": the compute units and XCDs of the current device, as the planner and
+ * the decode kernel's grid use them (hipDeviceGetAttribute; -1 for unknown names).
+ * Heads the decode kernel finished on its recompute path are counted in the
+ * first word after the per-head counters of the workspace (byte offset 4096).
  */
 int mqk_set_option(const char* name, int64_t value);
 int64_t mqk_get_option(const char* name);

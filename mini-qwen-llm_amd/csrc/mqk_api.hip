@@ -98,7 +98,40 @@ bool epilogue_aligned(const EpilogueArgs& e) {
   return aligned16(e.q_gamma) && aligned16(e.k_gamma) && aligned16(e.cos) && aligned16(e.sin);
 }
 
-constexpr int64_t kCus = 256;  // MI355X compute units: one pipelined tile per CU at a time
+// Compute units and XCDs of the calling thread's current device, queried once
+// per device (an MI355X has 256 CUs in 8 XCDs; a partitioned one fewer).
+struct Topology {
+  int cus = 256;
+  int xcds = 8;
+};
+constexpr int kMaxTopoDevices = 64;
+std::mutex g_topo_mu;
+Topology g_topo[kMaxTopoDevices];
+bool g_topo_known[kMaxTopoDevices] = {};
+
+Topology device_topology() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxTopoDevices) {
+    (void)hipGetLastError();
+    return Topology{};
+  }
+  std::lock_guard<std::mutex> lock(g_topo_mu);
+  if (!g_topo_known[dev]) {
+    Topology t;
+    int cus = 0, xcds = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+      t.cus = cus;
+    if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess && xcds > 0 &&
+        t.cus % xcds == 0)
+      t.xcds = xcds;
+    else
+      t.xcds = t.cus % 8 == 0 ? 8 : 1;
+    (void)hipGetLastError();
+    g_topo[dev] = t;
+    g_topo_known[dev] = true;
+  }
+  return g_topo[dev];
+}
 
 // How a call's T tokens are split over kernels.  T <= 64: the split-K decode
 // kernel alone.  Otherwise a tile kernel; when the rows of its last, partial
@@ -112,10 +145,12 @@ struct Plan {
   int passes = 1;                  // 64-row blocks per decode launch
 };
 
-Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, bool allow_blocks = true) {
+Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const Topology& topo,
+                bool allow_blocks = true) {
   Plan pl;
+  const int64_t cus = topo.cus;
   if (use_decode(M) && aligned) {
-    pl.splits = decode_splits_for(M, K, n_tiles, int(g_decode_splits.load()));
+    pl.splits = decode_splits_for(M, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds);
     if (pl.splits > 0) {
       pl.tail = M;
       return pl;
@@ -140,7 +175,7 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, bool 
   const double tile_us = double(K) / 64.0 * (int4 ? 2.1 : 1.15) + 5.0;
   if (allow_blocks && aligned && M > 64 && g_prefill_tile.load() == 0 && g_decode_max_t.load() >= 64 &&
       nblk <= g_decode_blocks.load() && blocks_us <= tile_us) {
-    pl.splits = decode_splits_for(64, K, n_tiles, int(g_decode_splits.load()));
+    pl.splits = decode_splits_for(64, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds);
     if (pl.splits > 0) {
       pl.tail = M;
       pl.passes = int(std::min<int64_t>(per_launch, nblk));
@@ -152,10 +187,10 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, bool 
   const int64_t r = M % pl.v->bm;
   if (r == 0 || r > 64 || !use_decode(r)) return pl;
   const int64_t ct = n_tiles / pl.v->hpt;
-  const int64_t rounds_all = ((M + pl.v->bm - 1) / pl.v->bm * ct + kCus - 1) / kCus;
-  const int64_t rounds_main = ((M - r) / pl.v->bm * ct + kCus - 1) / kCus;
+  const int64_t rounds_all = ((M + pl.v->bm - 1) / pl.v->bm * ct + cus - 1) / cus;
+  const int64_t rounds_main = ((M - r) / pl.v->bm * ct + cus - 1) / cus;
   if (rounds_main >= rounds_all) return pl;
-  const int splits = decode_splits_for(r, K, n_tiles, int(g_decode_splits.load()));
+  const int splits = decode_splits_for(r, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds);
   if (splits > 0) {
     pl.tail = r;
     pl.splits = splits;
@@ -169,7 +204,10 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, bool 
 int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& e, float in_eps,
               void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (p.M == 0) return ok();
-  Plan pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e));
+  const Topology topo = device_topology();
+  p.cus = topo.cus;
+  p.xcds = topo.xcds;
+  Plan pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo);
   if (!pl.v && pl.splits == 0)
     return fail(MQK_ERR_BAD_OPTION, "prefill_tile variant %lld cannot run this problem (%d heads%s)",
                 (long long)g_prefill_tile.load(), p.n_tiles, int4 ? ", int4 weights" : "");
@@ -187,7 +225,7 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
   }
   if (!pl.v && p.M > 64 && !fits(base)) {
     // decode blocks planned, but a workspace sized without them: the tile kernel
-    pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), false);
+    pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, false);
     base = pl.splits > 0 ? decode_workspace_bytes(p.n_tiles, pl.splits) : decode_counter_bytes();
   }
   if (pl.v && pl.splits > 0 && !fits(base)) {
@@ -266,7 +304,7 @@ size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hid
   const int tiles = Hq + 2 * Hkv;
   size_t n = 0;
   for (int int4 = 0; int4 < 2; ++int4) {  // the same size serves both weight formats
-    const Plan pl = plan_fused(int4, T, hidden, tiles, true);
+    const Plan pl = plan_fused(int4, T, hidden, tiles, true, device_topology());
     if (pl.splits > 0) n = std::max(n, decode_workspace_bytes(tiles, pl.splits, pl.passes));
   }
   return n;
@@ -392,8 +430,8 @@ int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
 
 // ---- allocation-free variant of mqk_fused_qkv_rope_bf16 ---------------------------------
 // The decode kernel's scratch (its arrival counters, then its fp32 split partials)
-// lives in this file-scope device array instead of a caller workspace: 4 KiB of
-// counters plus 8 MiB of partials, enough for one 64-row block of any head count
+// lives in this file-scope device array instead of a caller workspace: 4.25 KiB
+// of counters plus 8 MiB of partials, enough for one 64-row block of any head count
 // up to one split per CU (e.g. 48 heads x 5 splits at hidden 4096: 7.5 MiB).
 // Each GPU holds its own copy for the life of the process.  Host code never
 // passes `scratch` itself to a kernel (in host code the name is a stand-in, not a
@@ -401,7 +439,7 @@ int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
 // device, and only that address is used.
 }  // extern "C"
 
-static __device__ __align__(256) unsigned char scratch[4096 + (size_t(8) << 20)];
+static __device__ __align__(256) unsigned char scratch[mqk::kDecodeCounterBytes + (size_t(8) << 20)];
 
 namespace {
 
@@ -540,6 +578,9 @@ int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales
   if (!aligned16(x)) return fail(MQK_ERR_MISALIGNED, "x must be 16-byte aligned");
   const int tiles = int((N + kHeadDim - 1) / kHeadDim);
   ProblemArgs p{x, M, K, tiles};
+  const Topology topo = device_topology();
+  p.cus = topo.cus;
+  p.xcds = topo.xcds;
   WeightArgs w{};
   w.qw[0] = qweight;
   w.sc[0] = scales;
@@ -697,6 +738,8 @@ int64_t mqk_get_option(const char* name) {
   if (!strcmp(name, "decode_blocks")) return g_decode_blocks.load();
   if (!strcmp(name, "decode_passes")) return g_decode_passes.load();
   if (!strcmp(name, "decode_force_recompute")) return g_decode_force_recompute;
+  if (!strcmp(name, "device_cus")) return device_topology().cus;    // read-only: the current device's
+  if (!strcmp(name, "device_xcds")) return device_topology().xcds;  // topology as the planner uses it
   return -1;
 }
 

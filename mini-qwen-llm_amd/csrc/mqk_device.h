@@ -178,11 +178,11 @@ __device__ __forceinline__ void split_head(int h, int Hq, int Hkv, int& proj, in
 }
 
 // Maps a linear workgroup id onto a tile id so that consecutive tile ids land on
-// the same XCD (workgroups are dispatched round-robin over the 8 XCDs, and
-// each XCD has its own L2).
-__device__ __forceinline__ int xcd_tile_id(int bid, int nblocks) {
-  if ((nblocks & 7) != 0) return bid;
-  return (bid & 7) * (nblocks >> 3) + (bid >> 3);
+// the same XCD (workgroups are dispatched round-robin over the device's XCDs,
+// and each XCD has its own L2).
+__device__ __forceinline__ int xcd_tile_id(int bid, int nblocks, int xcds) {
+  if (xcds <= 1 || nblocks % xcds != 0) return bid;
+  return (bid % xcds) * (nblocks / xcds) + bid / xcds;
 }
 
 // ---------------------------------------------------------------------------

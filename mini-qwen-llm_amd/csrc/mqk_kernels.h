@@ -70,6 +70,11 @@ struct ProblemArgs {
   // bf16(in_gamma[k] * bf16(x[m, k] * in_scale[m])) instead of x (input_norm8).
   const uint16_t* in_gamma;  // [K] bf16
   const float* in_scale;     // [M] rsqrt(mean(x^2) + eps), from launch_row_scale
+  // Topology of the device the launch runs on (hipDeviceGetAttribute): compute
+  // units, and XCDs, each with its own L2; workgroup b is dispatched to XCD
+  // b % xcds.
+  int cus;
+  int xcds;
 };
 
 // One tile-kernel variant: BM rows x (HPT*128) columns per workgroup, with KZ
@@ -105,9 +110,15 @@ int tile_dma_lds_bytes(int id);
 hipError_t launch_row_scale(const uint16_t* x, int64_t M, int64_t K, float eps, float* scale,
                             hipStream_t stream);
 
-int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested);
+int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested, int cus, int xcds);
 size_t decode_workspace_bytes(int n_tiles, int splits, int passes = 1);
-size_t decode_counter_bytes();  // the arrival counters at the start of every workspace
+// The decode kernel's counters open every workspace: one arrival counter per
+// head (kDecodeMaxHeads), then a statistics line whose first word counts the
+// heads finished on the recompute path (a split ran on an unexpected XCD).
+constexpr int kDecodeMaxHeads = 1024;
+constexpr size_t kDecodeCounterBytes = size_t(kDecodeMaxHeads) * 4 + 256;
+constexpr int kDecodeRecomputeWord = kDecodeMaxHeads;
+size_t decode_counter_bytes();
 // The split-K decode kernel on the launch's p.M <= 256 rows: ceil(M / 64) blocks of
 // 64 rows share one stream of the weights; the workspace holds
 // decode_workspace_bytes(n_tiles, splits, blocks).

@@ -50,11 +50,10 @@ constexpr int kDecWaves = kDecThreads / 64;
 constexpr int kDecMaxNK = 16;           // largest k-range of one split, in 64-wide tiles
 constexpr int kDecLookahead = 6;        // weight tiles in flight per wave
 constexpr int kDecKc = kDecMaxNK * kBK;     // LDS row length of the x slice (bf16), 2 KB
-constexpr int kMaxHeads = 1024;
-constexpr int kCounterBytes = kMaxHeads * 4;
+constexpr int kMaxHeads = kDecodeMaxHeads;
+constexpr int kCounterBytes = int(kDecodeCounterBytes);
 constexpr int kTileFloats = kDecRows * kHeadDim;
 constexpr int kPitch = kHeadDim + 4;    // fp32 pitch of the finisher's LDS head tile
-constexpr int kXcds = 8;                // MI355X: 8 XCDs, workgroup b dispatched to XCD b % 8
 constexpr uint32_t kForeignUnit = 1u << 16;  // arrival-counter increment of a misplaced split
 
 static_assert(kDecRows * kDecKc * 2 > 160 * 1024 / 2, "x slice must keep one workgroup per CU");
@@ -380,9 +379,10 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   const int wave = tid >> 6;
   const int n_tiles = p.n_tiles;
   const int bid = blockIdx.x;
-  const int q = bid / kXcds;
+  const int xcds = p.xcds;
+  const int q = bid / xcds;
   const int split = q % splits;
-  const int head = (q / splits) * kXcds + bid % kXcds;
+  const int head = (q / splits) * xcds + bid % xcds;
   if (head >= n_tiles) return;  // padding workgroup
   const int M = int(p.M);
   const int nkt = int(p.K / kBK);
@@ -415,7 +415,8 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have reached the L2
   __syncthreads();                // ... and every thread's
   if (tid == 0) {
-    const bool foreign = force_recompute || xcc_id() != bid % kXcds;
+    // (XCC_ID is the physical XCD; a partition of the GPU holds xcds of them)
+    const bool foreign = force_recompute || xcc_id() % xcds != bid % xcds;
     const uint32_t inc = 1u + (foreign ? kForeignUnit : 0u);
     arrival = __hip_atomic_fetch_add(counters + head, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
   }
@@ -423,6 +424,8 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   const uint32_t seen = arrival;
   if ((seen & (kForeignUnit - 1)) != uint32_t(splits)) return;  // not the last split to arrive
   const bool recompute = (seen >> 16) != 0;
+  if (recompute && tid == 0)  // statistics: heads finished on the recompute path
+    __hip_atomic_fetch_add(counters + kDecodeRecomputeWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // thread -> row r = tid / 8, c = tid % 8 of the head tile: columns [8c, 8c+8)
   // and [64+8c, 64+8c+8), so every RoPE pair (d, d+64) is thread-local.  Its
@@ -577,26 +580,11 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   if (tid == 0) __hip_atomic_store(counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-int g_cus_per_xcd = 0;  // queried once (single-device processes)
-
-int cus_per_xcd() {
-  if (g_cus_per_xcd <= 0) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus >= kXcds)
-      g_cus_per_xcd = cus / kXcds;
-    else
-      g_cus_per_xcd = 32;  // MI355X: 256 CUs / 8 XCDs
-    (void)hipGetLastError();
-  }
-  return g_cus_per_xcd;
-}
-
 }  // namespace
 
 int g_decode_force_recompute = 0;
 
-int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested) {
+int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested, int cus, int xcds) {
   (void)M;
   const int nkt = int(K / kBK);
   if (nkt < 1) return 0;
@@ -604,8 +592,9 @@ int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested) {
   int s = requested;
   if (s <= 0) {
     // one workgroup per CU: (heads per XCD) x splits <= CUs per XCD
-    const int heads_per_xcd = (n_tiles + kXcds - 1) / kXcds;
-    s = cus_per_xcd() / heads_per_xcd;
+    xcds = xcds < 1 ? 1 : xcds;
+    const int heads_per_xcd = (n_tiles + xcds - 1) / xcds;
+    s = (cus / xcds) / heads_per_xcd;
     if (s > nkt) s = nkt;  // small hidden: at most one k tile per split
     if (s < min_splits) s = min_splits;
   }
@@ -628,7 +617,8 @@ hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, co
     return hipErrorInvalidValue;
   uint32_t* counters = static_cast<uint32_t*>(workspace);
   float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-  const dim3 grid(((p.n_tiles + kXcds - 1) / kXcds) * kXcds * splits);
+  if (p.xcds < 1) return hipErrorInvalidValue;
+  const dim3 grid(((p.n_tiles + p.xcds - 1) / p.xcds) * p.xcds * splits);
   const int fr = g_decode_force_recompute;
   auto a16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; };
   if (!(a16(e.q_gamma) && a16(e.k_gamma) && a16(e.cos) && a16(e.sin))) return hipErrorInvalidValue;

@@ -163,7 +163,7 @@ tile_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   // ---- tile coordinates: XCD-contiguous ids, grouped along M -------------
   const int n_mt = int((p.M + BM - 1) / BM);
   const int n_ht = p.n_tiles / HPT;
-  const int tile = xcd_tile_id(blockIdx.x, gridDim.x);
+  const int tile = xcd_tile_id(blockIdx.x, gridDim.x, p.xcds);
   const int per_group = group_m * n_ht;
   const int grp = tile / per_group;
   const int first_m = grp * group_m;

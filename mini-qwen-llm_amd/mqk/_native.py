@@ -239,6 +239,26 @@ def workspace(device: torch.device, stream, nbytes: int):
         return buf
 
 
+# Word of the workspace's statistics line that counts the heads the decode kernel
+# finished on its recompute path (include/mqk.h: after the 1024 arrival counters).
+_RECOMPUTE_WORD = 1024
+
+
+def decode_recomputes(device=None, stream=None) -> int:
+    """Heads the decode kernel has finished on its recompute path (some split of
+    the head ran on another XCD than the grid assumes, e.g. on a partitioned
+    GPU) in the workspace of ``stream`` (default: the current stream) since it
+    was allocated; 0 before its first use.  Synchronises with that stream."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    stream = torch.cuda.current_stream(device) if stream is None else stream
+    with _ws_lock:
+        buf = _workspaces.get((device.index, int(stream.cuda_stream)))
+    if buf is None:
+        return 0
+    stream.synchronize()
+    return int(buf[: 4 * (_RECOMPUTE_WORD + 1)].view(torch.int32)[_RECOMPUTE_WORD].item())
+
+
 def retired_workspaces() -> int:
     """Number of superseded workspaces kept alive for graphs captured earlier."""
     return len(_retired)

@@ -154,3 +154,31 @@ def test_decode_blocks_input_norm_four_blocks(device):
         torch.cuda.synchronize()
         for a, b in zip(out, alone):
             assert torch.equal(a[:, t0:t0 + 64], b), f"input-norm block at {t0} differs"
+
+
+def test_topology_and_recompute_statistic(device):
+    """The planner's topology comes from the device (all CUs; 8 XCDs on an
+    unpartitioned MI355X), and every head finished on the recompute path is
+    counted in the workspace's statistics word."""
+    import mqk
+    assert mqk.get_option("device_cus") == torch.cuda.get_device_properties(device).multi_processor_count
+    xcds = mqk.get_option("device_xcds")
+    assert xcds >= 1 and mqk.get_option("device_cus") % xcds == 0
+    print(f"  device: {mqk.get_option('device_cus')} CUs in {xcds} XCDs")
+    case = Case(16, 1, 1024, 16, 8, seed=4711, rows=4096,
+                positions=torch.arange(16, dtype=torch.int32) * 3)
+    args = case.args(device)
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        want = mqk.fused_qkv_rope(*args)
+        natural = mqk.decode_recomputes(device, stream)
+        print(f"  heads finished on the recompute path without forcing: {natural}")
+        mqk.set_option("decode_force_recompute", 1)
+        try:
+            got = [mqk.fused_qkv_rope(*args) for _ in range(3)]
+        finally:
+            mqk.set_option("decode_force_recompute", 0)
+        after = mqk.decode_recomputes(device, stream)
+    assert after - natural == 3 * (16 + 2 * 8)
+    for g in got:
+        assert all(torch.equal(a, b) for a, b in zip(g, want))

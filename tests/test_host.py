@@ -120,11 +120,12 @@ def test_workspace_size(lib):
     assert lib.mqk_fused_qkv_rope_workspace_size(2048, 32, 8, 4096) == 0     # tile kernel only
     assert lib.mqk_fused_qkv_rope_workspace_size(0, 32, 8, 4096) == 0
     n = lib.mqk_fused_qkv_rope_workspace_size(64, 32, 8, 4096)
-    assert n >= 4096 + 48 * 64 * 128 * 4  # counters + at least one fp32 partial per head
+    C = 4096 + 256  # 1024 arrival counters + the statistics line
+    assert n >= C + 48 * 64 * 128 * 4  # counters + at least one fp32 partial per head
     from mqk import _native
     # 64 < T: decode launches of up to four 64-row blocks; each block of a launch
     # has its own partials, so four blocks need four times the partial region
-    assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == 4096 + 4 * (n - 4096)
+    assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == C + 4 * (n - C)
     _native.set_option("decode_passes", 1)
     try:  # one block per launch: the launches share one block's region
         assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == n
@@ -144,7 +145,8 @@ def test_decode_block_crossovers(lib):
     launches 76 / 113 us against 136 us for its tile kernel), and neither at T = 1024
     (tile kernels 83 / 137 us against 155 us for four int4 launches)."""
     size = lambda T: lib.mqk_fused_qkv_rope_workspace_size(T, 32, 8, 4096)
-    n4 = 4096 + 4 * (size(64) - 4096)  # counters + four blocks of partials
+    C = 4096 + 256  # per-head arrival counters + the statistics line
+    n4 = C + 4 * (size(64) - C)  # counters + four blocks of partials
     assert size(512) == n4
     assert size(768) == n4   # the int4 plan
     assert size(1024) == 0
