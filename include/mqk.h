@@ -283,8 +283,14 @@ int mqk_fused_qkv_rope_ex_w4a16(const mqk_bf16* x, const int32_t* qw_q, const vo
  *                    with 64 < T tokens may run as (instead of a tile launch whose few tiles
  *                    leave most CUs idle), used where a cost model of both paths says the
  *                    launches are faster; 0: never
- *   "decode_passes"  4 (default): most 64-row blocks one decode launch covers, streaming
- *                    the weights once for all of them (1..4; the workspace size grows with it)
+ *   "decode_passes"  16 (default): most 64-row blocks one decode launch covers, streaming
+ *                    the weights once for all of them (1..16; the workspace size grows with it)
+ *   "decode_cost_model"  1 (default): decode blocks run where the cost model prefers them
+ *                    to a tile launch; 0: whenever decode_blocks allows (for measurements)
+ *   "decode_max_spins"  polls (~64 ns apart) a decode launch of several blocks makes while
+ *                    a block's designated finisher waits for its last splits, before it
+ *                    hands the block to the last split to arrive (default 16384, ~1 ms;
+ *                    0 hands off at once; for tests of the hand-off)
  *   "decode_force_recompute"  1: the decode kernel takes its recompute path (used when a
  *                    split ran on an unexpected XCD) for every head; for tests
  * Returns MQK_OK or MQK_ERR_BAD_OPTION.  mqk_get_option also reads "device_cus" and

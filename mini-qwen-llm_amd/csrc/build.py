@@ -14,6 +14,7 @@ from __future__ import annotations
 import argparse
 import concurrent.futures as cf
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -24,6 +25,9 @@ PKG = CSRC.parent / "mqk"
 OUT = PKG / "libmqk.so"
 BUILD_DIR = CSRC.parent / "_build"
 SOURCES = ["qkv_tile.hip", "qkv_tile_dma.hip", "qkv_decode.hip", "norm_rope.hip", "input_norm.hip", "mqk_api.hip"]
+# Sources whose kernels must not use scratch memory (register spills): the
+# compiler's resource-usage remarks are checked and the build fails otherwise.
+NO_SCRATCH = {"qkv_decode.hip"}
 ARCH = "gfx950"
 
 COMMON_FLAGS = [
@@ -49,15 +53,35 @@ def _filter(text: str) -> str:
     return "\n".join(keep)
 
 
+def _scratch_kernels(remarks: str) -> list[str]:
+    """Kernels with a non-zero ScratchSize in -Rpass-analysis=kernel-resource-usage output."""
+    bad, name = [], None
+    for ln in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", ln)
+        if m:
+            name = m.group(1)
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", ln)
+        if m and int(m.group(1)) > 0 and name:
+            bad.append(f"{name} ({m.group(1)} B/lane)")
+    return bad
+
+
 def _compile(src: str, verbose: bool) -> Path:
     obj = BUILD_DIR / (Path(src).stem + ".o")
-    cmd = [_hipcc(), *COMMON_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    check = src in NO_SCRATCH
+    cmd = [_hipcc(), *COMMON_FLAGS, *(["-Rpass-analysis=kernel-resource-usage"] if check else []),
+           "-c", str(CSRC / src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    msg = _filter(res.stdout + res.stderr).strip()
+    out = res.stdout + res.stderr
+    msg = _filter("\n".join(ln for ln in out.splitlines() if "remark:" not in ln)).strip()
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{msg}")
+    if check:
+        bad = _scratch_kernels(out)
+        if bad:
+            raise RuntimeError(f"{src}: kernels use scratch memory (register spills): " + "; ".join(bad))
     if msg and verbose:
         print(msg)
     return obj

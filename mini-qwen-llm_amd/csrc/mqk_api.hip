@@ -46,7 +46,8 @@ std::atomic<int64_t> g_decode_splits{0};
 std::atomic<int64_t> g_group_m{8};
 std::atomic<int64_t> g_tail_split{1};
 std::atomic<int64_t> g_decode_blocks{16};  // most 64-row decode blocks for one call (T > 64)
-std::atomic<int64_t> g_decode_passes{4};   // most 64-row blocks one decode launch covers (1..4)
+std::atomic<int64_t> g_decode_cost_model{1};  // 0: decode blocks whenever eligible (measurements)
+std::atomic<int64_t> g_decode_passes{16};  // most 64-row blocks one decode launch covers (1..16)
 
 constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace (per head)
 
@@ -146,7 +147,7 @@ struct Plan {
 };
 
 Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const Topology& topo,
-                bool allow_blocks = true) {
+                bool allow_blocks = true, bool in_norm = false) {
   Plan pl;
   const int64_t cus = topo.cus;
   if (use_decode(M) && aligned) {
@@ -156,26 +157,29 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
       return pl;
     }
   }
-  // A few 64-row blocks: decode launches, each streaming the weights over every
-  // CU once for up to four blocks, can beat a tile launch whose few tiles leave
-  // most CUs idle and stream their panels at a single CU's rate.  Measured at
-  // hidden 4096: a bf16 decode launch ~18 us against ~80 us for the best tile
-  // variant at T = 65..1024; int4 ~16 us per launch against ~136 us.  Each
-  // further block of a launch (x re-staged, its rows finished) adds ~7 us at
-  // hidden 4096 (bf16 T = 128 / 192 / 256 in one launch: 26.6 / 33 / 40.5 us).
-  // The models below follow those measurements (and hidden 2048: ~12 us per
-  // launch against ~42 us for the tile kernel).
+  // A few 64-row blocks: a decode launch streams the weights over every CU once
+  // for up to sixteen blocks (holding them in registers), which beats a tile
+  // launch whose few tiles leave most CUs idle and stream their panels at a
+  // single CU's rate.  Measured at hidden 4096 (kernel times): the first block
+  // of a launch ~19 us bf16 / ~17 us int4 (the weight stream), each further
+  // block ~5 us (its x slice staged, multiplied, published and finished by its
+  // designated split: T = 128 / 256 / 512 / 1024 take 25.6 / 39.3 / 56.9 / 93.5 us
+  // bf16), against ~83 us (bf16) and ~138 us (int4) for the best tile variant at
+  // T = 65..1024.  The models below follow those measurements; at hidden 4096 bf16
+  // runs as blocks up to T = 832, int4 up to T = 1024.
   const int64_t nblk = (M + 63) / 64;
-  const int64_t per_launch = std::max<int64_t>(1, std::min<int64_t>(g_decode_passes.load(), 4));
+  const int blk_splits = decode_splits_for(64, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds);
+  const int64_t per_launch = std::max<int64_t>(
+      1, std::min<int64_t>(g_decode_passes.load(), decode_max_blocks(n_tiles, K, blk_splits, int4 && in_norm)));
   const int64_t launches = (nblk + per_launch - 1) / per_launch;
   const double w_bytes = double(n_tiles) * kHeadDim * double(K) * (int4 ? 0.5 : 2.0);
   const double dec_us = int4 ? 4.0 + 3.0 * double(K) / 1024.0 : 8.0 + w_bytes / 5.0e6;
-  const double pass_us = 3.0 + double(K) / 4096.0 * 4.0;
+  const double pass_us = 0.5 + double(K) / 4096.0 * 4.5;
   const double blocks_us = double(launches) * dec_us + double(nblk - launches) * pass_us;
   const double tile_us = double(K) / 64.0 * (int4 ? 2.1 : 1.15) + 5.0;
   if (allow_blocks && aligned && M > 64 && g_prefill_tile.load() == 0 && g_decode_max_t.load() >= 64 &&
-      nblk <= g_decode_blocks.load() && blocks_us <= tile_us) {
-    pl.splits = decode_splits_for(64, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds);
+      nblk <= g_decode_blocks.load() && (blocks_us <= tile_us || !g_decode_cost_model.load())) {
+    pl.splits = blk_splits;
     if (pl.splits > 0) {
       pl.tail = M;
       pl.passes = int(std::min<int64_t>(per_launch, nblk));
@@ -207,25 +211,23 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
   const Topology topo = device_topology();
   p.cus = topo.cus;
   p.xcds = topo.xcds;
-  Plan pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo);
+  Plan pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, true, p.in_gamma != nullptr);
   if (!pl.v && pl.splits == 0)
     return fail(MQK_ERR_BAD_OPTION, "prefill_tile variant %lld cannot run this problem (%d heads%s)",
                 (long long)g_prefill_tile.load(), p.n_tiles, int4 ? ", int4 weights" : "");
   // (the decode kernel's arrival counters open every workspace and must stay zero,
   // so the scales never start before them, whichever kernel runs this call)
-  // (the four-block decode kernel with the input norm would spill registers)
-  if (p.in_gamma && pl.passes > 3) pl.passes = 3;
   size_t base = pl.splits > 0 ? decode_workspace_bytes(p.n_tiles, pl.splits, pl.passes) : decode_counter_bytes();
   // bytes the plan needs: the decode region, then (input norm) the per-token scales
   const size_t scale_bytes = p.in_gamma ? align_up(size_t(p.M) * sizeof(float), 256) : 0;
   auto fits = [&](size_t b) { return workspace && ws_bytes >= align_up(b, 256) + scale_bytes; };
-  if (!pl.v && pl.passes > 1 && !fits(base)) {
-    pl.passes = 1;  // a workspace sized for one block per launch
-    base = decode_workspace_bytes(p.n_tiles, pl.splits, 1);
+  while (!pl.v && pl.passes > 1 && !fits(base)) {
+    pl.passes = (pl.passes + 1) / 2;  // a workspace sized for fewer blocks per launch
+    base = decode_workspace_bytes(p.n_tiles, pl.splits, pl.passes);
   }
   if (!pl.v && p.M > 64 && !fits(base)) {
     // decode blocks planned, but a workspace sized without them: the tile kernel
-    pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, false);
+    pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, false, p.in_gamma != nullptr);
     base = pl.splits > 0 ? decode_workspace_bytes(p.n_tiles, pl.splits) : decode_counter_bytes();
   }
   if (pl.v && pl.splits > 0 && !fits(base)) {
@@ -707,6 +709,9 @@ int mqk_set_option(const char* name, int64_t value) {
   } else if (!strcmp(name, "decode_splits")) {
     if (value < 0 || value > 4096) return fail(MQK_ERR_BAD_OPTION, "decode_splits must be in [0, 4096]");
     g_decode_splits = value;
+  } else if (!strcmp(name, "decode_max_spins")) {
+    if (value < 0 || value > (1 << 24)) return fail(MQK_ERR_BAD_OPTION, "decode_max_spins must be in [0, 2^24]");
+    g_decode_max_spins = int(value);
   } else if (!strcmp(name, "decode_force_recompute")) {
     if (value != 0 && value != 1) return fail(MQK_ERR_BAD_OPTION, "decode_force_recompute must be 0 or 1");
     g_decode_force_recompute = int(value);
@@ -717,8 +722,11 @@ int mqk_set_option(const char* name, int64_t value) {
     if (value < 0 || value > 64) return fail(MQK_ERR_BAD_OPTION, "decode_blocks must be in [0, 64]");
     g_decode_blocks = value;
   } else if (!strcmp(name, "decode_passes")) {
-    if (value < 1 || value > 4) return fail(MQK_ERR_BAD_OPTION, "decode_passes must be in [1, 4]");
+    if (value < 1 || value > 16) return fail(MQK_ERR_BAD_OPTION, "decode_passes must be in [1, 16]");
     g_decode_passes = value;
+  } else if (!strcmp(name, "decode_cost_model")) {
+    if (value != 0 && value != 1) return fail(MQK_ERR_BAD_OPTION, "decode_cost_model must be 0 or 1");
+    g_decode_cost_model = value;
   } else if (!strcmp(name, "group_m")) {
     if (value < 1 || value > 1024) return fail(MQK_ERR_BAD_OPTION, "group_m must be in [1, 1024]");
     g_group_m = value;
@@ -737,7 +745,9 @@ int64_t mqk_get_option(const char* name) {
   if (!strcmp(name, "tail_split")) return g_tail_split.load();
   if (!strcmp(name, "decode_blocks")) return g_decode_blocks.load();
   if (!strcmp(name, "decode_passes")) return g_decode_passes.load();
+  if (!strcmp(name, "decode_cost_model")) return g_decode_cost_model.load();
   if (!strcmp(name, "decode_force_recompute")) return g_decode_force_recompute;
+  if (!strcmp(name, "decode_max_spins")) return g_decode_max_spins;
   if (!strcmp(name, "device_cus")) return device_topology().cus;    // read-only: the current device's
   if (!strcmp(name, "device_xcds")) return device_topology().xcds;  // topology as the planner uses it
   return -1;

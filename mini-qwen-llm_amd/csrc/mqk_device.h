@@ -169,6 +169,16 @@ __device__ __forceinline__ uint16_t* paged_row(const E& e, int64_t slot, int pro
   return cache + (slot * e.Hkv + hh) * kHeadDim;
 }
 
+// Element i (0, 1, 2) of three pointer values, selected arithmetically: a
+// select between kernel-argument fields makes the compiler copy the whole
+// argument struct to scratch memory to address the chosen field.
+template <class T>
+__device__ __forceinline__ T* pick3(int i, T* a, T* b, T* c) {
+  const uintptr_t ua = reinterpret_cast<uintptr_t>(a), ub = reinterpret_cast<uintptr_t>(b),
+                  uc = reinterpret_cast<uintptr_t>(c);
+  return reinterpret_cast<T*>(ua * uintptr_t(i == 0) + ub * uintptr_t(i == 1) + uc * uintptr_t(i == 2));
+}
+
 // Which projection a 128-column tile belongs to: 0 = Q, 1 = K, 2 = V, and the
 // tile's head index inside that projection.
 __device__ __forceinline__ void split_head(int h, int Hq, int Hkv, int& proj, int& hh) {
@@ -201,6 +211,25 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
       : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(gptr)
+      : "memory");
+}
+
+// dma16 of the 16 bytes at gptr + OFF bytes (OFF an immediate of the instruction,
+// 0 <= OFF < 4096), so a run of loads at fixed distances shares one address.  The
+// instruction offset moves the LDS destination as well (M0 + offset + 16 * lane),
+// so M0 is set to lds_base - OFF.
+template <int OFF>
+__device__ __forceinline__ void dma16_at(const void* gptr, uint32_t lds_base) {
+  static_assert(OFF >= 0 && OFF < 4096, "global instruction offset");
+  lds_base -= uint32_t(OFF);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off offset:%3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(gptr), "n"(OFF)
       : "memory");
 }
 

@@ -111,7 +111,11 @@ hipError_t launch_row_scale(const uint16_t* x, int64_t M, int64_t K, float eps, 
                             hipStream_t stream);
 
 int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested, int cus, int xcds);
-size_t decode_workspace_bytes(int n_tiles, int splits, int passes = 1);
+size_t decode_workspace_bytes(int n_tiles, int splits, int blocks = 1);
+// Most 64-row blocks one decode launch may cover with this many heads and splits
+// (one arrival counter per (head, block) in the workspace's counter region; one
+// block when a split's k range is too long to hold its weights in registers).
+int decode_max_blocks(int n_tiles, int64_t K, int splits, bool int4_norm);
 // The decode kernel's counters open every workspace: one arrival counter per
 // head (kDecodeMaxHeads), then a statistics line whose first word counts the
 // heads finished on the recompute path (a split ran on an unexpected XCD).
@@ -119,15 +123,20 @@ constexpr int kDecodeMaxHeads = 1024;
 constexpr size_t kDecodeCounterBytes = size_t(kDecodeMaxHeads) * 4 + 256;
 constexpr int kDecodeRecomputeWord = kDecodeMaxHeads;
 size_t decode_counter_bytes();
-// The split-K decode kernel on the launch's p.M <= 256 rows: ceil(M / 64) blocks of
-// 64 rows share one stream of the weights; the workspace holds
-// decode_workspace_bytes(n_tiles, splits, blocks).
+// The split-K decode kernel on the launch's p.M rows: ceil(M / 64) <=
+// decode_max_blocks(n_tiles) blocks of 64 rows share one stream of the weights;
+// the workspace holds decode_workspace_bytes(n_tiles, splits, blocks).  With
+// e.qkv == 0 it writes the plain product to e.out ([M, N], N = 128 * n_tiles).
 hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                          int splits, void* workspace, hipStream_t stream);
 
 // 1: the last workgroup of every head recomputes all splits itself (the path
 // taken when a split ran on an unexpected XCD); for tests.
 extern int g_decode_force_recompute;
+// Polls a designated finisher makes for the last splits of its block before it
+// hands the block to the last split to arrive (several-block launches); tests
+// set it low to exercise the hand-off.
+extern int g_decode_max_spins;
 
 // Standalone QK-norm + RoPE.
 hipError_t launch_norm_rope(const uint16_t* q_raw, const uint16_t* k_raw, const EpilogueArgs& e,

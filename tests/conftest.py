@@ -89,25 +89,22 @@ def device():
 
 
 # Short names of the library's kernels, by (demangled or mangled) kernel name.
-_KERNEL_NAMES = (("decode_kernel", "decode"), ("tile_dma_w4_kernel", "tile_w4"), ("tile_dma_kernel", "tile"),
-                 ("tile_kernel", "tile_reg"), ("row_scale_kernel", "row_scale"), ("norm_rope_kernel", "norm_rope"))
+_KERNEL_NAMES = (("decode_multi_kernel", "decode_multi"), ("decode_kernel", "decode"),
+                 ("tile_dma_w4_kernel", "tile_w4"), ("tile_dma_kernel", "tile"), ("tile_kernel", "tile_reg"),
+                 ("row_scale_kernel", "row_scale"), ("norm_rope_kernel", "norm_rope"))
 
 
 def _short_kernel_name(name: str):
-    import re
     for key, short in _KERNEL_NAMES:
         if key in name:
-            if short == "decode":  # blocks per launch = last template argument
-                m = re.search(r"decode_kernel<[^>]*?(\d+)>", name) or re.search(r"decode_kernelI.*?Li(\d+)E", name)
-                return f"decode<{m.group(1) if m else '?'}>"
             return short
     return None
 
 
 def launched_kernels(fn, *, warm=True):
     """The library kernels one call of ``fn`` launches, in launch order, as
-    short names ("decode<NP>", "tile", "tile_w4", "tile_reg", "row_scale",
-    "norm_rope"), recorded with torch.profiler (the reference counts its
+    short names ("decode" = one 64-row block, "decode_multi" = several blocks,
+    "tile", "tile_w4", "tile_reg", "row_scale", "norm_rope"), recorded with torch.profiler (the reference counts its
     kernels the same way, tests/test_fused_qkv_rope.py:287-311).  Other
     kernels (torch's own fills and copies) are left out."""
     from torch.profiler import ProfilerActivity, profile

@@ -1,13 +1,16 @@
 """GPU tests of the decode-block plan.
 
 A call of 64 < T tokens whose tile launch would leave most CUs idle (few row
-tiles, long K) runs instead as launches of the split-K decode kernel, each
-streaming the weights over every CU once for up to four 64-row blocks (option
-decode_passes); row 0 of a launch is the call's token 64 * (blocks before it),
-so positions, cache slots and varlen offsets keep the call's token index.  Each
-block must equal the decode kernel run on those 64 rows alone, bit for bit; the
-whole call must match the oracle and, within the acceptance bar, the tile path
-(option decode_blocks = 0).
+tiles, long K) runs instead as a launch of the split-K decode kernel that
+streams the weights over every CU once for all its 64-row blocks (up to
+sixteen; option decode_passes caps the blocks per launch, and row 0 of a
+further launch is the call's token 64 * (blocks before it), so positions,
+cache slots and varlen offsets keep the call's token index).  Block b is
+finished by its designated split b % splits, or, when that split's bounded
+wait runs out, by the last split to arrive.  Each block must equal the decode
+kernel run on those 64 rows alone, bit for bit, whatever the blocks per launch
+and whoever finishes it; the whole call must match the oracle and, within the
+acceptance bar, the tile path (option decode_blocks = 0).
 """
 from __future__ import annotations
 
@@ -47,20 +50,25 @@ def _close(a, b, label):
         assert float(excess.max()) <= 0 and rl <= REL_L2, f"{label} {name}: {ma} {rl}"
 
 
-@pytest.mark.parametrize("T", [65, 128, 200, 256, 300, 448])  # 300, 448: two launches
+@pytest.mark.parametrize("T", [65, 128, 200, 256, 300, 448, 832, 1024])
 def test_decode_blocks_bf16(T, device):
     import mqk
     pos = torch.randint(0, 8192, (T,), generator=torch.Generator().manual_seed(T), dtype=torch.int32)
     case = Case(1, T, 4096, 32, 8, seed=1100 + T, rows=8192, positions=pos)
     x, wq, wk, wv, gq, gk, cos, sin, p = case.args(device)
-    out = mqk.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin, p)
-    torch.cuda.synchronize()
+    call = lambda: mqk.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin, p)
+    # decode blocks whatever the cost model prefers (1024 tokens at hidden 4096
+    # run as a tile launch by default)
+    out = _with_option("decode_cost_model", 0, call)
     for t0 in range(0, T, 64):
         alone = mqk.fused_qkv_rope(x[:, t0:t0 + 64].contiguous(), wq, wk, wv, gq, gk, cos, sin, p[t0:t0 + 64])
         torch.cuda.synchronize()
         for a, b in zip(out, alone):
             assert torch.equal(a[:, t0:t0 + 64], b), f"T={T}: block at {t0} differs from the decode kernel alone"
-    tile = _with_option("decode_blocks", 0, lambda: mqk.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin, p))
+    for passes in (3, 1):  # several launches sharing the workspace in stream order
+        more = _with_option("decode_passes", passes, lambda: _with_option("decode_cost_model", 0, call))
+        assert all(torch.equal(a, b) for a, b in zip(out, more)), f"T={T}: {passes} blocks per launch"
+    tile = _with_option("decode_blocks", 0, call)
     _close(out, tile, f"T={T} blocks vs tile")
     idx = np.unique(np.concatenate([np.arange(0, 4), np.arange(60, 70), np.arange(T - 4, T)]).clip(0, T - 1))
     ref = case.oracle(token_idx=idx)
@@ -135,6 +143,26 @@ def test_decode_blocks_recompute_path(device):
     again = _with_option("decode_force_recompute", 1, lambda: mqk.fused_qkv_rope(*args))
     for a, b in zip(out, again):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("spins", [0, 1, 64])
+def test_decode_blocks_finisher_hand_off(spins, device):
+    """A designated finisher whose (host-shortened) wait runs out marks its block
+    abandoned and the block's last split to arrive finishes it instead: every
+    block is finished exactly once, bit-identical to the default."""
+    import mqk
+    T = 512
+    pos = torch.randint(0, 8192, (T,), generator=torch.Generator().manual_seed(12), dtype=torch.int32)
+    case = Case(1, T, 4096, 32, 8, seed=1450, rows=8192, positions=pos)
+    args = case.args(device)
+    want = mqk.fused_qkv_rope(*args)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        got = _with_option("decode_max_spins", spins, lambda: mqk.fused_qkv_rope(*args))
+        assert all(torch.equal(a, b) for a, b in zip(got, want)), f"spins={spins} rep={rep}"
+    again = mqk.fused_qkv_rope(*args)  # the counters were left at zero
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(again, want))
 
 
 def test_decode_blocks_input_norm_four_blocks(device):

@@ -96,8 +96,8 @@ def _replay_checks(graph, outs, want, rerun):
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("T,plan", [(32, ["decode<1>"]), (200, ["decode<4>"]),
-                                    (4128, ["tile_w4", "decode<1>"])])
+@pytest.mark.parametrize("T,plan", [(32, ["decode"]), (200, ["decode_multi"]),
+                                    (4128, ["tile_w4", "decode"])])
 def test_graph_replay_w4a16(T, plan, device):
     """The W4A16 front under capture, one case per launch plan: the decode kernel
     (T = 32), one four-block decode launch (T = 200), and the tile launch plus

@@ -123,14 +123,14 @@ def test_workspace_size(lib):
     C = 4096 + 256  # 1024 arrival counters + the statistics line
     assert n >= C + 48 * 64 * 128 * 4  # counters + at least one fp32 partial per head
     from mqk import _native
-    # 64 < T: decode launches of up to four 64-row blocks; each block of a launch
-    # has its own partials, so four blocks need four times the partial region
+    # 64 < T: one decode launch covers every 64-row block; each block has its own
+    # partials, so four blocks need four times the partial region
     assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == C + 4 * (n - C)
     _native.set_option("decode_passes", 1)
     try:  # one block per launch: the launches share one block's region
         assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == n
     finally:
-        _native.set_option("decode_passes", 4)
+        _native.set_option("decode_passes", 16)
     _native.set_option("decode_blocks", 0)
     try:
         assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == 0
@@ -140,16 +140,23 @@ def test_workspace_size(lib):
 
 def test_decode_block_crossovers(lib):
     """The plan's cost model reproduces the crossovers measured on MI355X at hidden
-    4096 (Qwen3-8B heads).  A workspace is needed exactly when decode launches run:
-    bf16 and int4 use decode blocks up to T = 512, int4 alone up to T = 768 (four-block
-    launches 76 / 113 us against 136 us for its tile kernel), and neither at T = 1024
-    (tile kernels 83 / 137 us against 155 us for four int4 launches)."""
+    4096 (Qwen3-8B heads): a workspace is needed exactly when decode launches run.
+    bf16 runs as decode blocks up to T = 832 (768 tokens: 73 us against 85 us for
+    the tile kernel; 896: 86 against 84), int4 up to T = 1024 (92 us against 138),
+    and beyond sixteen blocks (T > 1024) both run the tile kernel.  One launch
+    covers every block, each with its own partials."""
+    from mqk import _native
     size = lambda T: lib.mqk_fused_qkv_rope_workspace_size(T, 32, 8, 4096)
     C = 4096 + 256  # per-head arrival counters + the statistics line
-    n4 = C + 4 * (size(64) - C)  # counters + four blocks of partials
-    assert size(512) == n4
-    assert size(768) == n4   # the int4 plan
-    assert size(1024) == 0
+    one = size(64) - C  # partials of one 64-row block
+    for T in (128, 512, 768, 896, 1024):
+        assert size(T) == C + (T // 64) * one, T
+    assert size(1088) == 0
+    _native.set_option("decode_passes", 4)
+    try:  # at most four blocks per launch: the launches reuse four blocks' partials
+        assert size(1024) == C + 4 * one
+    finally:
+        _native.set_option("decode_passes", 16)
 
 
 def test_w4a16_validation(lib):
