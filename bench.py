@@ -158,6 +158,30 @@ def bench_w4a16(hidden, Hq, Hkv, seed, steps, warmup, dev, copies=6):
     return ms, T
 
 
+def bench_w4a16_gemm_decode(steps, warmup, dev, K=1024, N=4096, copies=160):
+    """The reference's published W4A16 GEMM decode shapes (docs/03_w4a16_awq.md:107-116):
+    x [M, 1024] @ int4 W [1024, 4096], M in {1, 4, 8, 16}, group 128.  Steps rotate
+    over `copies` weight sets (2.1 MB each, 336 MB in all, more than the Infinity
+    Cache).  Returns {M: (us per call, GB/s of algorithmic bytes)}."""
+    import torch
+    import mqk
+    g = torch.Generator(device=dev).manual_seed(77)
+    sets = []
+    for _ in range(copies):
+        qw = torch.randint(-2**31, 2**31 - 1, (K // 8, N), generator=g, device=dev, dtype=torch.int64).to(torch.int32)
+        sc = (0.005 + 0.015 * torch.rand(K // 128, N, generator=g, device=dev)).half()
+        qz = torch.randint(-2**31, 2**31 - 1, (K // 128, N // 8), generator=g, device=dev,
+                           dtype=torch.int64).to(torch.int32)
+        sets.append((qw, sc, qz))
+    res = {}
+    for M in (1, 4, 8, 16):
+        x = torch.randn(M, K, generator=g, device=dev).bfloat16()
+        ms, _ = time_steps(lambda i: mqk.w4a16_gemm(x, *sets[i % copies], 128), steps, warmup)
+        nbytes = K * N // 2 + (K // 128) * N * 2 + (K // 128) * N // 2 + M * K * 2 + M * N * 2
+        res[M] = (ms * 1e3, nbytes / (ms * 1e-3) / 1e9)
+    return res
+
+
 def cpu_baseline(budget_s=12.0):
     """The reference's unfused composition on the host in fp32, with PyTorch.
 
@@ -260,7 +284,7 @@ def copy_kernel(nbytes, steps, dev):
     torch.cuda.synchronize()
 
 
-WORKLOADS = ("c2", "c3", "c4", "c5", "mid", "copy")
+WORKLOADS = ("c2", "c3", "c4", "c5", "mid", "gemm", "copy")
 
 
 def run_only(name, steps, warmup, dev):
@@ -274,8 +298,10 @@ def run_only(name, steps, warmup, dev):
         ms, _ = bench_prefill(8192, 1, 8192, 2048, 32, 4, 3, steps, warmup, dev)
     elif name == "c5":
         ms, _ = bench_w4a16(hidden, Hq, Hkv, 4, steps, warmup, dev)
-    elif name == "mid":  # a 256-token decode step: one decode launch covering four 64-row blocks
-        ms, _ = bench_decode(256, hidden, Hq, Hkv, 2, steps, warmup, dev)
+    elif name == "mid":  # a 512-token call: one decode launch covering eight 64-row blocks
+        ms, _ = bench_decode(512, hidden, Hq, Hkv, 2, steps, warmup, dev)
+    elif name == "gemm":  # the W4A16 GEMM decode shapes, M = 1 / 4 / 8 / 16
+        ms = {m: v[0] * 1e-3 for m, v in bench_w4a16_gemm_decode(steps, warmup, dev).items()}
     else:
         copy_kernel(256 << 20, steps, dev)
         ms = float("nan")
@@ -369,6 +395,15 @@ def main(argv=None) -> int:
                                        "ms_per_step": round(ms5, 6), "bound": "mfma", "achieved_TFLOPs": round(a5, 2),
                                        "frac": round(a5 / PEAK_BF16_TFLOPS, 4)}
         log(f"[bench] config 5 W4A16 T={T5}: {ms5 * 1e3:.1f} us/step, {a5:.0f} TFLOP/s")
+        # the reference's W4A16 GEMM decode line (RTX 4090: 51-58 us per call)
+        wg = bench_w4a16_gemm_decode(max(100, args.steps), 100, dev)
+        sec["w4a16_gemm_decode_k1024_n4096"] = {
+            "us_per_call": {str(m): round(v[0], 2) for m, v in wg.items()},
+            "achieved_GBps": {str(m): round(v[1], 1) for m, v in wg.items()},
+            "reference_us_per_call_rtx4090": {"1": 51, "4": 58, "8": 57, "16": 58},
+            "note": "events over back-to-back calls of mqk.w4a16_gemm from Python (host launch cost "
+                    "included when it exceeds the kernel time); reference: docs/03_w4a16_awq.md:107-116"}
+        log("[bench] w4a16 GEMM K=1024 N=4096: " + ", ".join(f"M={m}: {v[0]:.1f} us" for m, v in wg.items()))
         # config 1: the Qwen3-0.6B-shaped layer, B=1 x S=128 (the reference runs it on
         # the CPU in fp32; here on the GPU in bf16, and the oracle's fp32 composition on the host)
         ms1, _ = bench_prefill(128, 1, 128, 1024, 16, 8, 0, 200, 200, dev)

@@ -17,7 +17,7 @@
  * Reference interface each entry point replaces (mini-qwen-llm):
  *   mqk_fused_qkv_rope_bf16   <- fused_qkv_rope()      mini_qwen/kernels/fused_qkv_rope.py:130-195
  *   mqk_qk_norm_rope_bf16     <- _qk_norm_rope_kernel  mini_qwen/kernels/fused_qkv_rope.py:46-127
- *   mqk_w4a16_gemm            <- w4a16_gemm()          mini_qwen/kernels/w4a16_gemm.py:194-247
+ *   mqk_w4a16_gemm(_ex)       <- w4a16_gemm()          mini_qwen/kernels/w4a16_gemm.py:194-247
  *   mqk_fused_qkv_rope_w4a16  <- the W4A16 attention front (3x LinearW4A16 + RMSNorm + RoPE),
  *                                mini_qwen/model/layers/attention.py:102-109 (prefill), :136-148 (decode)
  *   mqk_fused_qkv_rope_paged_* <- the above + the paged KV-cache scatter, write_kv_decode /
@@ -142,6 +142,23 @@ int mqk_qk_norm_rope_bf16(const mqk_bf16* q_raw, const mqk_bf16* k_raw, const mq
 int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales,
                    const int32_t* qzeros, int64_t M, int64_t K, int64_t N, int group,
                    int scale_type, mqk_bf16* out, void* stream);
+
+/* Workspace bytes mqk_w4a16_gemm_ex needs for these sizes (0: none). */
+size_t mqk_w4a16_gemm_workspace_size(int64_t M, int64_t K, int64_t N);
+
+/*
+ * mqk_w4a16_gemm with the kernel choice of the fused op: small and mid M (the
+ * decode regime of w4a16_gemm.py:110-189, the reference's M = 1 GEMV, and its
+ * published decode shapes M in {1, 4, 8, 16}, K = 1024, N = 4096) run on the
+ * split-K decode kernel, which streams the packed weights over every CU once for
+ * up to sixteen 64-row blocks; larger M on the tile kernels.  The workspace is
+ * as for mqk_fused_qkv_rope_bf16 (zero-filled once at allocation, not shared by
+ * calls that may overlap).  N not a multiple of 128 or operands not 16-byte
+ * aligned: the tile kernels of mqk_w4a16_gemm, no workspace needed.
+ */
+int mqk_w4a16_gemm_ex(const mqk_bf16* x, const int32_t* qweight, const void* scales, const int32_t* qzeros,
+                      int64_t M, int64_t K, int64_t N, int group, int scale_type, mqk_bf16* out,
+                      void* workspace, size_t ws_bytes, void* stream);
 
 /*
  * Fused W4A16 front: three int4 projections (q, k, v; each in the

@@ -273,6 +273,7 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
     et.q = shift(e.q, e.Hq);
     et.k = shift(e.k, e.Hkv);
     et.v = shift(e.v, e.Hkv);
+    if (e.out) et.out = e.out + t0 * e.N;  // plain GEMM output [M, N]
     const int st = hip_status(launch_decode(int4, pt, w, et, pl.splits, workspace, stream), "decode kernel launch");
     if (st != MQK_OK) return st;
   }
@@ -604,6 +605,46 @@ int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales
   if (!v) v = choose_tile_variant(1, M, tiles, 1);
   return hip_status(launch_tile(*v, 1, p, w, e, int(g_group_m.load()), static_cast<hipStream_t>(stream)),
                     "w4a16 tile kernel launch");
+}
+
+size_t mqk_w4a16_gemm_workspace_size(int64_t M, int64_t K, int64_t N) {
+  if (M <= 0 || K <= 0 || K % kBK != 0 || N <= 0 || N % kHeadDim != 0 || N / kHeadDim > kMaxTiles) return 0;
+  const int tiles = int(N / kHeadDim);
+  const Plan pl = plan_fused(1, M, K, tiles, true, device_topology());
+  return pl.splits > 0 ? decode_workspace_bytes(tiles, pl.splits, pl.passes) : 0;
+}
+
+int mqk_w4a16_gemm_ex(const mqk_bf16* x, const int32_t* qweight, const void* scales, const int32_t* qzeros,
+                      int64_t M, int64_t K, int64_t N, int group, int scale_type, mqk_bf16* out,
+                      void* workspace, size_t ws_bytes, void* stream) {
+  if (M < 0 || K <= 0) return fail(MQK_ERR_BAD_SHAPE, "need M >= 0, K > 0");
+  if (K % kBK != 0) return fail(MQK_ERR_UNSUPPORTED, "K=%lld must be a multiple of 64", (long long)K);
+  int st = validate_int4(qweight, scales, qzeros, K, N, group, scale_type, "w4a16_gemm");
+  if (st != MQK_OK) return st;
+  if (M == 0) return ok();
+  if (!x || !out) return fail(MQK_ERR_NULL_POINTER, "x/out must be non-NULL");
+  if (!aligned16(x)) return fail(MQK_ERR_MISALIGNED, "x must be 16-byte aligned");
+  // the planned kernels (split-K decode kernel for small M) need whole 128-column
+  // tiles and 16-byte aligned operands; anything else takes the tile kernels
+  if (N % kHeadDim != 0 || N / kHeadDim > kMaxTiles || !aligned16(qweight) || !aligned16(scales) ||
+      !aligned16(qzeros) || !aligned16(out))
+    return mqk_w4a16_gemm(x, qweight, scales, qzeros, M, K, N, group, scale_type, out, stream);
+  const int tiles = int(N / kHeadDim);
+  ProblemArgs p{x, M, K, tiles};
+  WeightArgs w{};
+  w.qw[0] = qweight;
+  w.sc[0] = scales;
+  w.qz[0] = qzeros;
+  w.n_cols[0] = N;
+  w.group = group;
+  w.scale_fp16 = scale_type == MQK_SCALE_FP16;
+  EpilogueArgs e{};
+  e.qkv = 0;
+  e.Hq = tiles;
+  e.Hkv = 0;
+  e.out = out;
+  e.N = N;
+  return run_fused(1, p, w, e, 0.f, workspace, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 static int fused_w4a16_impl(const mqk_bf16* x, const int32_t* qw_q, const void* sc_q,

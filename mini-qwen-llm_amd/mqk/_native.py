@@ -86,6 +86,10 @@ SIGNATURES = {
     "mqk_w4a16_gemm": (
         _I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P],
     ),
+    "mqk_w4a16_gemm_workspace_size": (_SZ, [_I64, _I64, _I64]),
+    "mqk_w4a16_gemm_ex": (
+        _I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _SZ, _P],
+    ),
     "mqk_fused_qkv_rope_w4a16": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P,  # x, (qw, sc, qz) x 3

@@ -69,11 +69,13 @@ def w4a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
     out = torch.empty(M, N, dtype=torch.bfloat16, device=device)
     if M == 0:
         return out
+    lib = _native.library()
     stream = torch.cuda.current_stream(device)
-    status = _native.call(device, _native.library().mqk_w4a16_gemm,
+    ws = _native.workspace(device, stream, int(lib.mqk_w4a16_gemm_workspace_size(M, K, N)))
+    status = _native.call(device, lib.mqk_w4a16_gemm_ex,
         x.data_ptr(), qweight.data_ptr(), scales.data_ptr(), qzeros.data_ptr(), M, K, N,
-        group_size, st, out.data_ptr(), stream.cuda_stream)
-    _native.check(status, "mqk_w4a16_gemm")
+        group_size, st, out.data_ptr(), _native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
+    _native.check(status, "mqk_w4a16_gemm_ex")
     return out
 
 

@@ -58,8 +58,9 @@ def _check_gemm(out, x, qw, sc, qz, group, label):
     assert rl <= 1e-2, f"{label}: rel L2 vs exact dequant {rl}"
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 128, 8), (1, 1024, 4096), (4, 1024, 4096), (16, 1024, 4096),
-                                   (200, 1024, 1000), (300, 512, 264)])
+@pytest.mark.parametrize("M,K,N", [(1, 128, 8), (1, 1024, 4096), (4, 1024, 4096), (8, 1024, 4096),
+                                   (16, 1024, 4096), (64, 1024, 4096), (65, 1024, 4096), (300, 4096, 1024),
+                                   (1024, 1024, 4096), (200, 1024, 1000), (300, 512, 264)])
 def test_w4a16_gemm(M, K, N, device):
     import mqk
     qw, sc, qz = _quant(K, N, seed=M + N)
@@ -68,6 +69,34 @@ def test_w4a16_gemm(M, K, N, device):
     torch.cuda.synchronize()
     assert out.shape == (M, N) and out.dtype == torch.bfloat16
     _check_gemm(out, x, qw, sc, qz, 128, f"M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("M", [1, 16, 200])
+def test_w4a16_gemm_decode_path_matches_tile(M, device):
+    """Small M runs on the split-K decode kernel (the reference's decode GEMV
+    regime, w4a16_gemm.py:110-189): it must agree with the tile kernel (forced
+    with decode_max_t = 0 and decode_blocks = 0) within the fp32 summation-order
+    bound, and launch one decode kernel, no tile kernel."""
+    import mqk
+    from conftest import launched_kernels
+    K, N = 1024, 4096
+    qw, sc, qz = (t.to(device) for t in _quant(K, N, seed=40 + M))
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(41 + M)).bfloat16().to(device)
+    run = lambda: mqk.w4a16_gemm(x, qw, sc, qz, 128)
+    assert launched_kernels(run) == (["decode"] if M <= 64 else ["decode_multi"])
+    dec = run()
+    mqk.set_option("decode_max_t", 0)
+    mqk.set_option("decode_blocks", 0)
+    try:
+        tile = run()
+        torch.cuda.synchronize()
+        assert launched_kernels(run) in (["tile_w4"], ["tile_reg"])
+    finally:
+        mqk.set_option("decode_max_t", 64)
+        mqk.set_option("decode_blocks", 16)
+    a, b = dec.float(), tile.float()
+    assert float((a - b).abs().max()) <= float(2.0 ** -7 * b.abs().max() + 1e-3)
+    _check_gemm(dec.cpu(), x.cpu(), qw.cpu(), sc.cpu(), qz.cpu(), 128, f"decode path M={M}")
 
 
 def test_w4a16_gemm_fp16_scales_and_group64(device):
