@@ -74,7 +74,7 @@ def test_noalloc_mid_t_then_single_token(device):
 
 def test_noalloc_prefill_then_decode(device):
     """A tile launch (which needs no scratch), then a decode step
-    at hidden 1024, whose 32 heads x 8 splits fill the scratch exactly."""
+    at hidden 1024."""
     _pair(Case(2, 600, 1024, 16, 8, seed=505), device)
     _pair(_decode_case(40, 506, hidden=1024, Hq=16, Hkv=8), device)
 
