@@ -37,6 +37,41 @@ namespace {
 
 constexpr int kEpiPitch = kHeadDim + 4;     // fp32 pitch of the epilogue head tile
 
+// Epilogue arithmetic with every rounding step written out (no contraction left
+// to the compiler), so that each tile shape's instantiation gives identical bits
+// for the same accumulators however the compiler schedules it.
+//
+// Sum of squares of one thread's 16 head dims d = 8c+i and 64+8c+i (i = 0..7).
+__device__ __forceinline__ float run_sumsq(const float (&lo)[8], const float (&hi)[8]) {
+#pragma clang fp contract(off)
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = ss + __builtin_fmaf(lo[i], lo[i], hi[i] * hi[i]);
+  return ss;
+}
+
+// 1 / rms of a head from the sum of squares of its 128 dims.
+__device__ __forceinline__ float head_rms(float ss, float eps) {
+#pragma clang fp contract(off)
+  return rsqrtf(__builtin_fmaf(ss, 1.0f / float(kHeadDim), eps));
+}
+
+// RMSNorm (fused_qkv_rope.py:98-100) then rotate-half RoPE (:102-118) of the
+// dim pair (d, d+64); gl / gh are the gammas of d / d+64 and element
+// (wd, sh) of the cos / sin registers holds the table values of d and d+64.
+__device__ __forceinline__ void norm_rope_pair(float& lo, float& hi, float rms, float gl, float gh,
+                                               const u32x4_t (&c2)[2], const u32x4_t (&s2)[2], int wd, int sh) {
+#pragma clang fp contract(off)
+  const float x1n = lo * rms * gl;
+  const float x2n = hi * rms * gh;
+  const float co1 = bf16_to_f32((c2[0][wd] >> sh) & 0xFFFFu);
+  const float co2 = bf16_to_f32((c2[1][wd] >> sh) & 0xFFFFu);
+  const float si1 = bf16_to_f32((s2[0][wd] >> sh) & 0xFFFFu);
+  const float si2 = bf16_to_f32((s2[1][wd] >> sh) & 0xFFFFu);
+  lo = __builtin_fmaf(x1n, co1, -(x2n * si1));
+  hi = __builtin_fmaf(x2n, co2, x1n * si2);
+}
+
 // SBK = K extent of one stage (32 or 64): staged rows of 64 or 128 bytes.  A
 // CU's L2 -> LDS rate depends on the bytes per row: 128-byte rows measured
 // ~1.35x the rate of 64-byte rows (fewer, full-line requests in flight).
@@ -206,11 +241,8 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
       }
       if (e.qkv && proj != 2) {
         // RMSNorm over the head (fused_qkv_rope.py:98-100), then rotate-half RoPE (:102-118)
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) ss += lo[i] * lo[i] + hi[i] * hi[i];
-        ss = sum8_lanes(ss);
-        const float rms = rsqrtf(ss * (1.0f / float(kHeadDim)) + e.eps);
+        const float ss = sum8_lanes(run_sumsq(lo, hi));
+        const float rms = head_rms(ss, e.eps);
         u32x4_t c2[2], s2[2];
         if constexpr (kPreload) {
           c2[0] = cs[q][0]; c2[1] = cs[q][1]; s2[0] = sn[q][0]; s2[1] = sn[q][1];
@@ -223,14 +255,7 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
           const int wd = i >> 1, sh = (i & 1) * 16;
           const float gl = kHoistGamma ? g1[i] : bf16_to_f32((g[0][wd] >> sh) & 0xFFFFu);
           const float gh = kHoistGamma ? g2[i] : bf16_to_f32((g[1][wd] >> sh) & 0xFFFFu);
-          const float x1n = lo[i] * rms * gl;
-          const float x2n = hi[i] * rms * gh;
-          const float co1 = bf16_to_f32((c2[0][wd] >> sh) & 0xFFFFu);
-          const float co2 = bf16_to_f32((c2[1][wd] >> sh) & 0xFFFFu);
-          const float si1 = bf16_to_f32((s2[0][wd] >> sh) & 0xFFFFu);
-          const float si2 = bf16_to_f32((s2[1][wd] >> sh) & 0xFFFFu);
-          lo[i] = x1n * co1 - x2n * si1;
-          hi[i] = x2n * co2 + x1n * si2;
+          norm_rope_pair(lo[i], hi[i], rms, gl, gh, c2, s2, wd, sh);
         }
       }
       if (t < p.M) {
