@@ -186,7 +186,7 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
       return pl;
     }
   }
-  pl.v = choose_tile_variant(int(g_prefill_tile.load()), M, n_tiles, int4);
+  pl.v = choose_tile_variant(int(g_prefill_tile.load()), M, n_tiles, int4, topo.cus);
   if (!pl.v || !g_tail_split.load() || !aligned || M <= 64) return pl;
   const int64_t r = M % pl.v->bm;
   if (r == 0 || r > 64 || !use_decode(r)) return pl;
@@ -252,7 +252,7 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
     // and with an input norm hold gamma in LDS next to their ring.
     if (v->id >= 10 && (!(epilogue_aligned(e) && (!int4 || int4_aligned(w))) ||
                         (p.in_gamma && tile_dma_lds_bytes(v->id) + p.K * 2 > 160 * 1024)))
-      v = choose_tile_variant(p.n_tiles % 2 == 0 ? 4 : 1, p.M, p.n_tiles, int4);
+      v = choose_tile_variant(p.n_tiles % 2 == 0 ? 4 : 1, p.M, p.n_tiles, int4, p.cus);
     ProblemArgs pm = p;
     pm.M = p.M - pl.tail;
     const int st = hip_status(launch_tile(*v, int4, pm, w, e, int(g_group_m.load()), stream), "tile kernel launch");
@@ -601,8 +601,8 @@ int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales
   // register-staged kernel (variant 1), which bounds-checks columns.
   const TileVariant* v = nullptr;
   if (N % kHeadDim == 0 && aligned16(qweight) && aligned16(scales) && aligned16(qzeros))
-    v = choose_tile_variant(int(g_prefill_tile.load()), M, tiles, 1);
-  if (!v) v = choose_tile_variant(1, M, tiles, 1);
+    v = choose_tile_variant(int(g_prefill_tile.load()), M, tiles, 1, topo.cus);
+  if (!v) v = choose_tile_variant(1, M, tiles, 1, topo.cus);
   return hip_status(launch_tile(*v, 1, p, w, e, int(g_group_m.load()), static_cast<hipStream_t>(stream)),
                     "w4a16 tile kernel launch");
 }

@@ -90,7 +90,7 @@ struct TileVariant {
 int tile_variant_count();
 const TileVariant* tile_variant(int index);
 // Picks a variant for the problem (id 0 = automatic).
-const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles, int int4);
+const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles, int int4, int cus);
 hipError_t launch_tile(const TileVariant& v, int int4, const ProblemArgs& p, const WeightArgs& w,
                        const EpilogueArgs& e, int group_m, hipStream_t stream);
 // Direct-to-LDS pipelined tile kernel (variant ids >= 10, bf16 weights).

@@ -423,14 +423,15 @@ static bool supports(const TileVariant& v, int int4) {
   return v.id < 10 || (int4 ? v.id >= 30 : v.id < 30);
 }
 
-const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles, int int4) {
+const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles, int int4, int cus_) {
   if (requested_id > 0) {
     const TileVariant* v = find_variant(requested_id);
     if (!v || n_tiles % v->hpt != 0 || !supports(*v, int4)) return nullptr;
     return v;
   }
   // Score = relative per-tile speed (measured on MI355X) x fraction of the last
-  // round of workgroups that is busy, assuming one workgroup per CU at a time.
+  // round of workgroups that is busy, assuming one workgroup per CU at a time
+  // (cus_: the device's compute units).
   struct Cand { int id; float speed; };
   // (per-tile rates measured on MI355X: 64-wide k stages (16, 17, 18) beat 32-wide
   // ones; 128x384 wins when its tiles fill the chip, 256x256 otherwise)
@@ -443,7 +444,7 @@ const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles,
   static const Cand int4_cands[] = {{31, 1.00f}, {30, 0.75f}, {32, 0.54f}};
   const Cand* cands = int4 ? int4_cands : bf16_cands;
   const int ncand = int(int4 ? sizeof(int4_cands) / sizeof(int4_cands[0]) : sizeof(bf16_cands) / sizeof(bf16_cands[0]));
-  const int64_t cus = 256;
+  const int64_t cus = cus_ > 0 ? cus_ : 256;
   const TileVariant* best = find_variant(1);
   float best_score = -1.f;
   for (int i = 0; i < ncand; ++i) {
