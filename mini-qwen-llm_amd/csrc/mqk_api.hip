@@ -48,6 +48,7 @@ std::atomic<int64_t> g_tail_split{1};
 std::atomic<int64_t> g_decode_blocks{16};  // most 64-row decode blocks for one call (T > 64)
 std::atomic<int64_t> g_decode_cost_model{1};  // 0: decode blocks whenever eligible (measurements)
 std::atomic<int64_t> g_decode_passes{16};  // most 64-row blocks one decode launch covers (1..16)
+std::atomic<int64_t> g_tile_ksplit{1};  // split-K tile launches: 0 off, 1 by cost model, >= 2 that split count
 
 constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace (per head)
 
@@ -144,10 +145,48 @@ struct Plan {
   int64_t tail = 0;                // rows run by the decode kernel after the tile rows
   int splits = 0;                  // decode kernel split-K factor (0: no decode launch)
   int passes = 1;                  // 64-row blocks per decode launch
+  int ksplit = 0;                  // tile launch split over K (0: one workgroup per tile)
 };
 
+// Split-K tile launch for problems with fewer tiles than CUs (bf16 weights):
+// variant 16 (128 x 384) when the heads tile by 3, else 18 (256 x 256).  Returns
+// the split count (0: none fits) and its modelled kernel time, fitted on MI355X
+// (hidden 1024 / 2048 / 4096, T = 129 .. 1024, 2 to 6 splits; within ~2 us):
+// ~15 us of launch, waits and epilogue, ~1.24 us per 64-k stage of a split, and
+// ~0.28 us per MB of fp32 partials published and read back.  At most one split
+// per 32-row unit of a tile (more would leave splits with no rows to finish).
+int plan_tile_split(int64_t M, int64_t K, int n_tiles, const Topology& topo, const TileVariant*& v, double& us) {
+  v = nullptr;
+  us = 1e30;
+  const int64_t req = g_tile_ksplit.load();
+  if (req == 0 || g_prefill_tile.load() != 0) return 0;
+  const int id = n_tiles % 3 == 0 ? 16 : (n_tiles % 2 == 0 ? 18 : 0);
+  if (id == 0) return 0;
+  for (int i = 0; i < tile_variant_count(); ++i)
+    if (tile_variant(i)->id == id) v = tile_variant(i);
+  if (!v) return 0;
+  const int64_t tiles = (M + v->bm - 1) / v->bm * (n_tiles / v->hpt);
+  const int64_t X = topo.xcds;
+  const int64_t slots = (tiles + X - 1) / X * X;  // tiles padded to whole XCD shares
+  const int64_t nkt = K / 64;
+  const double stage_us = id == 16 ? 1.24 : 1.3;
+  const double part_mb = (id == 16 ? 196608.0 : 262144.0) * 1e-6;  // one workgroup's partial
+  const int units = id == 16 ? 4 : 8;
+  int best = 0;
+  const int lo = req >= 2 ? int(req) : 2, hi = req >= 2 ? int(req) : units;
+  for (int s = lo; s <= hi; ++s) {
+    if (slots * s > topo.cus || nkt < 4 * int64_t(s) || tiles > 512) break;
+    const double t = 15.0 + double(nkt) / s * stage_us + 0.28 * part_mb * double(tiles) * s;
+    if (t < us) {
+      us = t;
+      best = s;
+    }
+  }
+  return best;
+}
+
 Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const Topology& topo,
-                bool allow_blocks = true, bool in_norm = false) {
+                bool allow_blocks = true, bool in_norm = false, bool allow_split = true) {
   Plan pl;
   const int64_t cus = topo.cus;
   if (use_decode(M) && aligned) {
@@ -177,14 +216,24 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
   const double pass_us = 0.5 + double(K) / 4096.0 * 4.5;
   const double blocks_us = double(launches) * dec_us + double(nblk - launches) * pass_us;
   const double tile_us = double(K) / 64.0 * (int4 ? 2.1 : 1.15) + 5.0;
-  if (allow_blocks && aligned && M > 64 && g_prefill_tile.load() == 0 && g_decode_max_t.load() >= 64 &&
-      nblk <= g_decode_blocks.load() && (blocks_us <= tile_us || !g_decode_cost_model.load())) {
+  // split-K tile launch (bf16): taken when its model beats both the one-workgroup-
+  // per-tile launch and the decode blocks
+  const TileVariant* sv = nullptr;
+  double split_us = 1e30;
+  const int ksplit = (!int4 && aligned && allow_split && M > 64) ? plan_tile_split(M, K, n_tiles, topo, sv, split_us) : 0;
+  const bool blocks_ok = allow_blocks && aligned && M > 64 && g_prefill_tile.load() == 0 &&
+                         g_decode_max_t.load() >= 64 && nblk <= g_decode_blocks.load() && blk_splits > 0;
+  const bool forced_split = ksplit > 0 && g_tile_ksplit.load() >= 2;
+  if (blocks_ok && !forced_split && (!g_decode_cost_model.load() || (blocks_us <= tile_us && blocks_us <= split_us))) {
     pl.splits = blk_splits;
-    if (pl.splits > 0) {
-      pl.tail = M;
-      pl.passes = int(std::min<int64_t>(per_launch, nblk));
-      return pl;
-    }
+    pl.tail = M;
+    pl.passes = int(std::min<int64_t>(per_launch, nblk));
+    return pl;
+  }
+  if (ksplit > 0 && (forced_split || split_us < tile_us)) {
+    pl.v = sv;
+    pl.ksplit = ksplit;
+    return pl;
   }
   pl.v = choose_tile_variant(int(g_prefill_tile.load()), M, n_tiles, int4, topo.cus);
   if (!pl.v || !g_tail_split.load() || !aligned || M <= 64) return pl;
@@ -217,18 +266,28 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
                 (long long)g_prefill_tile.load(), p.n_tiles, int4 ? ", int4 weights" : "");
   // (the decode kernel's arrival counters open every workspace and must stay zero,
   // so the scales never start before them, whichever kernel runs this call)
-  size_t base = pl.splits > 0 ? decode_workspace_bytes(p.n_tiles, pl.splits, pl.passes) : decode_counter_bytes();
-  // bytes the plan needs: the decode region, then (input norm) the per-token scales
+  auto region = [&](const Plan& q) {
+    if (q.ksplit > 0) return kDecodeCounterBytes + tile_split_part_bytes(q.v->id, p.M, p.n_tiles, q.ksplit);
+    return q.splits > 0 ? decode_workspace_bytes(p.n_tiles, q.splits, q.passes) : decode_counter_bytes();
+  };
+  size_t base = region(pl);
+  // bytes the plan needs: the decode (or split-tile) region, then (input norm) the per-token scales
   const size_t scale_bytes = p.in_gamma ? align_up(size_t(p.M) * sizeof(float), 256) : 0;
   auto fits = [&](size_t b) { return workspace && ws_bytes >= align_up(b, 256) + scale_bytes; };
+  const bool split_ok = epilogue_aligned(e) && !(p.in_gamma && pl.v && tile_dma_lds_bytes(pl.v->id) + p.K * 2 > 160 * 1024);
+  if (pl.ksplit > 0 && (!fits(base) || !split_ok)) {
+    // a workspace sized without the split-K tile launch (or operands it cannot take): plan without it
+    pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, true, p.in_gamma != nullptr, false);
+    base = region(pl);
+  }
   while (!pl.v && pl.passes > 1 && !fits(base)) {
     pl.passes = (pl.passes + 1) / 2;  // a workspace sized for fewer blocks per launch
     base = decode_workspace_bytes(p.n_tiles, pl.splits, pl.passes);
   }
   if (!pl.v && p.M > 64 && !fits(base)) {
     // decode blocks planned, but a workspace sized without them: the tile kernel
-    pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, false, p.in_gamma != nullptr);
-    base = pl.splits > 0 ? decode_workspace_bytes(p.n_tiles, pl.splits) : decode_counter_bytes();
+    pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, false, p.in_gamma != nullptr, false);
+    base = region(pl);
   }
   if (pl.v && pl.splits > 0 && !fits(base)) {
     pl.tail = 0;  // a workspace sized without the tail launch: run the tile kernel on every row
@@ -236,7 +295,8 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
     base = decode_counter_bytes();
   }
   const size_t scale_off = align_up(base, 256);
-  const size_t need = p.in_gamma ? scale_off + size_t(p.M) * sizeof(float) : (pl.splits > 0 ? base : 0);
+  const size_t need =
+      p.in_gamma ? scale_off + size_t(p.M) * sizeof(float) : ((pl.splits > 0 || pl.ksplit > 0) ? base : 0);
   if (need > 0 && (!workspace || ws_bytes < need))
     return fail(MQK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given%s", need, ws_bytes,
                 workspace ? "" : " (NULL)");
@@ -246,6 +306,10 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
     if (st != MQK_OK) return st;
     p.in_scale = scale;
   }
+  if (pl.ksplit > 0)
+    return hip_status(launch_tile_dma_split(pl.v->id, p, w, e, pl.ksplit, g_decode_force_recompute,
+                                            g_decode_max_spins, workspace, stream),
+                      "split-K tile kernel launch");
   if (pl.v) {
     const TileVariant* v = pl.v;
     // The pipelined variants (ids >= 10) read every operand with 16-byte direct loads,
@@ -309,6 +373,7 @@ size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hid
   for (int int4 = 0; int4 < 2; ++int4) {  // the same size serves both weight formats
     const Plan pl = plan_fused(int4, T, hidden, tiles, true, device_topology());
     if (pl.splits > 0) n = std::max(n, decode_workspace_bytes(tiles, pl.splits, pl.passes));
+    if (pl.ksplit > 0) n = std::max(n, kDecodeCounterBytes + tile_split_part_bytes(pl.v->id, T, tiles, pl.ksplit));
   }
   return n;
 }
@@ -768,6 +833,9 @@ int mqk_set_option(const char* name, int64_t value) {
   } else if (!strcmp(name, "decode_cost_model")) {
     if (value != 0 && value != 1) return fail(MQK_ERR_BAD_OPTION, "decode_cost_model must be 0 or 1");
     g_decode_cost_model = value;
+  } else if (!strcmp(name, "tile_ksplit")) {
+    if (value < 0 || value > 16) return fail(MQK_ERR_BAD_OPTION, "tile_ksplit must be in [0, 16]");
+    g_tile_ksplit = value;
   } else if (!strcmp(name, "group_m")) {
     if (value < 1 || value > 1024) return fail(MQK_ERR_BAD_OPTION, "group_m must be in [1, 1024]");
     g_group_m = value;
@@ -787,6 +855,7 @@ int64_t mqk_get_option(const char* name) {
   if (!strcmp(name, "decode_blocks")) return g_decode_blocks.load();
   if (!strcmp(name, "decode_passes")) return g_decode_passes.load();
   if (!strcmp(name, "decode_cost_model")) return g_decode_cost_model.load();
+  if (!strcmp(name, "tile_ksplit")) return g_tile_ksplit.load();
   if (!strcmp(name, "decode_force_recompute")) return g_decode_force_recompute;
   if (!strcmp(name, "decode_max_spins")) return g_decode_max_spins;
   if (!strcmp(name, "device_cus")) return device_topology().cus;    // read-only: the current device's

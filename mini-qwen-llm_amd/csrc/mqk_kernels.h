@@ -96,6 +96,21 @@ hipError_t launch_tile(const TileVariant& v, int int4, const ProblemArgs& p, con
 // Direct-to-LDS pipelined tile kernel (variant ids >= 10, bf16 weights).
 hipError_t launch_tile_dma(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e, int group_m,
                            hipStream_t stream);
+// Split-K launch of a pipelined bf16 variant (16: 128x384, 18: 256x256) for
+// problems with fewer tiles than CUs: each tile's K range is cut into ksplit
+// balanced ranges, run by ksplit workgroups on one XCD; each publishes its fp32
+// accumulators and counts its arrival in counters[tile]; once all have arrived,
+// each finishes its share of the tile's 32-row units (partials summed in split
+// order, then the tile epilogue on those rows).  A split whose bounded wait
+// (max_spins polls) runs out hands its units to the last arrival.  If a split
+// ran on another XCD (or force_recompute), the last arrival recomputes every
+// split (same arithmetic, same order) and finishes the whole tile.  The
+// workspace: kDecodeCounterBytes of counters (zero; words [0, 512) and
+// [512, 1024) per tile, re-armed by the launch), then
+// tile_split_part_bytes(...) of partials.
+hipError_t launch_tile_dma_split(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
+                                 int ksplit, int force_recompute, int max_spins, void* workspace, hipStream_t stream);
+size_t tile_split_part_bytes(int id, int64_t M, int n_tiles, int ksplit);
 // int4-weight (W4A16) variant of the pipelined kernel, ids 30-32.
 hipError_t launch_tile_dma_w4(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                               int group_m, hipStream_t stream);

@@ -154,10 +154,13 @@ __device__ __forceinline__ void norm_chunk(unsigned char* chunk_ptr, int64_t k0,
 // RoPE pair is thread-local; each output row segment is written with 16-byte
 // stores.  prow[q] holds the RoPE table row of this thread's row (tid/8) + q*kRowStep,
 // cslot[q] its paged-KV-cache slot (-1: none).
+// units: bit u set = rows [32u, 32u+32) of the tile are stored (the split-K
+// launch finishes a tile's rows in 32-row units spread over its workgroups).
 template <int BM, int NH, int WM, int WN, int THREADS, int MB, int NB, class RowV, class SlotV>
 __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], const RowV& prow,
                                               const SlotV& cslot, int ht, int64_t m0, const ProblemArgs& p,
-                                              const EpilogueArgs& e, unsigned char* smem) {
+                                              const EpilogueArgs& e, unsigned char* smem,
+                                              uint32_t units = 0xFFFFFFFFu) {
   constexpr int kTM = BM / WM;
   constexpr int kTN = NH * kHeadDim / WN;
   constexpr int kRowStep = THREADS / 8;
@@ -228,6 +231,8 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
     }
 #pragma unroll
     for (int q = 0; q < kPasses; ++q) {
+      constexpr uint32_t kPassUnits = (kRowStep / 32) >= 32 ? 0xFFFFFFFFu : ((1u << (kRowStep / 32)) - 1u);
+      if (((units >> (q * kRowStep / 32)) & kPassUnits) == 0) continue;  // no stored row in this pass
       const int r0 = (tid >> 3) + q * kRowStep;
       const int64_t t = m0 + r0;
       const float* rowp = ep + r0 * kEpiPitch;
@@ -258,7 +263,7 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
           norm_rope_pair(lo[i], hi[i], rms, gl, gh, c2, s2, wd, sh);
         }
       }
-      if (t < p.M) {
+      if (t < p.M && ((units >> (r0 >> 5)) & 1u)) {
         u32x4_t o1, o2;
         o1.x = pack_bf16x2(lo[0], lo[1]); o1.y = pack_bf16x2(lo[2], lo[3]);
         o1.z = pack_bf16x2(lo[4], lo[5]); o1.w = pack_bf16x2(lo[6], lo[7]);
@@ -287,6 +292,22 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
     }
     __syncthreads();  // the next head reuses ep
   }
+}
+
+// Split-K mode (SPLIT): kernel arguments of a launch_tile_dma_split launch.
+struct TileSplit {
+  int ksplit;          // K ranges per tile
+  int ctl;             // bit 0: every split counts as misplaced (recompute path, for tests)
+  int max_spins;       // polls of the arrival word before a split hands its rows off
+  float* part;         // fp32 partials: [tile][split][chunk 0..MB*NB*4-1][thread] of f32x4
+  uint32_t* counters;  // arrival counter per tile; kDecodeRecomputeWord counts recomputed tiles
+};
+
+constexpr uint32_t kSplitForeign = 1u << 24;  // arrival increment of a split on an unexpected XCD
+constexpr int kSplitExitOffset = 512;         // counters[512 + tile]: splits done with the arrival word (tiles < 512)
+
+__device__ __forceinline__ int hw_xcc_id() {
+  return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11));  // hwreg(HW_REG_XCC_ID, 0, 4)
 }
 
 template <int BM, int NH, int WM, int WN, int NS, int SBK>
@@ -438,6 +459,333 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, cslot, ht, m0, p, e, smem);
 }
 
+// The split-K launch of the pipelined kernel (a separate kernel, so that the
+// one-workgroup-per-tile kernel above keeps its own register allocation).
+template <int BM, int NH, int WM, int WN, int NS, int SBK>
+__global__ void __launch_bounds__(WM* WN * 64)
+tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp) {
+  using S = DmaShape<BM, NH, WM, WN, NS, SBK>;
+  constexpr int kRowBytes = S::kRowBytes;
+  constexpr int BN = S::kBN;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[S::kLdsBytes];
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WM;
+  const int wn = wave / WM;
+
+  // ---- tile coordinates: XCD-contiguous ids, grouped along M ------------------
+  const int n_mt = int((p.M + BM - 1) / BM);
+  const int n_ht = p.n_tiles / NH;
+  int mt, ht, split = 0, tile = 0;
+  bool foreign = false;
+  {
+    // Workgroup b runs on XCD b % X.  XCD x takes tiles [x*tpx, (x+1)*tpx), all
+    // splits of each (so a tile's partials meet in one L2); row tiles vary
+    // fastest, so an XCD's tiles share weight panels.
+    const int X = p.xcds;
+    const int tiles = n_mt * n_ht;
+    const int tpx = (tiles + X - 1) / X;
+    const int xcd = int(blockIdx.x) % X;
+    const int l = int(blockIdx.x) / X;
+    split = l % sp.ksplit;
+    const int slot = l / sp.ksplit;
+    tile = xcd * tpx + slot;
+    if (slot >= tpx || tile >= tiles) return;  // grid padding
+    mt = tile % n_mt;
+    ht = tile / n_mt;
+    foreign = (sp.ctl & 1) || hw_xcc_id() % X != xcd;
+  }
+  const int64_t m0 = int64_t(mt) * BM;
+
+  // Epilogue geometry: thread -> rows (tid / 8) + q * kRowStep and the column pairs
+  // [8c, 8c+8) / [64+8c, +8) of every head.  The RoPE table row of each of its
+  // rows (a positions[] load in positions mode) is read now, under the main loop.
+  constexpr int kRowStep = S::kThreads / 8;
+  constexpr int kPasses = BM / kRowStep;
+  // (vector types: indexed in registers even where the compiler merges the
+  // per-row code paths, where a plain array would go to scratch memory)
+  typedef int32_t RowV __attribute__((ext_vector_type(kPasses)));
+  typedef int64_t SlotV __attribute__((ext_vector_type(kPasses)));
+  RowV prow;
+  SlotV cslot;  // paged-KV-cache slot of the row (-1: none)
+#pragma unroll
+  for (int q = 0; q < kPasses; ++q) {
+    const int64_t t = m0 + (tid >> 3) + q * kRowStep;
+    prow[q] = (e.qkv && t < p.M) ? int32_t(rope_row(e, t)) : 0;
+    cslot[q] = (e.qkv && t < p.M) ? paged_slot(e, t) : -1;
+  }
+  const int64_t K = p.K;
+
+  // ---- this lane's sources: load instruction i of a stage fills staged rows
+  // [R*(wave + i*W), +R), R = rows per load; lane -> row +lane/chunks, slot lane%chunks
+  const uint16_t* src[S::kLoadsPerWave];
+  uint32_t dst_off[S::kLoadsPerWave];
+#pragma unroll
+  for (int i = 0; i < S::kLoadsPerWave; ++i) {
+    const int row0 = S::kRowsPerLoad * (wave + i * S::kWaves);
+    const int row = row0 + lane / S::kChunks;
+    const int chunk = stage_slot<SBK>(row, lane % S::kChunks);  // global chunk stored in slot lane % chunks
+    if (row < BM) {
+      int64_t grow = m0 + row;
+      grow = grow < p.M ? grow : p.M - 1;  // rows past M re-read the last row; never stored
+      src[i] = p.x + grow * K + chunk * 8;
+    } else {
+      const int brow = row - BM;
+      int proj, hh;
+      split_head(ht * NH + brow / kHeadDim, e.Hq, e.Hkv, proj, hh);
+      int64_t col = int64_t(hh) * kHeadDim + (brow % kHeadDim);
+      col = col < w.n_cols[proj] ? col : w.n_cols[proj] - 1;
+      src[i] = w.w[proj] + col * K + chunk * 8;
+    }
+    dst_off[i] = uint32_t(row0 * kRowBytes);
+  }
+  // input RMSNorm: scale of the x row and k offset of the chunk each of this
+  // lane's x loads brings in (load i < kALoads, row0 + lane / chunks, slot lane % chunks)
+  const bool in_norm = p.in_gamma != nullptr;
+  float a_scale[S::kALoads];
+  int a_koff[S::kALoads];
+#pragma unroll
+  for (int i = 0; i < S::kALoads; ++i) {
+    const int row = S::kRowsPerLoad * (wave + i * S::kWaves) + lane / S::kChunks;
+    int64_t grow = m0 + row;
+    grow = grow < p.M ? grow : p.M - 1;
+    a_scale[i] = in_norm ? p.in_scale[grow] : 1.f;
+    a_koff[i] = stage_slot<SBK>(row, lane % S::kChunks) * 8;
+  }
+  if (in_norm) {
+    stage_gamma<S::kThreads>(p);
+    __syncthreads();
+  }
+  // stage j of a k range starting at stage kt0 goes to ring slot j % NS
+  auto issue = [&](int kt0, int j) {
+    const uint32_t base = lds0 + uint32_t((j % NS) * S::kStageBytes);
+#pragma unroll
+    for (int i = 0; i < S::kLoadsPerWave; ++i) {
+      dma16(src[i] + int64_t(kt0 + j) * SBK, base + dst_off[i]);
+    }
+  };
+
+  // ---- main loop over stages [kt0, kt0 + nkt) -------------------------------------
+  f32x16_t acc[S::kMB][S::kNB];
+  const int c32 = lane & 31;
+  const int khalf = lane >> 5;
+  auto run_range = [&](int kt0, int nkt) {
+#pragma unroll
+  for (int mb = 0; mb < S::kMB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < S::kNB; ++nb) acc[mb][nb] = f32x16_t{};
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nkt) issue(kt0, s);
+
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int ahead = min(NS - 2, nkt - 1 - kt);  // stages already issued after kt
+    wait_stage<NS, S::kLoadsPerWave>(ahead);
+    if (in_norm) {  // this wave's x chunks of stage kt have landed: normalise them in place
+#pragma unroll
+      for (int i = 0; i < S::kALoads; ++i)
+        norm_chunk(smem + (kt % NS) * S::kStageBytes + dst_off[i] + lane * 16,
+                   int64_t(kt0 + kt) * SBK + a_koff[i], a_scale[i]);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    barrier();
+    if (kt + NS - 1 < nkt) issue(kt0, kt + NS - 1);
+    const unsigned char* st = smem + (kt % NS) * S::kStageBytes;
+#pragma unroll
+    for (int ks = 0; ks < SBK / 16; ++ks) {
+      const int chunk = 2 * ks + khalf;
+      u32x4_t af[S::kMB], bf[S::kNB];
+#pragma unroll
+      for (int mb = 0; mb < S::kMB; ++mb) {
+        const int row = wm * S::kTM + mb * 32 + c32;
+        af[mb] = *reinterpret_cast<const u32x4_t*>(st + row * kRowBytes + stage_slot<SBK>(row, chunk) * 16);
+      }
+#pragma unroll
+      for (int nb = 0; nb < S::kNB; ++nb) {
+        const int row = BM + wn * S::kTN + nb * 32 + c32;
+        bf[nb] = *reinterpret_cast<const u32x4_t*>(st + row * kRowBytes + stage_slot<SBK>(row, chunk) * 16);
+      }
+#pragma unroll
+      for (int mb = 0; mb < S::kMB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < S::kNB; ++nb) {
+          acc[mb][nb] = mfma_32x32x16(af[mb], bf[nb], acc[mb][nb]);
+        }
+    }
+  }
+  barrier();  // every wave is done with the ring; the epilogue (or the next range) reuses the LDS
+  };
+
+  const int nkt_all = int(K / SBK);
+  {
+    // ---- split-K: this split's range, its partial, the arrival ------------------
+    constexpr int kChunks = S::kMB * S::kNB * 4;  // f32x4 chunks of a thread's accumulators
+    const int ns = sp.ksplit;
+    auto range_of = [&](int sidx, int& kt0, int& nk) {
+      kt0 = int((int64_t(sidx) * nkt_all) / ns);
+      nk = int((int64_t(sidx + 1) * nkt_all) / ns) - kt0;
+    };
+    // chunk c of this thread in split sidx's partial: 16-byte stores / loads,
+    // 1 KB contiguous per wave instruction
+    auto part_at = [&](int sidx, int c) {
+      return reinterpret_cast<f32x4_t*>(sp.part) + ((int64_t(tile) * ns + sidx) * kChunks + c) * S::kThreads + tid;
+    };
+    // skip: units whose rows this workgroup finishes itself (not written)
+    auto publish = [&](int sidx, uint32_t skip) {
+#pragma unroll
+      for (int mb = 0; mb < S::kMB; ++mb)
+        if (!((skip >> (wm * S::kMB + mb)) & 1u))
+#pragma unroll
+        for (int nb = 0; nb < S::kNB; ++nb)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *part_at(sidx, (mb * S::kNB + nb) * 4 + q) =
+                f32x4_t{acc[mb][nb][4 * q], acc[mb][nb][4 * q + 1], acc[mb][nb][4 * q + 2], acc[mb][nb][4 * q + 3]};
+    };
+    // ---- this split's range and partial, then the arrival --------------------------
+    // The tile's rows form U = WM * MB units of 32 (unit u: rows [32u, 32u+32),
+    // held by waves wm = u / MB in accumulator block mb = u % MB).  Split s
+    // finishes units [s*U/ns, (s+1)*U/ns) once every split has arrived, reading
+    // only those rows of the ns partials.  Arrival word: bits 0-7 count the
+    // splits, bits 8-23 mark splits whose wait ran out (their units go to the last
+    // arrival), bits 24-31 count splits that ran on an unexpected XCD (then the
+    // last arrival recomputes the whole tile and the others leave).  The
+    // recomputation reuses the one main loop below (a second inlined copy of it
+    // would spill).
+    constexpr int U = WM * S::kMB;
+    uint32_t* arrive_word = sp.counters + tile;
+    uint32_t* exit_word = sp.counters + kSplitExitOffset + tile;
+    __shared__ uint32_t seen_word;
+    // Every split leaves through here once it no longer reads the arrival word;
+    // the last to leave re-arms both words for the next launch.
+    auto leave = [&]() {
+      if (tid == 0 && __hip_atomic_fetch_add(exit_word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u ==
+                          uint32_t(ns)) {
+        __hip_atomic_store(arrive_word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(exit_word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    };
+    auto arrived = [&](uint32_t w_) { return (w_ & 0xFFu) == uint32_t(ns); };
+    auto units_of = [&](int sidx) {
+      const int u0 = sidx * U / ns, u1 = (sidx + 1) * U / ns;
+      return u1 > u0 ? ((1u << u1) - 1u) & ~((1u << u0) - 1u) : 0u;
+    };
+    uint32_t units = 0;
+    bool recompute = false;
+    int sidx = split;
+#pragma unroll 1
+    for (;;) {
+      int kt0, nk;
+      range_of(sidx, kt0, nk);
+      run_range(kt0, nk);
+      publish(sidx, recompute ? 0u : units_of(split));
+      __builtin_amdgcn_s_waitcnt(0);  // this thread's partial has reached the L2
+      if (recompute) {
+        if (++sidx < ns) continue;
+        units = (1u << U) - 1u;
+        break;
+      }
+      __syncthreads();  // ... and every thread's
+      const uint32_t inc = 1u + (foreign ? kSplitForeign : 0u);
+      if (tid == 0)
+        seen_word = __hip_atomic_fetch_add(arrive_word, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
+      __syncthreads();
+      uint32_t v = seen_word;
+      units = units_of(split);
+      if (!arrived(v)) {
+        if (units == 0) {  // nothing of this tile to finish here
+          leave();
+          return;
+        }
+        if (tid == 0) {
+          // bounded wait for the other splits (they are normally resident and close)
+          for (int spin = 0; !arrived(v) && spin < sp.max_spins; ++spin) {
+            __builtin_amdgcn_s_sleep(2);
+            v = __hip_atomic_load(arrive_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          seen_word = v;
+        }
+        __syncthreads();
+        v = seen_word;
+        if (!arrived(v)) {
+          // hand this split's units to the last arrival: publish their rows too, then
+          // mark the hand-off (unless the last split arrived meanwhile)
+          publish(split, ~units);
+          __builtin_amdgcn_s_waitcnt(0);
+          __syncthreads();
+          if (tid == 0)
+            seen_word = __hip_atomic_fetch_or(arrive_word, 1u << (8 + split), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __syncthreads();
+          v = seen_word;
+        }
+        if (!arrived(v) || (v >> 24) != 0) {  // handed off, or the last arrival recomputes
+          leave();
+          return;
+        }
+        break;
+      }
+      if ((v >> 24) != 0) {
+        // A split ran on another XCD, so its partial may not be visible through
+        // this L2: recompute every split here and publish each into this L2.
+        if (tid == 0)
+          __hip_atomic_fetch_add(sp.counters + kDecodeRecomputeWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        recompute = true;
+        sidx = 0;
+        continue;
+      }
+      for (int s2 = 0; s2 < ns; ++s2)
+        if ((v >> (8 + s2)) & 1u) units |= units_of(s2);  // splits that handed off
+      break;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // Sum the finished units' rows in split order; each wave reads only its own
+    // fragment chunks.  This split's own rows come from its registers (it did not
+    // publish them), except on the recompute path, where every split was published.
+    const int mine = recompute ? -1 : split;
+    const uint32_t own_units = recompute ? 0u : units_of(split);
+    constexpr int kG = S::kNB <= 3 ? S::kNB : 1;  // accumulator blocks summed per group (registers)
+#pragma unroll
+    for (int mb = 0; mb < S::kMB; ++mb) {
+      if (!((units >> (wm * S::kMB + mb)) & 1u)) continue;
+      const bool own_rows = (own_units >> (wm * S::kMB + mb)) & 1u;
+#pragma unroll
+      for (int nb0 = 0; nb0 < S::kNB; nb0 += kG) {
+        f32x4_t v4[kG * 4];
+#pragma unroll 1
+        for (int sidx = 0; sidx < ns; ++sidx) {
+          f32x4_t t4[kG * 4];
+          if (own_rows && sidx == mine) {
+#pragma unroll
+            for (int g = 0; g < kG; ++g)
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                t4[g * 4 + q] = f32x4_t{acc[mb][nb0 + g][4 * q], acc[mb][nb0 + g][4 * q + 1],
+                                        acc[mb][nb0 + g][4 * q + 2], acc[mb][nb0 + g][4 * q + 3]};
+          } else {
+#pragma unroll
+            for (int c = 0; c < kG * 4; ++c) t4[c] = *part_at(sidx, (mb * S::kNB + nb0) * 4 + c);
+          }
+#pragma unroll
+          for (int c = 0; c < kG * 4; ++c) v4[c] = sidx == 0 ? t4[c] : v4[c] + t4[c];
+        }
+#pragma unroll
+        for (int g = 0; g < kG; ++g)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x4_t u4 = v4[g * 4 + q];
+            acc[mb][nb0 + g][4 * q] = u4.x; acc[mb][nb0 + g][4 * q + 1] = u4.y;
+            acc[mb][nb0 + g][4 * q + 2] = u4.z; acc[mb][nb0 + g][4 * q + 3] = u4.w;
+          }
+      }
+    }
+    leave();
+    tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, cslot, ht, m0, p, e, smem, units);
+  }
+}
+
 template <int BM, int NH, int WM, int WN, int NS, int SBK = 32>
 hipError_t launch_dma(const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e, int group_m,
                       hipStream_t stream) {
@@ -448,6 +796,36 @@ hipError_t launch_dma(const ProblemArgs& p, const WeightArgs& w, const EpilogueA
   if (S::kLdsBytes + dyn > 160 * 1024) return hipErrorInvalidValue;
   hipLaunchKernelGGL((tile_dma_kernel<BM, NH, WM, WN, NS, SBK>), dim3(blocks), dim3(S::kThreads), dyn, stream, p, w, e,
                      group_m < 1 ? 1 : group_m);
+  return hipGetLastError();
+}
+
+template <int BM, int NH, int WM, int WN, int NS, int SBK>
+size_t split_part_bytes(int64_t M, int n_tiles, int ksplit) {
+  using S = DmaShape<BM, NH, WM, WN, NS, SBK>;
+  const int64_t tiles = (M + BM - 1) / BM * (n_tiles / NH);
+  return size_t(tiles) * ksplit * S::kMB * S::kNB * 4 * S::kThreads * 16;
+}
+
+template <int BM, int NH, int WM, int WN, int NS, int SBK>
+hipError_t launch_dma_split(const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e, int ksplit,
+                            int force_recompute, int max_spins, void* workspace, hipStream_t stream) {
+  using S = DmaShape<BM, NH, WM, WN, NS, SBK>;
+  const int n_mt = int((p.M + BM - 1) / BM);
+  const int tiles = n_mt * (p.n_tiles / NH);
+  const int X = p.xcds > 0 ? p.xcds : 1;
+  const int tpx = (tiles + X - 1) / X;
+  const size_t dyn = p.in_gamma ? size_t(p.K) * 2 : 0;
+  if (S::kLdsBytes + dyn > 160 * 1024 || ksplit < 2 || ksplit > 16 || tiles > kSplitExitOffset ||
+      p.K / SBK < ksplit)
+    return hipErrorInvalidValue;
+  TileSplit sp;
+  sp.ksplit = ksplit;
+  sp.ctl = force_recompute ? 1 : 0;
+  sp.max_spins = max_spins;
+  sp.counters = static_cast<uint32_t*>(workspace);
+  sp.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kDecodeCounterBytes);
+  hipLaunchKernelGGL((tile_dma_split_kernel<BM, NH, WM, WN, NS, SBK>), dim3(X * ksplit * tpx), dim3(S::kThreads),
+                     dyn, stream, p, w, e, sp);
   return hipGetLastError();
 }
 
@@ -731,6 +1109,25 @@ int tile_dma_lds_bytes(int id) {
     case 30: return W4Shape<128, 3, 2, 4, 4>::kLdsBytes;
     case 31: return W4Shape<256, 2, 2, 4, 3>::kLdsBytes;
     case 32: return W4Shape<128, 2, 2, 2, 4>::kLdsBytes;
+    default: return 0;
+  }
+}
+
+hipError_t launch_tile_dma_split(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
+                                 int ksplit, int force_recompute, int max_spins, void* workspace, hipStream_t stream) {
+  switch (id) {
+    case 16:
+      return launch_dma_split<128, 3, 2, 4, 2, 64>(p, w, e, ksplit, force_recompute, max_spins, workspace, stream);
+    case 18:
+      return launch_dma_split<256, 2, 2, 4, 2, 64>(p, w, e, ksplit, force_recompute, max_spins, workspace, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+size_t tile_split_part_bytes(int id, int64_t M, int n_tiles, int ksplit) {
+  switch (id) {
+    case 16: return split_part_bytes<128, 3, 2, 4, 2, 64>(M, n_tiles, ksplit);
+    case 18: return split_part_bytes<256, 2, 2, 4, 2, 64>(M, n_tiles, ksplit);
     default: return 0;
   }
 }

@@ -126,14 +126,35 @@ def test_workspace_size(lib):
     # 64 < T: one decode launch covers every 64-row block; each block has its own
     # partials, so four blocks need four times the partial region
     assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == C + 4 * (n - C)
-    _native.set_option("decode_passes", 1)
-    try:  # one block per launch: the launches share one block's region
-        assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == n
+    _native.set_option("tile_ksplit", 0)  # decode blocks or the one-workgroup-per-tile launch only
+    try:
+        _native.set_option("decode_passes", 1)
+        try:  # one block per launch: the launches share one block's region
+            assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == n
+        finally:
+            _native.set_option("decode_passes", 16)
+        _native.set_option("decode_blocks", 0)
+        try:
+            assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == 0
+        finally:
+            _native.set_option("decode_blocks", 16)
     finally:
-        _native.set_option("decode_passes", 16)
+        _native.set_option("tile_ksplit", 1)
+    # Without decode blocks, bf16 T = 200 (2 x 16 tiles of 128 x 384) runs as a
+    # split-K tile launch of 4 splits (the planner's model: 4 beats 2 and 3): the
+    # counters, then one fp32 partial of a tile per (tile, split); int4 takes the
+    # tile kernel, which needs none.
     _native.set_option("decode_blocks", 0)
     try:
-        assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == 0
+        assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == C + 32 * 4 * 128 * 384 * 4
+        _native.set_option("tile_ksplit", 2)  # a forced split count
+        try:
+            assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == C + 32 * 2 * 128 * 384 * 4
+        finally:
+            _native.set_option("tile_ksplit", 1)
+        # 40 heads (no 3-head tiling): 1 x 20 tiles of 256 x 256; at hidden 2048 (32
+        # stages) the model's best split count is 5 (15 + 32/s * 1.3 + 1.47 * s us)
+        assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 4, 2048) == C + 20 * 5 * 256 * 256 * 4
     finally:
         _native.set_option("decode_blocks", 16)
 
@@ -141,10 +162,11 @@ def test_workspace_size(lib):
 def test_decode_block_crossovers(lib):
     """The plan's cost model reproduces the crossovers measured on MI355X at hidden
     4096 (Qwen3-8B heads): a workspace is needed exactly when decode launches run.
-    bf16 runs as decode blocks up to T = 832 (768 tokens: 73 us against 85 us for
-    the tile kernel; 896: 86 against 84), int4 up to T = 1024 (92 us against 138),
-    and beyond sixteen blocks (T > 1024) both run the tile kernel.  One launch
-    covers every block, each with its own partials."""
+    int4 runs as decode blocks up to T = 1024 (92 us against 138 for the tile
+    kernel), and beyond sixteen blocks (T > 1024) it runs the tile kernel.  One
+    launch covers every block, each with its own partials.  (bf16 takes the
+    split-K tile launch from T ~ 400, whose partials are smaller; the size is the
+    larger of the two formats' needs.)"""
     from mqk import _native
     size = lambda T: lib.mqk_fused_qkv_rope_workspace_size(T, 32, 8, 4096)
     C = 4096 + 256  # per-head arrival counters + the statistics line
@@ -153,10 +175,12 @@ def test_decode_block_crossovers(lib):
         assert size(T) == C + (T // 64) * one, T
     assert size(1088) == 0
     _native.set_option("decode_passes", 4)
+    _native.set_option("tile_ksplit", 0)  # (bf16's split-K partials at T = 1024 exceed four blocks')
     try:  # at most four blocks per launch: the launches reuse four blocks' partials
         assert size(1024) == C + 4 * one
     finally:
         _native.set_option("decode_passes", 16)
+        _native.set_option("tile_ksplit", 1)
 
 
 def test_w4a16_validation(lib):
