@@ -2,7 +2,7 @@
 """Benchmark of the fused QKV + QK-Norm + RoPE op on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
-    python bench.py --only {c2,c3,c4,c5,mid,copy} --steps K   # one workload, for profiler runs
+    python bench.py --only {c2,c3,c4,c5,mid,mid256,gemm,copy} --steps K   # one workload, for profiler runs
 
 Headline (``value``): BASELINE config 2, Qwen3-8B prefill B=4 x S=512 (2048
 tokens, hidden 4096, 32 Q heads, 8 KV heads, head_dim 128, bf16), tokens/s of
@@ -284,7 +284,7 @@ def copy_kernel(nbytes, steps, dev):
     torch.cuda.synchronize()
 
 
-WORKLOADS = ("c2", "c3", "c4", "c5", "mid", "gemm", "copy")
+WORKLOADS = ("c2", "c3", "c4", "c5", "mid", "mid256", "gemm", "copy")
 
 
 def run_only(name, steps, warmup, dev):
@@ -298,8 +298,10 @@ def run_only(name, steps, warmup, dev):
         ms, _ = bench_prefill(8192, 1, 8192, 2048, 32, 4, 3, steps, warmup, dev)
     elif name == "c5":
         ms, _ = bench_w4a16(hidden, Hq, Hkv, 4, steps, warmup, dev)
-    elif name == "mid":  # a 512-token call: one decode launch covering eight 64-row blocks
+    elif name == "mid":  # a 512-token call (random positions): the split-K tile launch
         ms, _ = bench_decode(512, hidden, Hq, Hkv, 2, steps, warmup, dev)
+    elif name == "mid256":  # a 256-token call: one decode launch covering four 64-row blocks
+        ms, _ = bench_decode(256, hidden, Hq, Hkv, 2, steps, warmup, dev)
     elif name == "gemm":  # the W4A16 GEMM decode shapes, M = 1 / 4 / 8 / 16
         ms = {m: v[0] * 1e-3 for m, v in bench_w4a16_gemm_decode(steps, warmup, dev).items()}
     else:
@@ -388,6 +390,15 @@ def main(argv=None) -> int:
                                         "ms_per_step": round(ms4, 6), "bound": "mfma", "achieved_TFLOPs": round(a4, 2),
                                         "frac": round(a4 / PEAK_BF16_TFLOPS, 4)}
         log(f"[bench] config 4: {ms4 * 1e3:.1f} us/step, {a4:.0f} TFLOP/s")
+        # mid token counts: Qwen3-8B prefill of B=1 x S=512 (the reference's smallest
+        # published (B, S) point, docs/02_fused_qkv_rope.md:69-81, there at 0.6B shapes
+        # with paged attention included, so not comparable): the split-K tile launch
+        msm, _ = bench_prefill(512, 1, 512, hidden, Hq, Hkv, 5, max(100, args.steps), 200, dev)
+        am = flops(512, hidden, N) / (msm * 1e-3) / 1e12
+        sec["mid_qwen3_8b_b1_s512"] = {"tokens_per_s": round(512 / (msm * 1e-3), 1),
+                                       "ms_per_step": round(msm, 6), "bound": "mfma", "achieved_TFLOPs": round(am, 2),
+                                       "frac": round(am / PEAK_BF16_TFLOPS, 4)}
+        log(f"[bench] B=1 x S=512: {msm * 1e3:.1f} us/step, {am:.0f} TFLOP/s")
         # config 5: W4A16 ragged continuous batch
         ms5, T5 = bench_w4a16(hidden, Hq, Hkv, 4, 100, 100, dev)
         a5 = flops(T5, hidden, N) / (ms5 * 1e-3) / 1e12

@@ -307,14 +307,22 @@ int mqk_fused_qkv_rope_ex_w4a16(const mqk_bf16* x, const int32_t* qw_q, const vo
  *   "decode_max_spins"  polls (~64 ns apart) a decode launch of several blocks makes while
  *                    a block's designated finisher waits for its last splits, before it
  *                    hands the block to the last split to arrive (default 16384, ~1 ms;
- *                    0 hands off at once; for tests of the hand-off)
- *   "decode_force_recompute"  1: the decode kernel takes its recompute path (used when a
- *                    split ran on an unexpected XCD) for every head; for tests
+ *                    0 hands off at once; for tests of the hand-off).  The split-K tile
+ *                    launch bounds each split's wait for the others the same way.
+ *   "decode_force_recompute"  1: the decode kernel and the split-K tile launch take their
+ *                    recompute path (used when a split ran on an unexpected XCD) for every
+ *                    head / tile; for tests
+ *   "tile_ksplit"    bf16 calls with fewer tiles than CUs (64 < T up to ~1000 tokens at
+ *                    hidden 4096): 1 (default) = a split-K tile launch (each tile's K range
+ *                    over several workgroups of one XCD, fp32 partials in the workspace)
+ *                    where a cost model prefers it to the decode blocks and the plain tile
+ *                    launch; 0 = never; 2..16 = that split count whenever a split launch fits
  * Returns MQK_OK or MQK_ERR_BAD_OPTION.  mqk_get_option also reads "device_cus" and
  * "device_xcds": the compute units and XCDs of the current device, as the planner and
  * the decode kernel's grid use them (hipDeviceGetAttribute; -1 for unknown names).
- * Heads the decode kernel finished on its recompute path are counted in the
- * first word after the per-head counters of the workspace (byte offset 4096).
+ * Heads the decode kernel (and tiles the split-K tile launch) finished on their
+ * recompute path are counted in the first word after the per-head counters of the
+ * workspace (byte offset 4096).
  */
 int mqk_set_option(const char* name, int64_t value);
 int64_t mqk_get_option(const char* name);
