@@ -40,6 +40,38 @@ def test_graph_replay_matches_eager(B, S, device):
         torch.cuda.synchronize()
 
 
+def test_graph_replay_split_tile(device):
+    """The split-K tile launch (a bf16 call of 512 tokens at hidden 4096) in a graph:
+    its arrival and exit words are re-armed by the launch itself, so replays, with
+    eager calls of the same and of another plan in between, stay bit-exact."""
+    import mqk
+    from conftest import launched_kernels
+    T = 512
+    case = Case(1, T, 4096, 32, 8, seed=997, rows=8192,
+                positions=torch.randint(0, 8192, (T,), generator=torch.Generator().manual_seed(4), dtype=torch.int32))
+    args = case.args(device)
+    small = Case(1, 64, 4096, 32, 8, seed=998, rows=8192,
+                 positions=torch.arange(64, dtype=torch.int32)).args(device)
+    assert launched_kernels(lambda: mqk.fused_qkv_rope(*args)) == ["tile_split"]
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        eager = mqk.fused_qkv_rope(*args)  # also sizes the stream's workspace
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = mqk.fused_qkv_rope(*args)
+    for rep in range(4):
+        for t in out:
+            t.fill_(0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(out, eager)), f"replay {rep}"
+        with torch.cuda.stream(stream):  # eager work on the graph's stream (same workspace)
+            mqk.fused_qkv_rope(*small)
+            mqk.fused_qkv_rope(*args)
+        torch.cuda.synchronize()
+
+
 def test_graph_replay_new_inputs(device):
     """Replays read the captured input buffers: new values copied in give new outputs."""
     import mqk
