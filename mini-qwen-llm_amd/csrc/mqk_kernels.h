@@ -111,7 +111,7 @@ hipError_t launch_tile_dma(int id, const ProblemArgs& p, const WeightArgs& w, co
 hipError_t launch_tile_dma_split(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                                  int ksplit, int force_recompute, int max_spins, void* workspace, hipStream_t stream);
 size_t tile_split_part_bytes(int id, int64_t M, int n_tiles, int ksplit);
-// int4-weight (W4A16) variant of the pipelined kernel, ids 30-32.
+// int4-weight (W4A16) variant of the pipelined kernel, ids 30-33.
 hipError_t launch_tile_dma_w4(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                               int group_m, hipStream_t stream);
 

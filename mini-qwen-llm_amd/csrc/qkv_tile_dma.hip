@@ -165,6 +165,7 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
   constexpr int kTN = NH * kHeadDim / WN;
   constexpr int kRowStep = THREADS / 8;
   constexpr int kPasses = BM / kRowStep;
+  static_assert(BM % kRowStep == 0, "the epilogue's row passes must cover the tile");
   // gamma / cos / sin depend only on the token: with few rows per thread they are
   // loaded once for all NH heads of the tile (16 VGPRs per row)
   constexpr bool kPreload = kPasses <= 4;
@@ -1109,6 +1110,7 @@ int tile_dma_lds_bytes(int id) {
     case 30: return W4Shape<128, 3, 2, 4, 4>::kLdsBytes;
     case 31: return W4Shape<256, 2, 2, 4, 3>::kLdsBytes;
     case 32: return W4Shape<128, 2, 2, 2, 4>::kLdsBytes;
+    case 33: return W4Shape<256, 2, 1, 8, 3>::kLdsBytes;
     default: return 0;
   }
 }
@@ -1138,6 +1140,7 @@ hipError_t launch_tile_dma_w4(int id, const ProblemArgs& p, const WeightArgs& w,
     case 30: return launch_dma_w4<128, 3, 2, 4, 4>(p, w, e, group_m, stream);  // 128x384, 4 stages
     case 31: return launch_dma_w4<256, 2, 2, 4, 3>(p, w, e, group_m, stream);  // 256x256, 3 stages
     case 32: return launch_dma_w4<128, 2, 2, 2, 4>(p, w, e, group_m, stream);  // 128x256, 4 waves
+    case 33: return launch_dma_w4<256, 2, 1, 8, 3>(p, w, e, group_m, stream);  // 256x256, 256x32 waves
     default: return hipErrorInvalidValue;
   }
 }

@@ -112,7 +112,7 @@ def test_input_norm_decode_recompute_path(device):
     _check_normed_copy(v1[0], case.x[0], gam.cpu(), ks)
 
 
-@pytest.mark.parametrize("S,tile", [(1, 0), (16, 0), (300, 0), (300, 4), (300, 31), (300, 32)])
+@pytest.mark.parametrize("S,tile", [(1, 0), (16, 0), (300, 0), (300, 4), (300, 31), (300, 32), (300, 33)])
 def test_input_norm_w4a16(S, tile, device):
     import mqk
     hidden, Hq, Hkv, B = 512, 4, 2, 3

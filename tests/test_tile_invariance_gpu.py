@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 
 D = HEAD_DIM
 BF16_DMA_VARIANTS = [10, 11, 12, 13, 14, 15, 16, 17, 18]
-INT4_DMA_VARIANTS = [30, 31, 32]
+INT4_DMA_VARIANTS = [30, 31, 32, 33]
 
 
 def _with_variant(variant, fn):

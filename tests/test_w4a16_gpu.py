@@ -422,7 +422,7 @@ def test_qk_norm_rope_matches_fused(device):
     assert (ko.float() - kf.float()).abs().max().item() <= 4e-2
 
 
-@pytest.mark.parametrize("variant", [1, 2, 3, 4, 30, 31, 32])
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 30, 31, 32, 33])
 @pytest.mark.parametrize("scale_dtype", [torch.bfloat16, torch.float16])
 def test_fused_w4a16_tile_variants(variant, scale_dtype, device):
     """Every int4 tile variant on a ragged-length shape (T = 600: row tail), 24 heads,
