@@ -273,21 +273,24 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
         if (e.qkv) {
           const int H = proj == 0 ? e.Hq : e.Hkv;
           uint16_t* base = proj == 0 ? e.q : (proj == 1 ? e.k : e.v);  // k / v may be null (cache only)
+          // (non-temporal: the tile's rows are written once and read by a later
+          // kernel, so they need not stay in this XCD's L2; measured ~2 % faster)
           if (base) {
             uint16_t* dst = base + (t * H + hh) * kHeadDim;
-            *reinterpret_cast<u32x4_t*>(dst + 8 * c8) = o1;
-            *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8) = o2;
+            __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(dst + 8 * c8));
+            __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8));
           }
           if (proj != 0 && cslot[q] >= 0) {
             uint16_t* crow = paged_row(e, cslot[q], proj, hh);
-            *reinterpret_cast<u32x4_t*>(crow + 8 * c8) = o1;
-            *reinterpret_cast<u32x4_t*>(crow + kHalfDim + 8 * c8) = o2;
+            __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(crow + 8 * c8));
+            __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(crow + kHalfDim + 8 * c8));
           }
         } else {
           const int64_t col0 = int64_t(head) * kHeadDim;  // plain GEMM output [M, N]
           uint16_t* dst = e.out + t * e.N + col0;
-          if (col0 + 8 * c8 + 8 <= e.N) *reinterpret_cast<u32x4_t*>(dst + 8 * c8) = o1;
-          if (col0 + kHalfDim + 8 * c8 + 8 <= e.N) *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8) = o2;
+          if (col0 + 8 * c8 + 8 <= e.N) __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(dst + 8 * c8));
+          if (col0 + kHalfDim + 8 * c8 + 8 <= e.N)
+            __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8));
         }
       }
     }
