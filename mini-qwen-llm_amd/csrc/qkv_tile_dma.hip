@@ -480,7 +480,7 @@ tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp)
   const int wm = wave % WM;
   const int wn = wave / WM;
 
-  // ---- tile coordinates: XCD-contiguous ids, grouped along M ------------------
+  // ---- tile and split of this workgroup ----------------------------------------
   const int n_mt = int((p.M + BM - 1) / BM);
   const int n_ht = p.n_tiles / NH;
   int mt, ht, split = 0, tile = 0;
@@ -578,54 +578,53 @@ tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp)
   const int khalf = lane >> 5;
   auto run_range = [&](int kt0, int nkt) {
 #pragma unroll
-  for (int mb = 0; mb < S::kMB; ++mb)
+    for (int mb = 0; mb < S::kMB; ++mb)
 #pragma unroll
-    for (int nb = 0; nb < S::kNB; ++nb) acc[mb][nb] = f32x16_t{};
+      for (int nb = 0; nb < S::kNB; ++nb) acc[mb][nb] = f32x16_t{};
 #pragma unroll
-  for (int s = 0; s < NS - 1; ++s)
-    if (s < nkt) issue(kt0, s);
+    for (int s = 0; s < NS - 1; ++s)
+      if (s < nkt) issue(kt0, s);
 
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int ahead = min(NS - 2, nkt - 1 - kt);  // stages already issued after kt
-    wait_stage<NS, S::kLoadsPerWave>(ahead);
-    if (in_norm) {  // this wave's x chunks of stage kt have landed: normalise them in place
+    for (int kt = 0; kt < nkt; ++kt) {
+      const int ahead = min(NS - 2, nkt - 1 - kt);  // stages already issued after kt
+      wait_stage<NS, S::kLoadsPerWave>(ahead);
+      if (in_norm) {  // this wave's x chunks of stage kt have landed: normalise them in place
 #pragma unroll
-      for (int i = 0; i < S::kALoads; ++i)
-        norm_chunk(smem + (kt % NS) * S::kStageBytes + dst_off[i] + lane * 16,
-                   int64_t(kt0 + kt) * SBK + a_koff[i], a_scale[i]);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    }
-    barrier();
-    if (kt + NS - 1 < nkt) issue(kt0, kt + NS - 1);
-    const unsigned char* st = smem + (kt % NS) * S::kStageBytes;
-#pragma unroll
-    for (int ks = 0; ks < SBK / 16; ++ks) {
-      const int chunk = 2 * ks + khalf;
-      u32x4_t af[S::kMB], bf[S::kNB];
-#pragma unroll
-      for (int mb = 0; mb < S::kMB; ++mb) {
-        const int row = wm * S::kTM + mb * 32 + c32;
-        af[mb] = *reinterpret_cast<const u32x4_t*>(st + row * kRowBytes + stage_slot<SBK>(row, chunk) * 16);
+        for (int i = 0; i < S::kALoads; ++i)
+          norm_chunk(smem + (kt % NS) * S::kStageBytes + dst_off[i] + lane * 16,
+                     int64_t(kt0 + kt) * SBK + a_koff[i], a_scale[i]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       }
+      barrier();
+      if (kt + NS - 1 < nkt) issue(kt0, kt + NS - 1);
+      const unsigned char* st = smem + (kt % NS) * S::kStageBytes;
 #pragma unroll
-      for (int nb = 0; nb < S::kNB; ++nb) {
-        const int row = BM + wn * S::kTN + nb * 32 + c32;
-        bf[nb] = *reinterpret_cast<const u32x4_t*>(st + row * kRowBytes + stage_slot<SBK>(row, chunk) * 16);
-      }
+      for (int ks = 0; ks < SBK / 16; ++ks) {
+        const int chunk = 2 * ks + khalf;
+        u32x4_t af[S::kMB], bf[S::kNB];
 #pragma unroll
-      for (int mb = 0; mb < S::kMB; ++mb)
+        for (int mb = 0; mb < S::kMB; ++mb) {
+          const int row = wm * S::kTM + mb * 32 + c32;
+          af[mb] = *reinterpret_cast<const u32x4_t*>(st + row * kRowBytes + stage_slot<SBK>(row, chunk) * 16);
+        }
 #pragma unroll
         for (int nb = 0; nb < S::kNB; ++nb) {
-          acc[mb][nb] = mfma_32x32x16(af[mb], bf[nb], acc[mb][nb]);
+          const int row = BM + wn * S::kTN + nb * 32 + c32;
+          bf[nb] = *reinterpret_cast<const u32x4_t*>(st + row * kRowBytes + stage_slot<SBK>(row, chunk) * 16);
         }
+#pragma unroll
+        for (int mb = 0; mb < S::kMB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < S::kNB; ++nb) {
+            acc[mb][nb] = mfma_32x32x16(af[mb], bf[nb], acc[mb][nb]);
+          }
+      }
     }
-  }
-  barrier();  // every wave is done with the ring; the epilogue (or the next range) reuses the LDS
+    barrier();  // every wave is done with the ring; the epilogue (or the next range) reuses the LDS
   };
 
   const int nkt_all = int(K / SBK);
-  {
-    // ---- split-K: this split's range, its partial, the arrival ------------------
+  {  // ---- split-K: this split's range, its partial, the arrival, the finish ----
     constexpr int kChunks = S::kMB * S::kNB * 4;  // f32x4 chunks of a thread's accumulators
     const int ns = sp.ksplit;
     auto range_of = [&](int sidx, int& kt0, int& nk) {
