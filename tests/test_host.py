@@ -159,6 +159,28 @@ def test_workspace_size(lib):
         _native.set_option("decode_blocks", 16)
 
 
+def test_split_tile_plan(lib):
+    """The planner's split-K tile model at Qwen3-8B dims (bf16 needs the split
+    workspace; int4 keeps its decode blocks, so the size is the larger need):
+    512 tokens as 4 x 16 tiles of 128 x 384 in 4 splits, 1024 tokens as 8 x 16
+    tiles in 2 splits; both fit the CUs once (tiles x splits <= 256)."""
+    from mqk import _native
+    C = 4096 + 256
+    part = 128 * 384 * 4  # one tile's fp32 partial
+    _native.set_option("decode_blocks", 0)  # int4 then takes its tile kernel: no workspace
+    try:
+        assert lib.mqk_fused_qkv_rope_workspace_size(512, 32, 8, 4096) == C + 64 * 4 * part
+        assert lib.mqk_fused_qkv_rope_workspace_size(1024, 32, 8, 4096) == C + 128 * 2 * part
+        assert lib.mqk_fused_qkv_rope_workspace_size(2048, 32, 8, 4096) == 0  # 256 tiles: one each
+        _native.set_option("tile_ksplit", 0)
+        try:
+            assert lib.mqk_fused_qkv_rope_workspace_size(512, 32, 8, 4096) == 0
+        finally:
+            _native.set_option("tile_ksplit", 1)
+    finally:
+        _native.set_option("decode_blocks", 16)
+
+
 def test_decode_block_crossovers(lib):
     """The plan's cost model reproduces the crossovers measured on MI355X at hidden
     4096 (Qwen3-8B heads): a workspace is needed exactly when decode launches run.

@@ -5,7 +5,8 @@ same way (tests/test_fused_qkv_rope.py:287-311; 33 unfused against 6 fused,
 docs/02_fused_qkv_rope.md:65-67).  Here the whole front is one launch in the
 common cases; a split-off tail adds a decode launch, the fused input RMSNorm
 adds its pre-pass, and mid token counts run as one decode launch covering all
-their 64-row blocks ("decode_multi").  Each case names the plan it expects, so
+their 64-row blocks ("decode_multi") or as one split-K tile launch
+("tile_split").  Each case names the plan it expects, so
 a change of the planner shows up here as well as in the timings.
 """
 from __future__ import annotations
@@ -49,6 +50,16 @@ def test_mid_t_decode_block_launches(T, plan, device):
         assert launched_kernels(_bf16_call(case, device)) == plan
     finally:
         mqk.set_option("decode_cost_model", 1)
+
+
+@pytest.mark.parametrize("T,plan", [(128, ["decode_multi"]), (256, ["decode_multi"]), (512, ["tile_split"]),
+                                    (1024, ["tile_split"]), (2048, ["tile"])])
+def test_default_plan_by_token_count(T, plan, device):
+    """The default planner at hidden 4096 (bf16): decode blocks for a few 64-row
+    blocks, the split-K tile launch from about 400 tokens while tiles are fewer
+    than CUs, one tile per workgroup once the tiles fill the CUs."""
+    case = Case(1, T, HID, HQ, HKV, seed=15 + T)
+    assert launched_kernels(_bf16_call(case, device)) == plan
 
 
 def test_tail_split_adds_one_decode_launch(device):
