@@ -151,10 +151,10 @@ struct Plan {
 // Split-K tile launch for problems with fewer tiles than CUs (bf16 weights):
 // variant 16 (128 x 384) when the heads tile by 3, else 18 (256 x 256).  Returns
 // the split count (0: none fits) and its modelled kernel time, fitted on MI355X
-// (hidden 1024 / 2048 / 4096, T = 129 .. 1024, 2 to 6 splits; within ~2 us):
-// ~15 us of launch, waits and epilogue, ~1.24 us per 64-k stage of a split, and
-// ~0.28 us per MB of fp32 partials published and read back.  At most one split
-// per 32-row unit of a tile (more would leave splits with no rows to finish).
+// (hidden 4096, T = 129 .. 1024, 2 to 8 splits; within ~1.5 us): ~9.5 us of
+// launch and waits, ~1.13 us per 64-k stage of a split, ~0.24 us per MB of fp32
+// partials published and read back, and ~5.2 us per 32-row unit of a tile that
+// one split finishes (the busiest split: ceil(units / splits)).
 int plan_tile_split(int64_t M, int64_t K, int n_tiles, const Topology& topo, const TileVariant*& v, double& us) {
   v = nullptr;
   us = 1e30;
@@ -169,14 +169,15 @@ int plan_tile_split(int64_t M, int64_t K, int n_tiles, const Topology& topo, con
   const int64_t X = topo.xcds;
   const int64_t slots = (tiles + X - 1) / X * X;  // tiles padded to whole XCD shares
   const int64_t nkt = K / 64;
-  const double stage_us = id == 16 ? 1.24 : 1.3;
+  const double stage_us = id == 16 ? 1.13 : 1.5;  // (256 x 256: 1.33x the MFMA work per stage)
   const double part_mb = (id == 16 ? 196608.0 : 262144.0) * 1e-6;  // one workgroup's partial
   const int units = id == 16 ? 4 : 8;
   int best = 0;
-  const int lo = req >= 2 ? int(req) : 2, hi = req >= 2 ? int(req) : units;
+  const int lo = req >= 2 ? int(req) : 2, hi = req >= 2 ? int(req) : 8;
   for (int s = lo; s <= hi; ++s) {
-    if (slots * s > topo.cus || nkt < 4 * int64_t(s) || tiles > 512) break;
-    const double t = 15.0 + double(nkt) / s * stage_us + 0.28 * part_mb * double(tiles) * s;
+    if (slots * s > topo.cus || nkt < 4 * int64_t(s) || tiles > kSplitMaxTiles) break;
+    const double t = 9.5 + double(nkt) / s * stage_us + 0.24 * part_mb * double(tiles) * s +
+                     5.2 * double((units + s - 1) / s);
     if (t < us) {
       us = t;
       best = s;
@@ -214,7 +215,8 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
   const double w_bytes = double(n_tiles) * kHeadDim * double(K) * (int4 ? 0.5 : 2.0);
   const double dec_us = int4 ? 4.0 + 3.0 * double(K) / 1024.0 : 8.0 + w_bytes / 5.0e6;
   const double pass_us = 0.5 + double(K) / 4096.0 * 4.5;
-  const double blocks_us = double(launches) * dec_us + double(nblk - launches) * pass_us;
+  // (+3 us for a launch of several blocks: T = 128 / 256 / 512 measured 25.6 / 39.3 / 56.9)
+  const double blocks_us = double(launches) * dec_us + double(nblk - launches) * pass_us + (nblk > 1 ? 3.0 : 0.0);
   const double tile_us = double(K) / 64.0 * (int4 ? 2.1 : 1.15) + 5.0;
   // split-K tile launch (bf16): taken when its model beats both the one-workgroup-
   // per-tile launch and the decode blocks

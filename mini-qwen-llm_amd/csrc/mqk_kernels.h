@@ -105,9 +105,9 @@ hipError_t launch_tile_dma(int id, const ProblemArgs& p, const WeightArgs& w, co
 // (max_spins polls) runs out hands its units to the last arrival.  If a split
 // ran on another XCD (or force_recompute), the last arrival recomputes every
 // split (same arithmetic, same order) and finishes the whole tile.  The
-// workspace: kDecodeCounterBytes of counters (zero; words [0, 512) and
-// [512, 1024) per tile, re-armed by the launch), then
-// tile_split_part_bytes(...) of partials.
+// workspace: kDecodeCounterBytes of counters (zero; the tile words at
+// kSplitWordsOffset, re-armed by the launch), then tile_split_part_bytes(...)
+// of partials.
 hipError_t launch_tile_dma_split(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                                  int ksplit, int force_recompute, int max_spins, void* workspace, hipStream_t stream);
 size_t tile_split_part_bytes(int id, int64_t M, int n_tiles, int ksplit);
@@ -133,9 +133,15 @@ size_t decode_workspace_bytes(int n_tiles, int splits, int blocks = 1);
 int decode_max_blocks(int n_tiles, int64_t K, int splits, bool int4_norm);
 // The decode kernel's counters open every workspace: one arrival counter per
 // head (kDecodeMaxHeads), then a statistics line whose first word counts the
-// heads finished on the recompute path (a split ran on an unexpected XCD).
+// heads finished on the recompute path (a split ran on an unexpected XCD), then
+// the split-K tile launch's words: one 128-byte line per tile (its arrival word,
+// then its exit word), so that the splits of different tiles never contend for
+// a line.
 constexpr int kDecodeMaxHeads = 1024;
-constexpr size_t kDecodeCounterBytes = size_t(kDecodeMaxHeads) * 4 + 256;
+constexpr size_t kSplitWordsOffset = size_t(kDecodeMaxHeads) * 4 + 256;
+constexpr int kSplitMaxTiles = 512;
+constexpr size_t kSplitLineBytes = 128;
+constexpr size_t kDecodeCounterBytes = kSplitWordsOffset + size_t(kSplitMaxTiles) * kSplitLineBytes;
 constexpr int kDecodeRecomputeWord = kDecodeMaxHeads;
 size_t decode_counter_bytes();
 // The split-K decode kernel on the launch's p.M rows: ceil(M / 64) <=

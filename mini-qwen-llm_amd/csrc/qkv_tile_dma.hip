@@ -298,6 +298,83 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
   }
 }
 
+// Norm, RoPE and 16-byte stores of 32 finished rows of a tile (rows t0 .. t0+31
+// of the call), held in LDS as fp32 [32][pitch] over the tile's NH heads: thread
+// -> (head j, row, c8) takes the column pairs [8c8, +8) / [64+8c8, +8) of one head
+// of one row, the same arithmetic as tile_epilogue.
+template <int NH, int THREADS>
+__device__ __forceinline__ void finish_unit_rows(const float* tile, int pitch, int64_t t0, int ht,
+                                                 const ProblemArgs& p, const EpilogueArgs& e) {
+  constexpr int kItems = 32 * NH * 8;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int it0 = 0; it0 < kItems; it0 += THREADS) {
+    const int it = it0 + tid;
+    if (kItems % THREADS != 0 && it >= kItems) break;  // (whole groups of 8 lanes leave together)
+    const int j = it / 256, rr = (it >> 3) & 31, c8 = it & 7;
+    const int64_t t = t0 + rr;
+    const int head = ht * NH + j;
+    int proj, hh;
+    split_head(head, e.Hq, e.Hkv, proj, hh);
+    const float* rowp = tile + rr * pitch + j * kHeadDim;
+    float lo[8], hi[8];
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const f32x4_t a = *reinterpret_cast<const f32x4_t*>(rowp + 8 * c8 + 4 * v);
+      const f32x4_t b = *reinterpret_cast<const f32x4_t*>(rowp + kHalfDim + 8 * c8 + 4 * v);
+      lo[4 * v] = a.x; lo[4 * v + 1] = a.y; lo[4 * v + 2] = a.z; lo[4 * v + 3] = a.w;
+      hi[4 * v] = b.x; hi[4 * v + 1] = b.y; hi[4 * v + 2] = b.z; hi[4 * v + 3] = b.w;
+    }
+    const bool valid = t < p.M;
+    if (e.qkv && proj != 2) {
+      const float ss = sum8_lanes(run_sumsq(lo, hi));
+      const float rms = head_rms(ss, e.eps);
+      const int64_t base = (valid ? rope_row(e, t) : 0) * kHeadDim;
+      u32x4_t c2[2], s2[2];
+      c2[0] = *reinterpret_cast<const u32x4_t*>(e.cos + base + 8 * c8);
+      c2[1] = *reinterpret_cast<const u32x4_t*>(e.cos + base + kHalfDim + 8 * c8);
+      s2[0] = *reinterpret_cast<const u32x4_t*>(e.sin + base + 8 * c8);
+      s2[1] = *reinterpret_cast<const u32x4_t*>(e.sin + base + kHalfDim + 8 * c8);
+      const uint16_t* gam = proj == 0 ? e.q_gamma : e.k_gamma;
+      const u32x4_t g0 = *reinterpret_cast<const u32x4_t*>(gam + 8 * c8);
+      const u32x4_t g1 = *reinterpret_cast<const u32x4_t*>(gam + kHalfDim + 8 * c8);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int wd = i >> 1, sh = (i & 1) * 16;
+        norm_rope_pair(lo[i], hi[i], rms, bf16_to_f32((g0[wd] >> sh) & 0xFFFFu),
+                       bf16_to_f32((g1[wd] >> sh) & 0xFFFFu), c2, s2, wd, sh);
+      }
+    }
+    if (!valid) continue;
+    u32x4_t o1, o2;
+    o1.x = pack_bf16x2(lo[0], lo[1]); o1.y = pack_bf16x2(lo[2], lo[3]);
+    o1.z = pack_bf16x2(lo[4], lo[5]); o1.w = pack_bf16x2(lo[6], lo[7]);
+    o2.x = pack_bf16x2(hi[0], hi[1]); o2.y = pack_bf16x2(hi[2], hi[3]);
+    o2.z = pack_bf16x2(hi[4], hi[5]); o2.w = pack_bf16x2(hi[6], hi[7]);
+    if (e.qkv) {
+      const int H = proj == 0 ? e.Hq : e.Hkv;
+      uint16_t* obase = proj == 0 ? e.q : (proj == 1 ? e.k : e.v);  // k / v may be null (cache only)
+      if (obase) {
+        uint16_t* dst = obase + (t * H + hh) * kHeadDim;
+        __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(dst + 8 * c8));
+        __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8));
+      }
+      const int64_t slot = proj != 0 ? paged_slot(e, t) : -1;
+      if (slot >= 0) {
+        uint16_t* crow = paged_row(e, slot, proj, hh);
+        __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(crow + 8 * c8));
+        __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(crow + kHalfDim + 8 * c8));
+      }
+    } else {
+      const int64_t col0 = int64_t(head) * kHeadDim;  // plain GEMM output [M, N]
+      uint16_t* dst = e.out + t * e.N + col0;
+      if (col0 + 8 * c8 + 8 <= e.N) __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(dst + 8 * c8));
+      if (col0 + kHalfDim + 8 * c8 + 8 <= e.N)
+        __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8));
+    }
+  }
+}
+
 // Split-K mode (SPLIT): kernel arguments of a launch_tile_dma_split launch.
 struct TileSplit {
   int ksplit;          // K ranges per tile
@@ -308,7 +385,6 @@ struct TileSplit {
 };
 
 constexpr uint32_t kSplitForeign = 1u << 24;  // arrival increment of a split on an unexpected XCD
-constexpr int kSplitExitOffset = 512;         // counters[512 + tile]: splits done with the arrival word (tiles < 512)
 
 __device__ __forceinline__ int hw_xcc_id() {
   return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11));  // hwreg(HW_REG_XCC_ID, 0, 4)
@@ -659,8 +735,9 @@ tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp)
     // recomputation reuses the one main loop below (a second inlined copy of it
     // would spill).
     constexpr int U = WM * S::kMB;
-    uint32_t* arrive_word = sp.counters + tile;
-    uint32_t* exit_word = sp.counters + kSplitExitOffset + tile;
+    uint32_t* arrive_word =
+        reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(sp.counters) + kSplitWordsOffset + tile * kSplitLineBytes);
+    uint32_t* exit_word = arrive_word + 1;
     __shared__ uint32_t seen_word;
     // Every split leaves through here once it no longer reads the arrival word;
     // the last to leave re-arms both words for the next launch.
@@ -744,48 +821,95 @@ tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp)
       break;
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    // Sum the finished units' rows in split order; each wave reads only its own
-    // fragment chunks.  This split's own rows come from its registers (it did not
-    // publish them), except on the recompute path, where every split was published.
+    leave();
+    // ---- finish the units: every thread sums a share of a unit's fragment chunks
+    // over the partials in split order into an LDS tile [32 rows][BN], then the
+    // unit's rows get norm, RoPE and 16-byte stores.  This split's own rows come
+    // from its registers through LDS (it did not publish them), except on the
+    // recompute path, where every split was published.
     const int mine = recompute ? -1 : split;
     const uint32_t own_units = recompute ? 0u : units_of(split);
-    constexpr int kG = S::kNB <= 3 ? S::kNB : 1;  // accumulator blocks summed per group (registers)
-#pragma unroll
-    for (int mb = 0; mb < S::kMB; ++mb) {
-      if (!((units >> (wm * S::kMB + mb)) & 1u)) continue;
-      const bool own_rows = (own_units >> (wm * S::kMB + mb)) & 1u;
-#pragma unroll
-      for (int nb0 = 0; nb0 < S::kNB; nb0 += kG) {
-        f32x4_t v4[kG * 4];
+    constexpr int kUC = S::kNB * 4;              // f32x4 chunks per thread of a unit's waves
+    constexpr int kUThreads = WN * 64;           // threads holding one unit (one wm)
+    constexpr int kItems = kUC * kUThreads;      // f32x4 chunks of a unit
+    static_assert(kItems % S::kThreads == 0, "unit chunks per thread");
+    constexpr int kPer = kItems / S::kThreads;
+    constexpr int kBatch = 2;                    // splits whose loads are in flight together (4 spill)
+    constexpr int kTPitch = BN + 4;              // fp32 pitch of the unit tile
+    f32x4_t* own_buf = reinterpret_cast<f32x4_t*>(smem);                  // [kUC][kUThreads]
+    float* utile = reinterpret_cast<float*>(smem + size_t(kItems) * 16);  // [32][kTPitch]
+    static_assert(size_t(kItems) * 16 + 32 * kTPitch * 4 <= size_t(S::kLdsBytes), "unit finish LDS");
+    // a unit chunk item -> (chunk c, thread r of the unit's waves)
+    auto item_src = [&](int it, int sidx) {
+      const int c = it / kUThreads, r = it % kUThreads;
+      return reinterpret_cast<const f32x4_t*>(sp.part) +
+             ((int64_t(tile) * ns + sidx) * kChunks + c) * S::kThreads + r;  // r is offset below
+    };
 #pragma unroll 1
-        for (int sidx = 0; sidx < ns; ++sidx) {
-          f32x4_t t4[kG * 4];
-          if (own_rows && sidx == mine) {
+    for (int u = 0; u < U; ++u) {
+      if (!((units >> u) & 1u)) continue;
+      const int uwm = u / S::kMB, umb = u % S::kMB;
+      const bool own = (own_units >> u) & 1u;
+      if (own && wm == uwm) {
 #pragma unroll
-            for (int g = 0; g < kG; ++g)
+        for (int mb = 0; mb < S::kMB; ++mb)  // (compile-time indices: acc stays in registers)
+          if (mb == umb)
+#pragma unroll
+            for (int nb = 0; nb < S::kNB; ++nb)
 #pragma unroll
               for (int q = 0; q < 4; ++q)
-                t4[g * 4 + q] = f32x4_t{acc[mb][nb0 + g][4 * q], acc[mb][nb0 + g][4 * q + 1],
-                                        acc[mb][nb0 + g][4 * q + 2], acc[mb][nb0 + g][4 * q + 3]};
-          } else {
+                own_buf[(nb * 4 + q) * kUThreads + wn * 64 + lane] =
+                    f32x4_t{acc[mb][nb][4 * q], acc[mb][nb][4 * q + 1], acc[mb][nb][4 * q + 2], acc[mb][nb][4 * q + 3]};
+      }
+      __syncthreads();
+      // the unit's threads sit at workgroup thread wn * 64 * WM ... : thread index of
+      // (wave wm = uwm, wn) lane L is (wn * WM + uwm) * 64 + L
+      f32x4_t v[kPer];
+#pragma unroll 1
+      for (int s0 = 0; s0 < ns; s0 += kBatch) {
+        f32x4_t t[kBatch][kPer];
 #pragma unroll
-            for (int c = 0; c < kG * 4; ++c) t4[c] = *part_at(sidx, (mb * S::kNB + nb0) * 4 + c);
+        for (int b = 0; b < kBatch; ++b) {
+          const int sidx = s0 + b;
+#pragma unroll
+          for (int i = 0; i < kPer; ++i) {
+            const int it = tid + i * S::kThreads;
+            const int c = it / kUThreads, r = it % kUThreads;
+            if (sidx < ns && !(own && sidx == mine)) {
+              const int th = ((r >> 6) * WM + uwm) * 64 + (r & 63);
+              t[b][i] = *(reinterpret_cast<const f32x4_t*>(sp.part) +
+                          ((int64_t(tile) * ns + sidx) * kChunks + umb * kUC + c) * S::kThreads + th);
+            } else if (sidx < ns) {
+              t[b][i] = own_buf[c * kUThreads + r];
+            }
           }
-#pragma unroll
-          for (int c = 0; c < kG * 4; ++c) v4[c] = sidx == 0 ? t4[c] : v4[c] + t4[c];
         }
 #pragma unroll
-        for (int g = 0; g < kG; ++g)
+        for (int b = 0; b < kBatch; ++b)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const f32x4_t u4 = v4[g * 4 + q];
-            acc[mb][nb0 + g][4 * q] = u4.x; acc[mb][nb0 + g][4 * q + 1] = u4.y;
-            acc[mb][nb0 + g][4 * q + 2] = u4.z; acc[mb][nb0 + g][4 * q + 3] = u4.w;
-          }
+          for (int i = 0; i < kPer; ++i)
+            if (s0 + b < ns) v[i] = (s0 + b == 0) ? t[b][i] : v[i] + t[b][i];
       }
+      // chunk c = nb*4 + q of unit thread r (wave wn = r / 64, lane L = r % 64) holds
+      // rows 8q + 4*(L >> 5) + 0..3, column wn*TN + nb*32 + (L & 31) of the unit
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int it = tid + i * S::kThreads;
+        const int c = it / kUThreads, r = it % kUThreads;
+        const int nb = c >> 2, q = c & 3, L = r & 63;
+        const int row = 8 * q + 4 * (L >> 5);
+        const int col = (r >> 6) * S::kTN + nb * 32 + (L & 31);
+        float* d = utile + row * kTPitch + col;
+        d[0] = v[i].x;
+        d[kTPitch] = v[i].y;
+        d[2 * kTPitch] = v[i].z;
+        d[3 * kTPitch] = v[i].w;
+      }
+      __syncthreads();
+      finish_unit_rows<NH, S::kThreads>(utile, kTPitch, m0 + u * 32, ht, p, e);
+      __syncthreads();  // the next unit reuses the LDS
     }
-    leave();
-    tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, cslot, ht, m0, p, e, smem, units);
+    (void)item_src;
   }
 }
 
@@ -818,7 +942,7 @@ hipError_t launch_dma_split(const ProblemArgs& p, const WeightArgs& w, const Epi
   const int X = p.xcds > 0 ? p.xcds : 1;
   const int tpx = (tiles + X - 1) / X;
   const size_t dyn = p.in_gamma ? size_t(p.K) * 2 : 0;
-  if (S::kLdsBytes + dyn > 160 * 1024 || ksplit < 2 || ksplit > 16 || tiles > kSplitExitOffset ||
+  if (S::kLdsBytes + dyn > 160 * 1024 || ksplit < 2 || ksplit > 16 || tiles > kSplitMaxTiles ||
       p.K / SBK < ksplit)
     return hipErrorInvalidValue;
   TileSplit sp;

@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import HEAD_DIM, Case, f32
+from conftest import HEAD_DIM, Case, f32, launched_kernels
 from oracle import qkv_rope_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -37,6 +37,11 @@ def _with_option(name, value, fn):
         return out
     finally:
         mqk.set_option(name, old)
+
+
+def _blocks(fn):
+    """fn with the decode blocks forced (the planner takes them whenever eligible)."""
+    return _with_option("decode_cost_model", 0, fn)
 
 
 def _close(a, b, label):
@@ -138,9 +143,10 @@ def test_decode_blocks_recompute_path(device):
     pos = torch.randint(0, 8192, (T,), generator=torch.Generator().manual_seed(3), dtype=torch.int32)
     case = Case(1, T, 4096, 32, 8, seed=1400, rows=8192, positions=pos)
     args = case.args(device)
-    out = mqk.fused_qkv_rope(*args)
-    torch.cuda.synchronize()
-    again = _with_option("decode_force_recompute", 1, lambda: mqk.fused_qkv_rope(*args))
+    call = lambda: _blocks(lambda: mqk.fused_qkv_rope(*args))
+    assert launched_kernels(call) == ["decode_multi"]
+    out = call()
+    again = _with_option("decode_force_recompute", 1, call)
     for a, b in zip(out, again):
         assert torch.equal(a, b)
 
@@ -155,13 +161,13 @@ def test_decode_blocks_finisher_hand_off(spins, device):
     pos = torch.randint(0, 8192, (T,), generator=torch.Generator().manual_seed(12), dtype=torch.int32)
     case = Case(1, T, 4096, 32, 8, seed=1450, rows=8192, positions=pos)
     args = case.args(device)
-    want = mqk.fused_qkv_rope(*args)
-    torch.cuda.synchronize()
+    call = lambda: _blocks(lambda: mqk.fused_qkv_rope(*args))
+    assert launched_kernels(call) == ["decode_multi"]
+    want = call()
     for rep in range(3):
-        got = _with_option("decode_max_spins", spins, lambda: mqk.fused_qkv_rope(*args))
+        got = _with_option("decode_max_spins", spins, call)
         assert all(torch.equal(a, b) for a, b in zip(got, want)), f"spins={spins} rep={rep}"
-    again = mqk.fused_qkv_rope(*args)  # the counters were left at zero
-    torch.cuda.synchronize()
+    again = call()  # the counters were left at zero
     assert all(torch.equal(a, b) for a, b in zip(again, want))
 
 
@@ -174,8 +180,9 @@ def test_decode_blocks_input_norm_four_blocks(device):
     case = Case(1, T, hidden, 32, 8, seed=1500, rows=8192, positions=pos)
     x, wq, wk, wv, gq, gk, cos, sin, p = case.args(device)
     g_in = (1 + 0.3 * torch.randn(hidden, generator=torch.Generator().manual_seed(5))).bfloat16().to(device)
-    out = mqk.fused_qkv_rope_ex(x, wq, wk, wv, gq, gk, cos, sin, p, input_norm_w=g_in)
-    torch.cuda.synchronize()
+    call = lambda: _blocks(lambda: mqk.fused_qkv_rope_ex(x, wq, wk, wv, gq, gk, cos, sin, p, input_norm_w=g_in))
+    assert launched_kernels(call) == ["row_scale", "decode_multi"]
+    out = call()
     for t0 in range(0, T, 64):
         alone = mqk.fused_qkv_rope_ex(x[:, t0:t0 + 64].contiguous(), wq, wk, wv, gq, gk, cos, sin,
                                       p[t0:t0 + 64], input_norm_w=g_in)

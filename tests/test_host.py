@@ -120,14 +120,14 @@ def test_workspace_size(lib):
     assert lib.mqk_fused_qkv_rope_workspace_size(2048, 32, 8, 4096) == 0     # tile kernel only
     assert lib.mqk_fused_qkv_rope_workspace_size(0, 32, 8, 4096) == 0
     n = lib.mqk_fused_qkv_rope_workspace_size(64, 32, 8, 4096)
-    C = 4096 + 256  # 1024 arrival counters + the statistics line
+    C = 4096 + 256 + 512 * 128  # 1024 arrival counters, the statistics line, a line per split-K tile
     assert n >= C + 48 * 64 * 128 * 4  # counters + at least one fp32 partial per head
     from mqk import _native
-    # 64 < T: one decode launch covers every 64-row block; each block has its own
-    # partials, so four blocks need four times the partial region
-    assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == C + 4 * (n - C)
     _native.set_option("tile_ksplit", 0)  # decode blocks or the one-workgroup-per-tile launch only
     try:
+        # 64 < T: one decode launch covers every 64-row block; each block has its own
+        # partials, so four blocks need four times the partial region
+        assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == C + 4 * (n - C)
         _native.set_option("decode_passes", 1)
         try:  # one block per launch: the launches share one block's region
             assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == n
@@ -141,20 +141,20 @@ def test_workspace_size(lib):
     finally:
         _native.set_option("tile_ksplit", 1)
     # Without decode blocks, bf16 T = 200 (2 x 16 tiles of 128 x 384) runs as a
-    # split-K tile launch of 4 splits (the planner's model: 4 beats 2 and 3): the
-    # counters, then one fp32 partial of a tile per (tile, split); int4 takes the
-    # tile kernel, which needs none.
+    # split-K tile launch of 7 splits (the planner's model; 6 and 8 measured within
+    # 1 us of each other): the counters, then one fp32 partial of a tile per
+    # (tile, split); int4 takes the tile kernel, which needs none.
     _native.set_option("decode_blocks", 0)
     try:
-        assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == C + 32 * 4 * 128 * 384 * 4
+        assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == C + 32 * 7 * 128 * 384 * 4
         _native.set_option("tile_ksplit", 2)  # a forced split count
         try:
             assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 8, 4096) == C + 32 * 2 * 128 * 384 * 4
         finally:
             _native.set_option("tile_ksplit", 1)
-        # 40 heads (no 3-head tiling): 1 x 20 tiles of 256 x 256; at hidden 2048 (32
-        # stages) the model's best split count is 5 (15 + 32/s * 1.3 + 1.47 * s us)
-        assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 4, 2048) == C + 20 * 5 * 256 * 256 * 4
+        # 40 heads (no 3-head tiling): 1 x 20 tiles of 256 x 256 (8 row units each);
+        # at hidden 2048 (32 stages) the model's best split count is 8
+        assert lib.mqk_fused_qkv_rope_workspace_size(200, 32, 4, 2048) == C + 20 * 8 * 256 * 256 * 4
     finally:
         _native.set_option("decode_blocks", 16)
 
@@ -165,7 +165,7 @@ def test_split_tile_plan(lib):
     512 tokens as 4 x 16 tiles of 128 x 384 in 4 splits, 1024 tokens as 8 x 16
     tiles in 2 splits; both fit the CUs once (tiles x splits <= 256)."""
     from mqk import _native
-    C = 4096 + 256
+    C = 4096 + 256 + 512 * 128
     part = 128 * 384 * 4  # one tile's fp32 partial
     _native.set_option("decode_blocks", 0)  # int4 then takes its tile kernel: no workspace
     try:
@@ -191,7 +191,7 @@ def test_decode_block_crossovers(lib):
     larger of the two formats' needs.)"""
     from mqk import _native
     size = lambda T: lib.mqk_fused_qkv_rope_workspace_size(T, 32, 8, 4096)
-    C = 4096 + 256  # per-head arrival counters + the statistics line
+    C = 4096 + 256 + 512 * 128  # arrival counters, the statistics line, a line per split-K tile
     one = size(64) - C  # partials of one 64-row block
     for T in (128, 512, 768, 896, 1024):
         assert size(T) == C + (T // 64) * one, T

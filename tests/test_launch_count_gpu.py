@@ -52,11 +52,11 @@ def test_mid_t_decode_block_launches(T, plan, device):
         mqk.set_option("decode_cost_model", 1)
 
 
-@pytest.mark.parametrize("T,plan", [(128, ["decode_multi"]), (256, ["decode_multi"]), (512, ["tile_split"]),
-                                    (1024, ["tile_split"]), (2048, ["tile"])])
+@pytest.mark.parametrize("T,plan", [(128, ["decode_multi"]), (192, ["decode_multi"]), (256, ["tile_split"]),
+                                    (512, ["tile_split"]), (1024, ["tile_split"]), (2048, ["tile"])])
 def test_default_plan_by_token_count(T, plan, device):
     """The default planner at hidden 4096 (bf16): decode blocks for a few 64-row
-    blocks, the split-K tile launch from about 400 tokens while tiles are fewer
+    blocks, the split-K tile launch from about 200 tokens while tiles are fewer
     than CUs, one tile per workgroup once the tiles fill the CUs."""
     case = Case(1, T, HID, HQ, HKV, seed=15 + T)
     assert launched_kernels(_bf16_call(case, device)) == plan
@@ -78,7 +78,7 @@ def test_tail_split_adds_one_decode_launch(device):
 
 
 @pytest.mark.parametrize("B,S,plan", [(64, 1, ["row_scale", "decode"]), (4, 512, ["row_scale", "tile"]),
-                                      (1, 256, ["row_scale", "decode_multi"])])
+                                      (1, 128, ["row_scale", "decode_multi"]), (1, 256, ["row_scale", "tile_split"])])
 def test_input_norm_adds_its_pre_pass(B, S, plan, device):
     g = torch.Generator().manual_seed(15)
     pos = torch.randint(0, 4096, (B * S,), generator=g, dtype=torch.int32) if S == 1 else None
