@@ -2,7 +2,7 @@
 """Benchmark of the fused QKV + QK-Norm + RoPE op on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
-    python bench.py --only {c2,c3,c4,c5,mid,mid256,gemm,copy} --steps K   # one workload, for profiler runs
+    python bench.py --only {c2,c3,c4,c5,mid,mid256,mid128,gemm,copy} --steps K   # one workload, for profiler runs
 
 Headline (``value``): BASELINE config 2, Qwen3-8B prefill B=4 x S=512 (2048
 tokens, hidden 4096, 32 Q heads, 8 KV heads, head_dim 128, bf16), tokens/s of
@@ -284,7 +284,7 @@ def copy_kernel(nbytes, steps, dev):
     torch.cuda.synchronize()
 
 
-WORKLOADS = ("c2", "c3", "c4", "c5", "mid", "mid256", "gemm", "copy")
+WORKLOADS = ("c2", "c3", "c4", "c5", "mid", "mid256", "mid128", "gemm", "copy")
 
 
 def run_only(name, steps, warmup, dev):
@@ -300,8 +300,10 @@ def run_only(name, steps, warmup, dev):
         ms, _ = bench_w4a16(hidden, Hq, Hkv, 4, steps, warmup, dev)
     elif name == "mid":  # a 512-token call (random positions): the split-K tile launch
         ms, _ = bench_decode(512, hidden, Hq, Hkv, 2, steps, warmup, dev)
-    elif name == "mid256":  # a 256-token call: one decode launch covering four 64-row blocks
+    elif name == "mid256":  # a 256-token call: the split-K tile launch
         ms, _ = bench_decode(256, hidden, Hq, Hkv, 2, steps, warmup, dev)
+    elif name == "mid128":  # a 128-token call: one decode launch covering two 64-row blocks
+        ms, _ = bench_decode(128, hidden, Hq, Hkv, 2, steps, warmup, dev)
     elif name == "gemm":  # the W4A16 GEMM decode shapes, M = 1 / 4 / 8 / 16
         ms = {m: v[0] * 1e-3 for m, v in bench_w4a16_gemm_decode(steps, warmup, dev).items()}
     else:

@@ -104,7 +104,7 @@ size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hid
  * callers that cannot call hipMalloc (code under HIP-graph capture, tight
  * serving loops, harnesses that forbid allocation).  It has no counterpart in
  * the reference.  The decode kernel's counters and partials live in a fixed
- * device array of 4.25 KiB + 8 MiB per GPU, held until the process ends; calls
+ * device array of 68.25 KiB + 8 MiB per GPU, held until the process ends; calls
  * whose decode launch needs more (e.g. T <= 64 with more than 256 heads x
  * splits) return MQK_ERR_WORKSPACE before launching anything, and larger T run
  * with fewer 64-row blocks per decode launch (bit-identical results).  Every
