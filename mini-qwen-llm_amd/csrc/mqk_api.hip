@@ -150,11 +150,15 @@ struct Plan {
 
 // Split-K tile launch for problems with fewer tiles than CUs (bf16 weights):
 // variant 16 (128 x 384) when the heads tile by 3, else 18 (256 x 256).  Returns
-// the split count (0: none fits) and its modelled kernel time, fitted on MI355X
-// (hidden 4096, T = 129 .. 1024, 2 to 8 splits; within ~1.5 us): ~9.5 us of
-// launch and waits, ~1.13 us per 64-k stage of a split, ~0.24 us per MB of fp32
-// partials published and read back, and ~5.2 us per 32-row unit of a tile that
-// one split finishes (the busiest split: ceil(units / splits)).
+// the split count (0: none fits) and its modelled kernel time, fitted on MI355X:
+// a fixed cost (launch and waits), a cost per 64-k stage of the busiest split, per
+// MB of fp32 partials published and read back, and per 32-row unit of a tile that
+// the busiest split finishes (ceil(units / splits)).
+//   128 x 384 (hidden 4096, T = 129 .. 1024, 2 to 8 splits; within ~1.5 us):
+//     9.5 us, 1.13 us per stage, 0.24 us per MB, 5.2 us per unit.
+//   256 x 256 (hidden 1024 / 2048 / 5120 with 32 / 40 / 56 heads, T = 128 .. 1536,
+//     2 to 8 splits; rms error 1.5 us): 12.6 us, 1.6 us per stage of
+//     ceil(stages / splits), 0.195 us per MB, 0.35 us per unit.
 int plan_tile_split(int64_t M, int64_t K, int n_tiles, const Topology& topo, const TileVariant*& v, double& us) {
   v = nullptr;
   us = 1e30;
@@ -169,15 +173,17 @@ int plan_tile_split(int64_t M, int64_t K, int n_tiles, const Topology& topo, con
   const int64_t X = topo.xcds;
   const int64_t slots = (tiles + X - 1) / X * X;  // tiles padded to whole XCD shares
   const int64_t nkt = K / 64;
-  const double stage_us = id == 16 ? 1.13 : 1.5;  // (256 x 256: 1.33x the MFMA work per stage)
+  const double fixed_us = id == 16 ? 9.5 : 12.6, stage_us = id == 16 ? 1.13 : 1.6;
+  const double mb_us = id == 16 ? 0.24 : 0.195, unit_us = id == 16 ? 5.2 : 0.35;
   const double part_mb = (id == 16 ? 196608.0 : 262144.0) * 1e-6;  // one workgroup's partial
   const int units = id == 16 ? 4 : 8;
   int best = 0;
   const int lo = req >= 2 ? int(req) : 2, hi = req >= 2 ? int(req) : 8;
   for (int s = lo; s <= hi; ++s) {
     if (slots * s > topo.cus || nkt < 4 * int64_t(s) || tiles > kSplitMaxTiles) break;
-    const double t = 9.5 + double(nkt) / s * stage_us + 0.24 * part_mb * double(tiles) * s +
-                     5.2 * double((units + s - 1) / s);
+    const double stages = id == 16 ? double(nkt) / s : double((nkt + s - 1) / s);
+    const double t = fixed_us + stages * stage_us + mb_us * part_mb * double(tiles) * s +
+                     unit_us * double((units + s - 1) / s);
     if (t < us) {
       us = t;
       best = s;
@@ -206,18 +212,23 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
   // designated split: T = 128 / 256 / 512 / 1024 take 25.6 / 39.3 / 56.9 / 93.5 us
   // bf16), against ~83 us (bf16) and ~138 us (int4) for the best tile variant at
   // T = 65..1024.  The models below follow those measurements; at hidden 4096 bf16
-  // runs as blocks up to T = 832, int4 up to T = 1024.
+  // runs as blocks up to T = 832, int4 up to T = 1024.  The bf16 block costs were
+  // refitted over hidden 1024 / 2048 / 4096 (32 / 40 / 48 heads, T = 128 .. 1024;
+  // within ~2.5 us): the first block ~14.2 us + 0.187 us per MB of weights, each
+  // further block 2.17 + 0.584 * K/1024 us.  The one-workgroup-per-tile launch
+  // costs ~1.15 us per 64-k stage with 128 x 384 tiles, ~1.27 us with the others.
   const int64_t nblk = (M + 63) / 64;
   const int blk_splits = decode_splits_for(64, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds);
   const int64_t per_launch = std::max<int64_t>(
       1, std::min<int64_t>(g_decode_passes.load(), decode_max_blocks(n_tiles, K, blk_splits, int4 && in_norm)));
   const int64_t launches = (nblk + per_launch - 1) / per_launch;
   const double w_bytes = double(n_tiles) * kHeadDim * double(K) * (int4 ? 0.5 : 2.0);
-  const double dec_us = int4 ? 4.0 + 3.0 * double(K) / 1024.0 : 8.0 + w_bytes / 5.0e6;
-  const double pass_us = 0.5 + double(K) / 4096.0 * 4.5;
-  // (+3 us for a launch of several blocks: T = 128 / 256 / 512 measured 25.6 / 39.3 / 56.9)
-  const double blocks_us = double(launches) * dec_us + double(nblk - launches) * pass_us + (nblk > 1 ? 3.0 : 0.0);
-  const double tile_us = double(K) / 64.0 * (int4 ? 2.1 : 1.15) + 5.0;
+  const double dec_us = int4 ? 4.0 + 3.0 * double(K) / 1024.0 : 14.2 + 0.187 * w_bytes * 1e-6;
+  const double pass_us = int4 ? 0.5 + double(K) / 4096.0 * 4.5 : 2.17 + 0.584 * double(K) / 1024.0;
+  // (int4: +3 us for a launch of several blocks)
+  const double blocks_us = double(launches) * dec_us + double(nblk - launches) * pass_us +
+                           (int4 && nblk > 1 ? 3.0 : 0.0);
+  const double tile_us = double(K) / 64.0 * (int4 ? 2.1 : (n_tiles % 3 == 0 ? 1.15 : 1.27)) + 5.0;
   // split-K tile launch (bf16): taken when its model beats both the one-workgroup-
   // per-tile launch and the decode blocks
   const TileVariant* sv = nullptr;

@@ -181,6 +181,31 @@ def test_split_tile_plan(lib):
         _native.set_option("decode_blocks", 16)
 
 
+def test_split_tile_plan_other_shapes(lib):
+    """The split-K model for 256 x 256 tiles, refitted on MI355X measurements at
+    hidden 1024 / 2048 / 5120: the split counts it picks (shown by the partials'
+    size) are the fastest measured, or within ~2 us of it.  Hidden 5120 (Qwen3-14B
+    heads) at T = 768 / 1024: 2 splits, 86.7 / 94.6 us against 110.5 / 117.2 us for
+    one tile per workgroup; hidden 2048 (30B-A3B heads) at T = 512: 4 splits,
+    32.7 us against 42.0 us for decode blocks."""
+    from mqk import _native
+    C = 4096 + 256 + 512 * 128
+    part = 256 * 256 * 4
+    size = lambda T, hq, hkv, h: lib.mqk_fused_qkv_rope_workspace_size(T, hq, hkv, h)
+    _native.set_option("decode_blocks", 0)  # int4 then takes its tile kernel: no workspace
+    try:
+        for T, hq, hkv, h, tiles, s in ((128, 32, 4, 2048, 20, 8), (512, 32, 4, 2048, 40, 4),
+                                        (768, 32, 4, 2048, 60, 4), (1024, 32, 4, 2048, 80, 3),
+                                        (128, 40, 8, 5120, 28, 8), (512, 40, 8, 5120, 56, 4),
+                                        (768, 40, 8, 5120, 84, 2), (1024, 40, 8, 5120, 112, 2),
+                                        (256, 16, 8, 1024, 16, 4)):
+            assert size(T, hq, hkv, h) == C + tiles * s * part, (T, h)
+        for T, hq, hkv, h in ((1536, 32, 4, 2048), (1536, 40, 8, 5120), (1024, 16, 8, 1024)):
+            assert size(T, hq, hkv, h) == 0, (T, h)  # one tile per workgroup
+    finally:
+        _native.set_option("decode_blocks", 16)
+
+
 def test_decode_block_crossovers(lib):
     """The plan's cost model reproduces the crossovers measured on MI355X at hidden
     4096 (Qwen3-8B heads): a workspace is needed exactly when decode launches run.

@@ -62,6 +62,19 @@ def test_default_plan_by_token_count(T, plan, device):
     assert launched_kernels(_bf16_call(case, device)) == plan
 
 
+@pytest.mark.parametrize("hidden,hq,hkv,T,plan", [
+    (1024, 16, 8, 128, ["decode_multi"]), (1024, 16, 8, 1024, ["tile"]),
+    (2048, 32, 4, 128, ["decode_multi"]), (2048, 32, 4, 512, ["tile_split"]), (2048, 32, 4, 1536, ["tile"]),
+    (5120, 40, 8, 1024, ["tile_split"])])
+def test_default_plan_other_shapes(hidden, hq, hkv, T, plan, device):
+    """The planner at the other Qwen3 attention shapes takes the kernel family
+    measured fastest on MI355X (bf16): e.g. hidden 2048 at T = 512 as split-K tiles
+    (32.7 us against 42.0 for decode blocks), hidden 5120 at T = 1024 as split-K
+    tiles (94.6 us against 117.2 for one tile per workgroup)."""
+    case = Case(1, T, hidden, hq, hkv, seed=17 + T)
+    assert launched_kernels(_bf16_call(case, device)) == plan
+
+
 def test_tail_split_adds_one_decode_launch(device):
     """2080 tokens in 128 x 384 tiles: 16 full row tiles fill the 256 CUs once,
     and the last 32 rows go to the decode kernel instead of a second round."""
