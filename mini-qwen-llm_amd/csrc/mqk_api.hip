@@ -217,18 +217,22 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
   // within ~2.5 us): the first block ~14.2 us + 0.187 us per MB of weights, each
   // further block 2.17 + 0.584 * K/1024 us.  The one-workgroup-per-tile launch
   // costs ~1.15 us per 64-k stage with 128 x 384 tiles, ~1.27 us with the others.
+  // int4, refitted over the same shapes and hidden 5120 (40/8 heads): the first
+  // block max(14.5, 1.45 * k tiles per split) us, each further block
+  // 1.95 + 0.71 * K/1024 us, the tile kernel 2.1 us per stage + 7 us.
   const int64_t nblk = (M + 63) / 64;
   const int blk_splits = decode_splits_for(64, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds);
   const int64_t per_launch = std::max<int64_t>(
       1, std::min<int64_t>(g_decode_passes.load(), decode_max_blocks(n_tiles, K, blk_splits, int4 && in_norm)));
   const int64_t launches = (nblk + per_launch - 1) / per_launch;
   const double w_bytes = double(n_tiles) * kHeadDim * double(K) * (int4 ? 0.5 : 2.0);
-  const double dec_us = int4 ? 4.0 + 3.0 * double(K) / 1024.0 : 14.2 + 0.187 * w_bytes * 1e-6;
-  const double pass_us = int4 ? 0.5 + double(K) / 4096.0 * 4.5 : 2.17 + 0.584 * double(K) / 1024.0;
-  // (int4: +3 us for a launch of several blocks)
-  const double blocks_us = double(launches) * dec_us + double(nblk - launches) * pass_us +
-                           (int4 && nblk > 1 ? 3.0 : 0.0);
-  const double tile_us = double(K) / 64.0 * (int4 ? 2.1 : (n_tiles % 3 == 0 ? 1.15 : 1.27)) + 5.0;
+  // (int4's first block is bound by the 64-k tiles each split dequantises and
+  // multiplies, ~1.45 us each, over a ~14.5 us floor)
+  const int64_t split_kt = blk_splits > 0 ? (K / 64 + blk_splits - 1) / blk_splits : 0;
+  const double dec_us = int4 ? std::max(14.5, 1.45 * double(split_kt)) : 14.2 + 0.187 * w_bytes * 1e-6;
+  const double pass_us = int4 ? 1.95 + 0.71 * double(K) / 1024.0 : 2.17 + 0.584 * double(K) / 1024.0;
+  const double blocks_us = double(launches) * dec_us + double(nblk - launches) * pass_us;
+  const double tile_us = int4 ? double(K) / 64.0 * 2.1 + 7.0 : double(K) / 64.0 * (n_tiles % 3 == 0 ? 1.15 : 1.27) + 5.0;
   // split-K tile launch (bf16): taken when its model beats both the one-workgroup-
   // per-tile launch and the decode blocks
   const TileVariant* sv = nullptr;
