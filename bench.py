@@ -2,7 +2,7 @@
 """Benchmark of the fused QKV + QK-Norm + RoPE op on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
-    python bench.py --only {c2,c3,c4,c5,mid,mid256,mid128,gemm,copy} --steps K   # one workload, for profiler runs
+    python bench.py --only {c1f32,c2,c3,c4,c5,mid,mid256,mid128,gemm,copy} --steps K   # one workload, for profiler runs
 
 Headline (``value``): BASELINE config 2, Qwen3-8B prefill B=4 x S=512 (2048
 tokens, hidden 4096, 32 Q heads, 8 KV heads, head_dim 128, bf16), tokens/s of
@@ -92,16 +92,22 @@ def time_steps(fn, steps, warmup):
     return e0.elapsed_time(e1) / steps, wall
 
 
-def bench_prefill(S_total, B, S, hidden, Hq, Hkv, seed, steps, warmup, dev, copies=6):
+def bench_prefill(S_total, B, S, hidden, Hq, Hkv, seed, steps, warmup, dev, copies=6, fp32=False):
     """Steps rotate over `copies` sets of (x, weights), more bytes than the 256 MB
     Infinity Cache for the BASELINE prefill configs, so each step reads its
-    inputs from HBM instead of finding the previous step's in the cache."""
+    inputs from HBM instead of finding the previous step's in the cache.
+    fp32=True runs the op on fp32 copies of the same inputs (the fp32 front)."""
     import mqk
     x, ws, gq, gk, cos, sin = make_inputs(S_total, hidden, Hq, Hkv, S, seed, dev, copies)
     import torch
     g = torch.Generator(device=dev).manual_seed(seed + 7)
     xs = [x.reshape(B, S, hidden)] + [torch.randn(B, S, hidden, generator=g, device=dev).bfloat16()
                                       for _ in range(copies - 1)]
+    if fp32:
+        xs = [t.float() for t in xs]
+        ws = [tuple(w.float() for w in set_) for set_ in ws]
+        gq, gk = gq.float(), gk.float()
+        cos, sin = (t.to(dev) for t in mqk.rope_tables(D, S))  # the fp32 tables
 
     def step(i):
         wq, wk, wv = ws[i % copies]
@@ -284,13 +290,15 @@ def copy_kernel(nbytes, steps, dev):
     torch.cuda.synchronize()
 
 
-WORKLOADS = ("c2", "c3", "c4", "c5", "mid", "mid256", "mid128", "gemm", "copy")
+WORKLOADS = ("c1f32", "c2", "c3", "c4", "c5", "mid", "mid256", "mid128", "gemm", "copy")
 
 
 def run_only(name, steps, warmup, dev):
     """One workload alone (for profiler runs); prints one JSON line of timings."""
     B, S, hidden, Hq, Hkv = 4, 512, 4096, 32, 8
-    if name == "c2":
+    if name == "c1f32":  # config 1 in fp32 (the fp32 front)
+        ms, _ = bench_prefill(128, 1, 128, 1024, 16, 8, 0, steps, warmup, dev, fp32=True)
+    elif name == "c2":
         ms, _ = bench_prefill(B * S, B, S, hidden, Hq, Hkv, 1, steps, warmup, dev)
     elif name == "c3":
         ms, _ = bench_decode(64, hidden, Hq, Hkv, 2, steps, warmup, dev)
@@ -418,16 +426,19 @@ def main(argv=None) -> int:
                     "included when it exceeds the kernel time); reference: docs/03_w4a16_awq.md:107-116"}
         log("[bench] w4a16 GEMM K=1024 N=4096: " + ", ".join(f"M={m}: {v[0]:.1f} us" for m, v in wg.items()))
         # config 1: the Qwen3-0.6B-shaped layer, B=1 x S=128 (the reference runs it on
-        # the CPU in fp32; here on the GPU in bf16, and the oracle's fp32 composition on the host)
+        # the CPU in fp32; here on the GPU in fp32 and in bf16, and the oracle's fp32
+        # composition on the host)
+        ms1f, _ = bench_prefill(128, 1, 128, 1024, 16, 8, 0, 200, 200, dev, fp32=True)
         ms1, _ = bench_prefill(128, 1, 128, 1024, 16, 8, 0, 200, 200, dev)
-        c1 = {"gpu_tokens_per_s": round(128 / (ms1 * 1e-3), 1), "gpu_ms_per_step": round(ms1, 6),
-              "gpu_dtype": "bf16"}
+        c1 = {"gpu_tokens_per_s": round(128 / (ms1f * 1e-3), 1), "gpu_ms_per_step": round(ms1f, 6),
+              "gpu_dtype": "fp32",
+              "gpu_bf16_tokens_per_s": round(128 / (ms1 * 1e-3), 1), "gpu_bf16_ms_per_step": round(ms1, 6)}
         if not args.no_cpu:
             ctps, cms = cpu_config1()
             c1.update({"cpu_fp32_tokens_per_s": round(ctps, 1), "cpu_ms_per_call": round(cms, 3),
                        "cpu_kind": "port (torch fp32 unfused composition)"})
         sec["config1_qwen3_0p6b_s128"] = c1
-        log(f"[bench] config 1: {ms1 * 1e3:.1f} us/step on the GPU")
+        log(f"[bench] config 1: {ms1f * 1e3:.1f} us/step on the GPU in fp32, {ms1 * 1e3:.1f} in bf16")
         result["secondary"] = sec
 
     if not args.no_cpu:

@@ -16,6 +16,7 @@
  *
  * Reference interface each entry point replaces (mini-qwen-llm):
  *   mqk_fused_qkv_rope_bf16   <- fused_qkv_rope()      mini_qwen/kernels/fused_qkv_rope.py:130-195
+ *   mqk_fused_qkv_rope_f32    <- fused_qkv_rope() called with fp32 tensors (same lines)
  *   mqk_qk_norm_rope_bf16     <- _qk_norm_rope_kernel  mini_qwen/kernels/fused_qkv_rope.py:46-127
  *   mqk_w4a16_gemm(_ex)       <- w4a16_gemm()          mini_qwen/kernels/w4a16_gemm.py:194-247
  *   mqk_fused_qkv_rope_w4a16  <- the W4A16 attention front (3x LinearW4A16 + RMSNorm + RoPE),
@@ -94,6 +95,20 @@ int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
                             int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
                             int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
                             void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * fp32 twin of mqk_fused_qkv_rope_bf16: x, weights, q_gamma / k_gamma and the
+ * cos / sin tables are fp32, and q / k / v are written in fp32
+ * (mini_qwen/kernels/fused_qkv_rope.py:130-195 run on fp32 tensors: an fp32
+ * GEMM, then the norm and RoPE of :84-127 loading and storing fp32).  Products
+ * and sums in fp32 on the matrix cores; norm and RoPE in fp32.  Same position
+ * rules and validation as the bf16 entry point; hidden must be a multiple of
+ * 32.  Needs no workspace.  Launches on `stream` without synchronising.
+ */
+int mqk_fused_qkv_rope_f32(const float* x, const float* w_q, const float* w_k, const float* w_v,
+                           const float* q_gamma, const float* k_gamma, const float* cos, const float* sin,
+                           const int32_t* positions, int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv,
+                           int D, int64_t cos_rows, float eps, float* q, float* k, float* v, void* stream);
 
 /* Workspace bytes needed by mqk_fused_qkv_rope_bf16 / _w4a16 for these sizes
  * (0 when the chosen kernels need none). */

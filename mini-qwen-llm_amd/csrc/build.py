@@ -24,10 +24,11 @@ CSRC = Path(__file__).resolve().parent
 PKG = CSRC.parent / "mqk"
 OUT = PKG / "libmqk.so"
 BUILD_DIR = CSRC.parent / "_build"
-SOURCES = ["qkv_tile.hip", "qkv_tile_dma.hip", "qkv_decode.hip", "norm_rope.hip", "input_norm.hip", "mqk_api.hip"]
+SOURCES = ["qkv_tile.hip", "qkv_tile_dma.hip", "qkv_decode.hip", "norm_rope.hip", "input_norm.hip", "qkv_f32.hip",
+           "mqk_api.hip"]
 # Sources whose kernels must not use scratch memory (register spills): the
 # compiler's resource-usage remarks are checked and the build fails otherwise.
-NO_SCRATCH = {"qkv_decode.hip"}
+NO_SCRATCH = {"qkv_decode.hip", "qkv_f32.hip"}
 ARCH = "gfx950"
 
 COMMON_FLAGS = [

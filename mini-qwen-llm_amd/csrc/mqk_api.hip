@@ -513,6 +513,50 @@ int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
                          cos_rows, eps, q, k, v, nullptr, workspace, ws_bytes, stream);
 }
 
+int mqk_fused_qkv_rope_f32(const float* x, const float* w_q, const float* w_k, const float* w_v,
+                           const float* q_gamma, const float* k_gamma, const float* cos, const float* sin,
+                           const int32_t* positions, int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv,
+                           int D, int64_t cos_rows, float eps, float* q, float* k, float* v, void* stream) {
+  if (T < 0 || hidden <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0)
+    return fail(MQK_ERR_BAD_SHAPE, "need T >= 0, hidden > 0, Hq > 0, Hkv > 0, D > 0");
+  if (D % 2 != 0) return fail(MQK_ERR_BAD_SHAPE, "head_dim must be even (RoPE rotate_half), got %d", D);
+  if (D != kHeadDim) return fail(MQK_ERR_UNSUPPORTED, "head_dim %d not supported (only 128)", D);
+  if (hidden % kF32BK != 0)
+    return fail(MQK_ERR_UNSUPPORTED, "hidden %lld must be a multiple of %d", (long long)hidden, kF32BK);
+  if (Hq + 2 * Hkv > kMaxTiles) return fail(MQK_ERR_UNSUPPORTED, "Hq + 2*Hkv must be <= %d", kMaxTiles);
+  if (T > (int64_t(1) << 31) / 2) return fail(MQK_ERR_UNSUPPORTED, "T too large");
+  if (T == 0) return ok();
+  if (!x || !q || !k || !v) return fail(MQK_ERR_NULL_POINTER, "x/q/k/v must be non-NULL");
+  if (!w_q || !w_k || !w_v) return fail(MQK_ERR_NULL_POINTER, "w_q/w_k/w_v must be non-NULL");
+  if (!aligned16(x) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(w_q) ||
+      !aligned16(w_k) || !aligned16(w_v))
+    return fail(MQK_ERR_MISALIGNED, "x/q/k/v and the weights must be 16-byte aligned");
+  int st = check_rope_args(q_gamma, k_gamma, cos, sin, S, cos_rows, positions, eps);
+  if (st != MQK_OK) return st;
+  F32Args a{};
+  a.x = x;
+  a.w[0] = w_q;
+  a.w[1] = w_k;
+  a.w[2] = w_v;
+  a.q_gamma = q_gamma;
+  a.k_gamma = k_gamma;
+  a.cos = cos;
+  a.sin = sin;
+  a.positions = positions;
+  a.M = T;
+  a.K = hidden;
+  a.S = positions ? 1 : S;
+  a.cos_rows = cos_rows;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.eps = eps;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  return hip_status(launch_f32_qkv(a, device_topology().xcds, static_cast<hipStream_t>(stream)),
+                    "f32 front launch");
+}
+
 // ---- allocation-free variant of mqk_fused_qkv_rope_bf16 ---------------------------------
 // The decode kernel's scratch (its arrival counters, then its fp32 split partials)
 // lives in this file-scope device array instead of a caller workspace: 4.25 KiB

@@ -327,6 +327,25 @@ __device__ __forceinline__ float sum8_lanes(float v) {
   return v;
 }
 
+// Epilogue arithmetic with every rounding step written out (no contraction left
+// to the compiler), so that each tile shape's instantiation gives identical bits
+// for the same accumulators however the compiler schedules it.
+//
+// Sum of squares of one thread's 16 head dims d = 8c+i and 64+8c+i (i = 0..7).
+__device__ __forceinline__ float run_sumsq(const float (&lo)[8], const float (&hi)[8]) {
+#pragma clang fp contract(off)
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = ss + __builtin_fmaf(lo[i], lo[i], hi[i] * hi[i]);
+  return ss;
+}
+
+// 1 / rms of a head from the sum of squares of its 128 dims.
+__device__ __forceinline__ float head_rms(float ss, float eps) {
+#pragma clang fp contract(off)
+  return rsqrtf(__builtin_fmaf(ss, 1.0f / float(kHeadDim), eps));
+}
+
 __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 }  // namespace mqk

@@ -163,4 +163,29 @@ extern int g_decode_max_spins;
 hipError_t launch_norm_rope(const uint16_t* q_raw, const uint16_t* k_raw, const EpilogueArgs& e,
                             int64_t T, hipStream_t stream);
 
+// fp32 front (fp32 x, weights, norm weights and RoPE tables; fp32 outputs).
+struct F32Args {
+  const float* x;       // [M, K]
+  const float* w[3];    // w_q [Hq*128, K], w_k / w_v [Hkv*128, K]
+  const float* q_gamma;
+  const float* k_gamma;
+  const float* cos;     // [cos_rows, 128]
+  const float* sin;
+  const int32_t* positions;  // [M] or null: prefill, token t uses row t % S
+  int64_t M, K, S, cos_rows;
+  int Hq, Hkv;
+  float eps;
+  float* q;             // [M, Hq, 128]
+  float* k;             // [M, Hkv, 128]
+  float* v;             // [M, Hkv, 128]
+  // (fields read by rope_row: no varlen, launch row 0 is token 0)
+  const int32_t* cu_seqlens = nullptr;
+  const int32_t* seq_pos0 = nullptr;
+  int64_t n_seqs = 0;
+  int64_t t0 = 0;
+};
+constexpr int kF32RowTile = 32;  // rows per workgroup of the fp32 kernel
+constexpr int kF32BK = 32;       // k extent of one staged fp32 tile
+hipError_t launch_f32_qkv(const F32Args& a, int xcds, hipStream_t stream);
+
 }  // namespace mqk

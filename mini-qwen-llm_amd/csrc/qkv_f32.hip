@@ -1,0 +1,133 @@
+// The fused front for fp32 callers: fp32 x, weights, norm weights and RoPE
+// tables in, fp32 q / k / v out.  The reference op accepts fp32 tensors too:
+// its GEMM is then an fp32 matmul and its Triton kernel loads, normalises,
+// rotates and stores in fp32 (mini_qwen/kernels/fused_qkv_rope.py:84-127,
+// :167-173; the fp32 layer of the reference's CPU-runnable configuration).
+//
+// One workgroup of four waves computes 32 token rows x one head (128 columns):
+// each wave owns 32 columns and runs the fp32 matrix core
+// (v_mfma_f32_32x32x2_f32: products and sums in fp32) over k tiles of 32 staged
+// in LDS, the next tile's loads in registers under the current tile's MFMAs.
+// The accumulators then go through LDS so that eight threads hold a row's
+// 128 dims (each the RoPE pairs d, d+64 for eight d), apply RMSNorm and RoPE
+// in fp32, and store.
+#include "mqk_device.h"
+#include "mqk_kernels.h"
+
+namespace mqk {
+namespace {
+
+constexpr int kRows = kF32RowTile;
+constexpr int kKT = kF32BK;
+constexpr int kPitch = kKT + 1;          // LDS row pitch of the staged tiles (odd: no bank conflicts)
+constexpr int kEpiPitch = kHeadDim + 4;  // LDS row pitch of the accumulator tile
+constexpr int kThreads = 256;
+static_assert(kHeadDim * kPitch >= kRows * kEpiPitch, "the accumulator tile reuses the weight tile's LDS");
+
+__global__ void __launch_bounds__(kThreads) f32_qkv_kernel(F32Args a, int xcds) {
+  __shared__ float xs[kRows * kPitch];
+  __shared__ float ws[kHeadDim * kPitch];
+  const int n_rt = int((a.M + kRows - 1) / kRows);
+  const int tile = xcd_tile_id(int(blockIdx.x), int(gridDim.x), xcds);
+  const int rt = tile % n_rt;
+  const int h = tile / n_rt;
+  int proj, hh;
+  split_head(h, a.Hq, a.Hkv, proj, hh);
+  const float* W = a.w[proj] + int64_t(hh) * kHeadDim * a.K;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row0 = int64_t(rt) * kRows;
+
+  // staging: thread tid loads 4 consecutive k of x row (tid / 8) and of weight
+  // rows (tid / 8) + 32 j, j = 0..3
+  const int sr = tid >> 3, sk = (tid & 7) * 4;
+  const bool x_in = row0 + sr < a.M;
+  const float* xp = a.x + (x_in ? (row0 + sr) * a.K : 0) + sk;
+  const float* wp = W + int64_t(sr) * a.K + sk;
+  f32x4_t xr, wr[4];
+  auto load = [&](int64_t k0) {
+    xr = x_in ? *reinterpret_cast<const f32x4_t*>(xp + k0) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wr[j] = *reinterpret_cast<const f32x4_t*>(wp + int64_t(32 * j) * a.K + k0);
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xs[sr * kPitch + sk + i] = xr[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ws[(sr + 32 * j) * kPitch + sk + i] = wr[j][i];
+  };
+
+  f32x16_t acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  // lane l multiplies x row (l & 31) with weight row 32 * wave + (l & 31), at k
+  // slot (l >> 5) of each pair of k
+  const float* xa = xs + (lane & 31) * kPitch + (lane >> 5);
+  const float* wb = ws + (32 * wave + (lane & 31)) * kPitch + (lane >> 5);
+  load(0);
+  for (int64_t k0 = 0; k0 < a.K; k0 += kKT) {
+    stage();
+    __syncthreads();
+    if (k0 + kKT < a.K) load(k0 + kKT);
+#pragma unroll
+    for (int kk = 0; kk < kKT / 2; ++kk)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[2 * kk], wb[2 * kk], acc, 0, 0, 0);
+    __syncthreads();
+  }
+
+  // accumulators -> LDS: acc[i] = C[8 * (i / 4) + 4 * (l >> 5) + i % 4][l & 31]
+  float* ep = ws;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    ep[(8 * (i >> 2) + 4 * (lane >> 5) + (i & 3)) * kEpiPitch + 32 * wave + (lane & 31)] = acc[i];
+  __syncthreads();
+
+  // thread tid: row r = tid / 8, dims d = 8c .. 8c+7 and 64 + 8c .. (c = tid % 8)
+  const int r = tid >> 3, c = tid & 7;
+  const int64_t t = row0 + r;
+  float lo[8], hi[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    lo[i] = ep[r * kEpiPitch + 8 * c + i];
+    hi[i] = ep[r * kEpiPitch + kHalfDim + 8 * c + i];
+  }
+  if (proj < 2) {
+    // (every lane takes part in the 8-lane sum; rows past M hold zeros)
+    const float ss = sum8_lanes(run_sumsq(lo, hi));
+    const float rms = head_rms(ss, a.eps);
+    if (t < a.M) {
+      const float* g = proj == 0 ? a.q_gamma : a.k_gamma;
+      const int64_t prow = rope_row(a, t) * kHeadDim;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma clang fp contract(off)
+        const int d = 8 * c + i;
+        const float x1n = lo[i] * rms * g[d];
+        const float x2n = hi[i] * rms * g[d + kHalfDim];
+        lo[i] = __builtin_fmaf(x1n, a.cos[prow + d], -(x2n * a.sin[prow + d]));
+        hi[i] = __builtin_fmaf(x2n, a.cos[prow + d + kHalfDim], x1n * a.sin[prow + d + kHalfDim]);
+      }
+    }
+  }
+  if (t < a.M) {
+    const int H = proj == 0 ? a.Hq : a.Hkv;
+    float* dst = pick3(proj, a.q, a.k, a.v) + (t * H + hh) * kHeadDim + 8 * c;
+    *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{lo[0], lo[1], lo[2], lo[3]};
+    *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{lo[4], lo[5], lo[6], lo[7]};
+    *reinterpret_cast<f32x4_t*>(dst + kHalfDim) = f32x4_t{hi[0], hi[1], hi[2], hi[3]};
+    *reinterpret_cast<f32x4_t*>(dst + kHalfDim + 4) = f32x4_t{hi[4], hi[5], hi[6], hi[7]};
+  }
+}
+
+}  // namespace
+
+hipError_t launch_f32_qkv(const F32Args& a, int xcds, hipStream_t stream) {
+  const int64_t n_rt = (a.M + kRows - 1) / kRows;
+  const int64_t blocks = n_rt * (a.Hq + 2 * a.Hkv);
+  if (a.K % kKT != 0 || blocks <= 0 || blocks > (int64_t(1) << 31) - 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(f32_qkv_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0, stream, a, xcds);
+  return hipGetLastError();
+}
+
+}  // namespace mqk

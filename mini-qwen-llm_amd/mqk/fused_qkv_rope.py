@@ -25,8 +25,13 @@ Differences from the reference, all deliberate:
     bit-equality with torch's own GEMM, which no independent kernel can give);
   * positions outside ``[0, cos.shape[0])`` are clamped instead of read out of
     bounds; int64 positions are accepted and converted;
-  * inputs must be bf16 CUDA/HIP tensors (TypeError / ValueError otherwise);
-    non-contiguous inputs are made contiguous.
+  * inputs must be CUDA/HIP tensors, either all bf16 or all fp32 (TypeError /
+    ValueError otherwise); non-contiguous inputs are made contiguous.
+
+fp32 inputs (the dtype of the reference's CPU-runnable fp32 layer) take a
+separate kernel: an fp32 projection on the matrix cores (fp32 products and
+sums), norm and RoPE in fp32, fp32 outputs, as the reference computes for fp32
+tensors (an fp32 GEMM, then its kernel loads and stores fp32).
 """
 from __future__ import annotations
 
@@ -63,9 +68,9 @@ def _positions(positions: Optional[torch.Tensor], T: int, device) -> Optional[to
     return positions.to(torch.int32)
 
 
-def _rope_tables(cos, sin, D, device):
-    cos = _require(cos, "cos", device)
-    sin = _require(sin, "sin", device)
+def _rope_tables(cos, sin, D, device, dtype=torch.bfloat16):
+    cos = _require(cos, "cos", device, dtype)
+    sin = _require(sin, "sin", device, dtype)
     if cos.dim() != 2 or cos.shape[1] != D or sin.shape != cos.shape:
         raise ValueError(f"cos/sin must both be [rows, {D}], got {tuple(cos.shape)} / {tuple(sin.shape)}")
     if cos.shape[0] < 1:
@@ -91,30 +96,40 @@ def fused_qkv_rope(
     H_KV = w_k.shape[0] // D
     assert D % 2 == 0, "head_dim must be even (RoPE rotate_half)"
     device = x.device
-    x = _require(x, "x", device)
-    w_q = _require(w_q, "w_q", device)
-    w_k = _require(w_k, "w_k", device)
-    w_v = _require(w_v, "w_v", device)
-    q_norm_w = _require(q_norm_w, "q_norm_w", device)
-    k_norm_w = _require(k_norm_w, "k_norm_w", device)
+    dtype = torch.float32 if isinstance(x, torch.Tensor) and x.dtype == torch.float32 else torch.bfloat16
+    x = _require(x, "x", device, dtype)
+    w_q = _require(w_q, "w_q", device, dtype)
+    w_k = _require(w_k, "w_k", device, dtype)
+    w_v = _require(w_v, "w_v", device, dtype)
+    q_norm_w = _require(q_norm_w, "q_norm_w", device, dtype)
+    k_norm_w = _require(k_norm_w, "k_norm_w", device, dtype)
     if w_q.shape != (H_Q * D, H) or w_k.shape != (H_KV * D, H) or w_v.shape != (H_KV * D, H):
         raise ValueError(
             f"weight shapes {tuple(w_q.shape)}, {tuple(w_k.shape)}, {tuple(w_v.shape)} do not match "
             f"H_Q={H_Q}, H_KV={H_KV}, D={D}, hidden={H}")
     if k_norm_w.shape != (D,):
         raise ValueError(f"k_norm_w must be [{D}], got {tuple(k_norm_w.shape)}")
-    cos, sin = _rope_tables(cos, sin, D, device)
+    cos, sin = _rope_tables(cos, sin, D, device, dtype)
     T = B * S
     pos = _positions(positions, T, device)
 
-    q = torch.empty(B, S, H_Q, D, dtype=torch.bfloat16, device=device)
-    k = torch.empty(B, S, H_KV, D, dtype=torch.bfloat16, device=device)
-    v = torch.empty(B, S, H_KV, D, dtype=torch.bfloat16, device=device)
+    q = torch.empty(B, S, H_Q, D, dtype=dtype, device=device)
+    k = torch.empty(B, S, H_KV, D, dtype=dtype, device=device)
+    v = torch.empty(B, S, H_KV, D, dtype=dtype, device=device)
     if T == 0:
         return q, k, v
 
     lib = _native.library()
     stream = torch.cuda.current_stream(device)
+    if dtype == torch.float32:
+        status = _native.call(
+            device, lib.mqk_fused_qkv_rope_f32,
+            x.data_ptr(), w_q.data_ptr(), w_k.data_ptr(), w_v.data_ptr(),
+            q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), _native.ptr(pos),
+            T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), stream.cuda_stream)
+        _native.check(status, "mqk_fused_qkv_rope_f32")
+        return q, k, v
     nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, H_Q, H_KV, H))
     ws = _native.workspace(device, stream, nbytes)
     status = _native.call(
@@ -191,12 +206,13 @@ def fused_qkv_rope_paged(
     H_KV = w_k.shape[0] // D
     assert D % 2 == 0, "head_dim must be even (RoPE rotate_half)"
     device = x.device
-    x = _require(x, "x", device)
-    w_q = _require(w_q, "w_q", device)
-    w_k = _require(w_k, "w_k", device)
-    w_v = _require(w_v, "w_v", device)
-    q_norm_w = _require(q_norm_w, "q_norm_w", device)
-    k_norm_w = _require(k_norm_w, "k_norm_w", device)
+    dtype = torch.float32 if isinstance(x, torch.Tensor) and x.dtype == torch.float32 else torch.bfloat16
+    x = _require(x, "x", device, dtype)
+    w_q = _require(w_q, "w_q", device, dtype)
+    w_k = _require(w_k, "w_k", device, dtype)
+    w_v = _require(w_v, "w_v", device, dtype)
+    q_norm_w = _require(q_norm_w, "q_norm_w", device, dtype)
+    k_norm_w = _require(k_norm_w, "k_norm_w", device, dtype)
     if w_q.shape != (H_Q * D, H) or w_k.shape != (H_KV * D, H) or w_v.shape != (H_KV * D, H):
         raise ValueError(
             f"weight shapes {tuple(w_q.shape)}, {tuple(w_k.shape)}, {tuple(w_v.shape)} do not match "
@@ -325,12 +341,13 @@ def fused_qkv_rope_ex(
     H_KV = w_k.shape[0] // D
     assert D % 2 == 0, "head_dim must be even (RoPE rotate_half)"
     device = x.device
-    x = _require(x, "x", device)
-    w_q = _require(w_q, "w_q", device)
-    w_k = _require(w_k, "w_k", device)
-    w_v = _require(w_v, "w_v", device)
-    q_norm_w = _require(q_norm_w, "q_norm_w", device)
-    k_norm_w = _require(k_norm_w, "k_norm_w", device)
+    dtype = torch.float32 if isinstance(x, torch.Tensor) and x.dtype == torch.float32 else torch.bfloat16
+    x = _require(x, "x", device, dtype)
+    w_q = _require(w_q, "w_q", device, dtype)
+    w_k = _require(w_k, "w_k", device, dtype)
+    w_v = _require(w_v, "w_v", device, dtype)
+    q_norm_w = _require(q_norm_w, "q_norm_w", device, dtype)
+    k_norm_w = _require(k_norm_w, "k_norm_w", device, dtype)
     if w_q.shape != (H_Q * D, H) or w_k.shape != (H_KV * D, H) or w_v.shape != (H_KV * D, H):
         raise ValueError(
             f"weight shapes {tuple(w_q.shape)}, {tuple(w_k.shape)}, {tuple(w_v.shape)} do not match "

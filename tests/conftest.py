@@ -92,7 +92,8 @@ def device():
 # Short names of the library's kernels, by (demangled or mangled) kernel name.
 _KERNEL_NAMES = (("decode_multi_kernel", "decode_multi"), ("decode_kernel", "decode"),
                  ("tile_dma_w4_kernel", "tile_w4"), ("tile_dma_split_kernel", "tile_split"), ("tile_dma_kernel", "tile"), ("tile_kernel", "tile_reg"),
-                 ("row_scale_kernel", "row_scale"), ("norm_rope_kernel", "norm_rope"))
+                 ("row_scale_kernel", "row_scale"), ("norm_rope_kernel", "norm_rope"),
+                 ("f32_qkv_kernel", "f32"))
 
 
 def _short_kernel_name(name: str):
@@ -105,7 +106,8 @@ def _short_kernel_name(name: str):
 def launched_kernels(fn, *, warm=True):
     """The library kernels one call of ``fn`` launches, in launch order, as
     short names ("decode" = one 64-row block, "decode_multi" = several blocks,
-    "tile", "tile_split" = split-K tile, "tile_w4", "tile_reg", "row_scale", "norm_rope"), recorded with torch.profiler (the reference counts its
+    "tile", "tile_split" = split-K tile, "tile_w4", "tile_reg", "row_scale", "norm_rope",
+    "f32" = the fp32 front), recorded with torch.profiler (the reference counts its
     kernels the same way, tests/test_fused_qkv_rope.py:287-311).  Other
     kernels (torch's own fills and copies) are left out."""
     from torch.profiler import ProfilerActivity, profile

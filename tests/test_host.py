@@ -242,6 +242,23 @@ def test_w4a16_validation(lib):
     assert call(M=0) == 0
 
 
+def test_f32_validation(lib):
+    """The fp32 entry point's checks run before any launch (fake pointers)."""
+    fake = 1 << 20
+    f = lambda T=4, hidden=1024, D=128, x=fake, q=fake, wq=fake, cr=8, S=4: lib.mqk_fused_qkv_rope_f32(
+        x, wq, fake, fake, fake, fake, fake, fake, None, T, S, hidden, 2, 1, D, cr, 1e-6, q, fake, fake, None)
+    assert f(D=96) == -3
+    assert f(D=127) == -2
+    assert f(hidden=48) == -3      # hidden % 32
+    assert f(x=None) == -1
+    assert f(wq=None) == -1
+    assert f(q=fake + 4) == -4
+    assert f(cr=0) == -2
+    assert f(S=0) == -2            # prefill mode needs S
+    assert f(T=0) == 0
+    assert f(T=-1) == -2
+
+
 def test_qk_norm_rope_validation(lib):
     fake = 1 << 20
     f = lambda T=4, Hq=2, Hkv=1, D=128, qr=fake: lib.mqk_qk_norm_rope_bf16(
