@@ -176,9 +176,19 @@ def call(device: torch.device, fn, *args) -> int:
     libmqk launches on the calling thread's current device, so a caller whose
     tensors live on another GPU than the current one (one process driving
     several GPUs) still gets the kernels on the tensors' device, next to the
-    stream and workspace that belong to it."""
+    stream and workspace that belong to it.  (The device is switched only when
+    it differs: the switch costs more host time than a decode kernel's launch.)"""
+    if torch.cuda.current_device() == device.index:
+        return fn(*args)
     with torch.cuda.device(device):
         return fn(*args)
+
+
+def stream_handle(device: torch.device) -> int:
+    """The raw hipStream_t of torch's current stream on ``device`` (what
+    ``torch.cuda.current_stream(device).cuda_stream`` returns, without building
+    the stream object on every call)."""
+    return int(torch._C._cuda_getCurrentRawStream(device.index))
 
 
 def check(status: int, what: str) -> None:
@@ -229,9 +239,19 @@ _retired: list = []
 
 
 def workspace(device: torch.device, stream, nbytes: int):
+    """The workspace of ``stream`` (a torch stream, or the raw handle of the
+    device's current stream) with at least ``nbytes`` bytes; None for 0."""
     if nbytes <= 0:
         return None
-    key = (device.index, int(stream.cuda_stream))
+    handle = stream if isinstance(stream, int) else int(stream.cuda_stream)
+    key = (device.index, handle)
+    buf = _workspaces.get(key)  # (the common case: an existing buffer that is large enough)
+    if buf is not None and buf.numel() >= nbytes:
+        return buf
+    if isinstance(stream, int):
+        stream = torch.cuda.current_stream(device)
+        if int(stream.cuda_stream) != handle:
+            raise MqkNativeError("a raw stream handle must be the device's current stream")
     with _ws_lock:
         buf = _workspaces.get(key)
         if buf is None or buf.numel() < nbytes:

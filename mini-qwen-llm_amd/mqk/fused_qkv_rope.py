@@ -46,26 +46,31 @@ EPS = 1e-6  # the reference hard-codes EPS=1e-6 (fused_qkv_rope.py:187)
 
 
 def _require(t: torch.Tensor, name: str, device: torch.device, dtype=torch.bfloat16) -> torch.Tensor:
+    # (integer device indices and no torch.device objects on the success path:
+    # these checks run for every tensor of every call)
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise ValueError(f"{name} must be on a GPU device, got {t.device}")
-    if t.device != device:
+    if t.get_device() != device.index:
         raise ValueError(f"{name} is on {t.device}, expected {device}")
     if dtype is not None and t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
-    return t.contiguous()
+    return t if t.is_contiguous() else t.contiguous()
 
 
 def _positions(positions: Optional[torch.Tensor], T: int, device) -> Optional[torch.Tensor]:
     if positions is None:
         return None
+    if not isinstance(positions, torch.Tensor):
+        raise TypeError("positions must be a torch.Tensor")
     if positions.dtype not in (torch.int32, torch.int64):
         raise TypeError(f"positions must be int32 (or int64), got {positions.dtype}")
-    positions = _require(positions, "positions", device, dtype=None).reshape(-1)
+    positions = _require(positions, "positions", device, dtype=None)
     if positions.numel() != T:
         raise ValueError(f"positions has {positions.numel()} entries, expected B*S = {T}")
-    return positions.to(torch.int32)
+    # (a contiguous tensor is read as its T entries in order, whatever its shape)
+    return positions if positions.dtype == torch.int32 else positions.to(torch.int32)
 
 
 def _rope_tables(cos, sin, D, device, dtype=torch.bfloat16):
@@ -120,14 +125,14 @@ def fused_qkv_rope(
         return q, k, v
 
     lib = _native.library()
-    stream = torch.cuda.current_stream(device)
+    stream = _native.stream_handle(device)
     if dtype == torch.float32:
         status = _native.call(
             device, lib.mqk_fused_qkv_rope_f32,
             x.data_ptr(), w_q.data_ptr(), w_k.data_ptr(), w_v.data_ptr(),
             q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), _native.ptr(pos),
             T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), stream.cuda_stream)
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), stream)
         _native.check(status, "mqk_fused_qkv_rope_f32")
         return q, k, v
     nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, H_Q, H_KV, H))
@@ -138,7 +143,7 @@ def fused_qkv_rope(
         q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), _native.ptr(pos),
         T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
         q.data_ptr(), k.data_ptr(), v.data_ptr(),
-        _native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
+        _native.ptr(ws), 0 if ws is None else ws.numel(), stream)
     _native.check(status, "mqk_fused_qkv_rope_bf16")
     return q, k, v
 
@@ -228,7 +233,7 @@ def fused_qkv_rope_paged(
     if T == 0:
         return q, k, v
     lib = _native.library()
-    stream = torch.cuda.current_stream(device)
+    stream = _native.stream_handle(device)
     nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, H_Q, H_KV, H))
     ws = _native.workspace(device, stream, nbytes)
     status = _native.call(device, lib.mqk_fused_qkv_rope_paged_bf16,
@@ -236,7 +241,7 @@ def fused_qkv_rope_paged(
         q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), _native.ptr(pos),
         T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
         q.data_ptr(), _native.ptr(k), _native.ptr(v), ctypes.byref(desc),
-        _native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
+        _native.ptr(ws), 0 if ws is None else ws.numel(), stream)
     _native.check(status, "mqk_fused_qkv_rope_paged_bf16")
     del keep
     return q, k, v
@@ -365,7 +370,7 @@ def fused_qkv_rope_ex(
     if T == 0:
         return q, k, v
     lib = _native.library()
-    stream = torch.cuda.current_stream(device)
+    stream = _native.stream_handle(device)
     nbytes = int(lib.mqk_fused_qkv_rope_ex_workspace_size(T, H_Q, H_KV, H, ctypes.byref(ext)))
     ws = _native.workspace(device, stream, nbytes)
     status = _native.call(device, lib.mqk_fused_qkv_rope_ex_bf16,
@@ -373,7 +378,7 @@ def fused_qkv_rope_ex(
         q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), _native.ptr(pos),
         T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
         q.data_ptr(), _native.ptr(k), _native.ptr(v), ctypes.byref(ext),
-        _native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
+        _native.ptr(ws), 0 if ws is None else ws.numel(), stream)
     _native.check(status, "mqk_fused_qkv_rope_ex_bf16")
     del keep
     return q, k, v
@@ -422,10 +427,10 @@ def qk_norm_rope(
     k_out = torch.empty_like(k_raw)
     if T == 0:
         return q_out, k_out
-    stream = torch.cuda.current_stream(device)
+    stream = _native.stream_handle(device)
     status = _native.call(device, _native.library().mqk_qk_norm_rope_bf16,
         q_raw.data_ptr(), k_raw.data_ptr(), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
         cos.data_ptr(), sin.data_ptr(), _native.ptr(pos), T, S, H_Q, H_KV, D, cos.shape[0],
-        float(eps), q_out.data_ptr(), k_out.data_ptr(), stream.cuda_stream)
+        float(eps), q_out.data_ptr(), k_out.data_ptr(), stream)
     _native.check(status, "mqk_qk_norm_rope_bf16")
     return q_out, k_out

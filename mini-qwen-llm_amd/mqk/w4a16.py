@@ -70,11 +70,11 @@ def w4a16_gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
     if M == 0:
         return out
     lib = _native.library()
-    stream = torch.cuda.current_stream(device)
+    stream = _native.stream_handle(device)
     ws = _native.workspace(device, stream, int(lib.mqk_w4a16_gemm_workspace_size(M, K, N)))
     status = _native.call(device, lib.mqk_w4a16_gemm_ex,
         x.data_ptr(), qweight.data_ptr(), scales.data_ptr(), qzeros.data_ptr(), M, K, N,
-        group_size, st, out.data_ptr(), _native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
+        group_size, st, out.data_ptr(), _native.ptr(ws), 0 if ws is None else ws.numel(), stream)
     _native.check(status, "mqk_w4a16_gemm_ex")
     return out
 
@@ -274,7 +274,7 @@ def _fused_w4a16(x, q_proj, k_proj, v_proj, q_norm_w, k_norm_w, cos, sin, positi
     if T == 0:
         return q, k, v
     lib = _native.library()
-    stream = torch.cuda.current_stream(device)
+    stream = _native.stream_handle(device)
     if ext is not None:
         nbytes = int(lib.mqk_fused_qkv_rope_ex_workspace_size(T, H_Q, H_KV, H, ctypes.byref(ext)))
     else:
@@ -285,7 +285,7 @@ def _fused_w4a16(x, q_proj, k_proj, v_proj, q_norm_w, k_norm_w, cos, sin, positi
             q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(),
             _native.ptr(pos), T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
             q.data_ptr(), _native.ptr(k), _native.ptr(v))
-    tail = (_native.ptr(ws), 0 if ws is None else ws.numel(), stream.cuda_stream)
+    tail = (_native.ptr(ws), 0 if ws is None else ws.numel(), stream)
     if ext is not None:
         status = _native.call(device, lib.mqk_fused_qkv_rope_ex_w4a16, *head, ctypes.byref(ext), *tail)
         _native.check(status, "mqk_fused_qkv_rope_ex_w4a16")

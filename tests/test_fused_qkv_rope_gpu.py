@@ -400,3 +400,45 @@ def test_large_t_64bit_offsets(device):
     ref = case.oracle(token_idx=idx)
     out = tuple(t.reshape(T, *t.shape[2:])[torch.as_tensor(idx)] for t in (q, k, v))
     _check(out, tuple(r[0] for r in ref), "T=270000")
+
+
+# ── argument checks of the Python shim (the reference asserts only an even D) ──
+
+def test_shim_rejects_bad_arguments(device):
+    import mqk
+    case = Case(1, 8, 1024, 16, 8, seed=140)
+    args = list(case.args(device))
+    bad = list(args)
+    bad[0] = case.x  # host tensor
+    with pytest.raises(ValueError, match="x must be on a GPU device"):
+        mqk.fused_qkv_rope(*bad)
+    bad = list(args)
+    bad[2] = bad[2].half()
+    with pytest.raises(TypeError, match="w_k must be torch.bfloat16"):
+        mqk.fused_qkv_rope(*bad)
+    with pytest.raises(TypeError, match="positions must be int32"):
+        mqk.fused_qkv_rope(*args[:8], torch.zeros(8, device=device))
+    with pytest.raises(ValueError, match="positions has 7 entries"):
+        mqk.fused_qkv_rope(*args[:8], torch.zeros(7, dtype=torch.int32, device=device))
+    with pytest.raises(ValueError, match="weight shapes"):
+        mqk.fused_qkv_rope(args[0], args[1][:, :512], *args[2:8])
+
+
+def test_shim_accepts_strided_and_int64_inputs(device):
+    """Non-contiguous inputs are made contiguous and int64 positions converted:
+    the result equals the call on contiguous int32 inputs bit for bit."""
+    import mqk
+    g = torch.Generator().manual_seed(141)
+    pos = torch.randint(0, 64, (16,), generator=g, dtype=torch.int32)
+    case = Case(16, 1, 1024, 16, 8, seed=141, rows=64, positions=pos)
+    args = list(case.args(device))
+    ref = mqk.fused_qkv_rope(*args)
+    strided = list(args)
+    strided[1] = args[1].t().contiguous().t()          # column-major w_q
+    strided[6] = torch.cat([args[6], args[6]], 1)[:, :HEAD_DIM]  # cos with row stride 2 * D
+    strided[8] = args[8].long()
+    assert not strided[1].is_contiguous() and not strided[6].is_contiguous()
+    out = mqk.fused_qkv_rope(*strided)
+    torch.cuda.synchronize()
+    for a, b in zip(out, ref):
+        assert torch.equal(a, b)

@@ -465,9 +465,11 @@ def test_ext_validation(lib):
 
 def test_native_call_makes_the_tensor_device_current(monkeypatch):
     """libmqk launches on the current HIP device: every launch goes through
-    _native.call, which enters torch.cuda.device(<the tensors' device>) around it."""
+    _native.call, which enters torch.cuda.device(<the tensors' device>) around it
+    when another device is current, and calls straight through otherwise."""
     from mqk import _native
     seen = []
+    monkeypatch.setattr(torch.cuda, "current_device", lambda: 0)
 
     class Recorder:
         def __init__(self, dev):
@@ -483,6 +485,9 @@ def test_native_call_makes_the_tensor_device_current(monkeypatch):
     r = _native.call(torch.device("cuda", 1), lambda a, b: seen.append(("launch", a, b)) or 7, 3, 4)
     assert r == 7
     assert seen == [("enter", "cuda:1"), ("launch", 3, 4), ("exit", "cuda:1")]
+    seen.clear()
+    assert _native.call(torch.device("cuda", 0), lambda a: seen.append(("launch", a)) or 8, 5) == 8
+    assert seen == [("launch", 5)]
 
 
 def test_every_launch_goes_through_native_call():
@@ -490,7 +495,7 @@ def test_every_launch_goes_through_native_call():
     import re
     pkg = ROOT / "mini-qwen-llm_amd" / "mqk"
     launching = re.compile(
-        r"\.(mqk_fused_qkv_rope(_paged|_ex)?_(bf16|w4a16)|mqk_w4a16_gemm(_ex)?|mqk_qk_norm_rope_bf16)\b")
+        r"\.(mqk_fused_qkv_rope(_paged|_ex)?_(bf16|w4a16|f32)|mqk_w4a16_gemm(_ex)?|mqk_qk_norm_rope_bf16)\b")
     launches = 0
     for f in pkg.glob("*.py"):
         if f.name == "_native.py":  # the ctypes signature table names every entry point
