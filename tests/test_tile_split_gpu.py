@@ -125,3 +125,21 @@ def test_split_tile_varlen_paged_input_norm(device):
     slots = _expected_slots(seq, posv, bt.numpy(), bs)
     _check_cache(kc, k, slots, "k cache")
     _check_cache(vc, v, slots, "v cache")
+
+
+@pytest.mark.parametrize("T,hidden,Hq,Hkv,plan", [
+    (128, 5120, 40, 8, "tile_split"), (768, 5120, 40, 8, "tile_split"), (1024, 5120, 40, 8, "tile_split"),
+    (512, 2048, 32, 4, "tile_split"), (1024, 2048, 32, 4, "tile_split"), (256, 1024, 16, 8, "tile_split"),
+    (384, 1024, 16, 8, "tile")])
+def test_default_plan_other_shapes_matches_oracle(T, hidden, Hq, Hkv, plan, device):
+    """The planner's own choices at the other Qwen3 attention shapes (Qwen3-14B
+    heads at hidden 5120, 30B-A3B at 2048, 0.6B at 1024), decode-style positions,
+    against the oracle; the plan is the one the refitted cost model picks there."""
+    import mqk
+    pos = torch.randint(0, 8192, (T,), generator=torch.Generator().manual_seed(T + hidden), dtype=torch.int32)
+    case = Case(1, T, hidden, Hq, Hkv, seed=2300 + T + hidden, rows=8192, positions=pos)
+    args = case.args(device)
+    assert launched_kernels(lambda: mqk.fused_qkv_rope(*args)) == [plan]
+    out = mqk.fused_qkv_rope(*args)
+    torch.cuda.synchronize()
+    _check_oracle(out, case, T, f"default plan T={T} hidden={hidden}")
