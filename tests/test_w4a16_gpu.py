@@ -192,6 +192,26 @@ def test_fused_w4a16(B, S, positions_mode, scale_dtype, device):
               f"w4a16 B={B} S={S}")
 
 
+@pytest.mark.parametrize("S,hidden,Hq,Hkv,plan", [
+    (256, 5120, 40, 8, ["decode"] * 4), (512, 5120, 40, 8, ["tile_w4"]), (1024, 1024, 16, 8, ["tile_w4"]),
+    (512, 1024, 16, 8, ["decode_multi"])])
+def test_fused_w4a16_default_plan_other_shapes(S, hidden, Hq, Hkv, plan, device):
+    """The int4 planner's choices at the other Qwen3 attention shapes, with
+    decode-style positions, against the oracle."""
+    import mqk
+    from conftest import launched_kernels
+    x, projs, gq, gk = _int4_case(1, S, hidden, Hq, Hkv, seed=S + hidden)
+    c, s = mqk.rope_tables(D, 8192)
+    cos, sin = c.bfloat16(), s.bfloat16()
+    pos = torch.randint(0, 8192, (S,), generator=torch.Generator().manual_seed(S + 1), dtype=torch.int32)
+    dp = [tuple(t.to(device) for t in p) for p in projs]
+    args = (x.to(device), *dp, gq.to(device), gk.to(device), cos.to(device), sin.to(device), pos.to(device))
+    assert launched_kernels(lambda: mqk.fused_qkv_rope_w4a16(*args)) == plan
+    out = mqk.fused_qkv_rope_w4a16(*args)
+    torch.cuda.synchronize()
+    _check_w4(out, x, projs, gq, gk, cos, sin, Hq, Hkv, pos.numpy(), f"w4a16 default plan S={S} hidden={hidden}")
+
+
 def test_config5_w4a16_ragged_full_size(device):
     """BASELINE config 5 at full size: Qwen3-8B dims (hidden 4096, 32/8 heads), AWQ
     int4 weights with random nibbles U{0..15}, fp16 scales U(0.005, 0.02), random
