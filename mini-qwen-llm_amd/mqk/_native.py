@@ -188,7 +188,13 @@ def stream_handle(device: torch.device) -> int:
     """The raw hipStream_t of torch's current stream on ``device`` (what
     ``torch.cuda.current_stream(device).cuda_stream`` returns, without building
     the stream object on every call)."""
-    return int(torch._C._cuda_getCurrentRawStream(device.index))
+    if _raw_stream is not None:
+        return int(_raw_stream(device.index))
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+# (torch's own accessor of the raw current stream; absent in some builds)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def check(status: int, what: str) -> None:

@@ -505,3 +505,18 @@ def test_every_launch_goes_through_native_call():
                 launches += 1
                 assert "_native.call(device, " in ln or ln.strip().startswith("device, lib."), f"{f.name}: {ln.strip()}"
     assert launches >= 8  # bf16 / paged / ex / qk-norm, int4 GEMM / plain / paged / ex
+
+
+def test_stream_handle_falls_back_to_the_public_api(monkeypatch):
+    """Without torch's raw-stream accessor the handle comes from
+    torch.cuda.current_stream(device).cuda_stream."""
+    from mqk import _native
+
+    class FakeStream:
+        cuda_stream = 12345
+
+    monkeypatch.setattr(_native, "_raw_stream", None)
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda dev=None: FakeStream())
+    assert _native.stream_handle(torch.device("cuda", 0)) == 12345
+    monkeypatch.setattr(_native, "_raw_stream", lambda idx: 777 + idx)
+    assert _native.stream_handle(torch.device("cuda", 1)) == 778
