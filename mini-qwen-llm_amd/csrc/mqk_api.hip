@@ -553,8 +553,10 @@ int mqk_fused_qkv_rope_f32(const float* x, const float* w_q, const float* w_k, c
   a.q = q;
   a.k = k;
   a.v = v;
-  return hip_status(launch_f32_qkv(a, device_topology().xcds, static_cast<hipStream_t>(stream)),
-                    "f32 front launch");
+  // 16-row tiles when 32-row tiles would leave CUs idle
+  const Topology topo = device_topology();
+  const int rows = (T + 31) / 32 * (Hq + 2 * Hkv) < topo.cus ? 16 : 32;
+  return hip_status(launch_f32_qkv(a, rows, topo.xcds, static_cast<hipStream_t>(stream)), "f32 front launch");
 }
 
 // ---- allocation-free variant of mqk_fused_qkv_rope_bf16 ---------------------------------

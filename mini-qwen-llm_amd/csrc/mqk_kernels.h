@@ -184,8 +184,8 @@ struct F32Args {
   int64_t n_seqs = 0;
   int64_t t0 = 0;
 };
-constexpr int kF32RowTile = 32;  // rows per workgroup of the fp32 kernel
 constexpr int kF32BK = 32;       // k extent of one staged fp32 tile
-hipError_t launch_f32_qkv(const F32Args& a, int xcds, hipStream_t stream);
+// rows: token rows per workgroup, 32 or 16
+hipError_t launch_f32_qkv(const F32Args& a, int rows, int xcds, hipStream_t stream);
 
 }  // namespace mqk

@@ -4,10 +4,10 @@
 // rotates and stores in fp32 (mini_qwen/kernels/fused_qkv_rope.py:84-127,
 // :167-173; the fp32 layer of the reference's CPU-runnable configuration).
 //
-// One workgroup of four waves computes 32 token rows x one head (128 columns):
-// each wave owns 32 columns and runs the fp32 matrix core
-// (v_mfma_f32_32x32x2_f32: products and sums in fp32) over k tiles of 32 staged
-// in LDS, the next tile's loads in registers under the current tile's MFMAs.
+// One workgroup of four waves computes 32 (or 16) token rows x one head (128
+// columns): each wave owns 32 columns and runs the fp32 matrix core (products
+// and sums in fp32) over k tiles of 32 staged in LDS, the next tile's loads in
+// registers under the current tile's MFMAs.
 // The accumulators then go through LDS so that eight threads hold a row's
 // 128 dims (each the RoPE pairs d, d+64 for eight d), apply RMSNorm and RoPE
 // in fp32, and store.
@@ -17,17 +17,21 @@
 namespace mqk {
 namespace {
 
-constexpr int kRows = kF32RowTile;
 constexpr int kKT = kF32BK;
 constexpr int kPitch = kKT + 1;          // LDS row pitch of the staged tiles (odd: no bank conflicts)
 constexpr int kEpiPitch = kHeadDim + 4;  // LDS row pitch of the accumulator tile
 constexpr int kThreads = 256;
-static_assert(kHeadDim * kPitch >= kRows * kEpiPitch, "the accumulator tile reuses the weight tile's LDS");
+static_assert(kHeadDim * kPitch >= 32 * kEpiPitch, "the accumulator tile reuses the weight tile's LDS");
 
+// ROWS = 32: each wave runs v_mfma_f32_32x32x2_f32 on its 32 x 32 block.
+// ROWS = 16 (launches whose 32-row tiles would leave CUs idle): each wave runs
+// v_mfma_f32_16x16x4_f32 on two 16 x 16 blocks.
+template <int ROWS>
 __global__ void __launch_bounds__(kThreads) f32_qkv_kernel(F32Args a, int xcds) {
-  __shared__ float xs[kRows * kPitch];
+  static_assert(ROWS == 16 || ROWS == 32, "row tile");
+  __shared__ float xs[ROWS * kPitch];
   __shared__ float ws[kHeadDim * kPitch];
-  const int n_rt = int((a.M + kRows - 1) / kRows);
+  const int n_rt = int((a.M + ROWS - 1) / ROWS);
   const int tile = xcd_tile_id(int(blockIdx.x), int(gridDim.x), xcds);
   const int rt = tile % n_rt;
   const int h = tile / n_rt;
@@ -35,12 +39,13 @@ __global__ void __launch_bounds__(kThreads) f32_qkv_kernel(F32Args a, int xcds) 
   split_head(h, a.Hq, a.Hkv, proj, hh);
   const float* W = a.w[proj] + int64_t(hh) * kHeadDim * a.K;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t row0 = int64_t(rt) * kRows;
+  const int64_t row0 = int64_t(rt) * ROWS;
 
-  // staging: thread tid loads 4 consecutive k of x row (tid / 8) and of weight
-  // rows (tid / 8) + 32 j, j = 0..3
+  // staging: thread tid loads 4 consecutive k of x row (tid / 8) (threads of
+  // rows < ROWS) and of weight rows (tid / 8) + 32 j, j = 0..3
   const int sr = tid >> 3, sk = (tid & 7) * 4;
-  const bool x_in = row0 + sr < a.M;
+  const bool x_row = sr < ROWS;
+  const bool x_in = x_row && row0 + sr < a.M;
   const float* xp = a.x + (x_in ? (row0 + sr) * a.K : 0) + sk;
   const float* wp = W + int64_t(sr) * a.K + sk;
   f32x4_t xr, wr[4];
@@ -50,41 +55,72 @@ __global__ void __launch_bounds__(kThreads) f32_qkv_kernel(F32Args a, int xcds) 
     for (int j = 0; j < 4; ++j) wr[j] = *reinterpret_cast<const f32x4_t*>(wp + int64_t(32 * j) * a.K + k0);
   };
   auto stage = [&]() {
+    if (x_row) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xs[sr * kPitch + sk + i] = xr[i];
+      for (int i = 0; i < 4; ++i) xs[sr * kPitch + sk + i] = xr[i];
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) ws[(sr + 32 * j) * kPitch + sk + i] = wr[j][i];
   };
 
-  f32x16_t acc;
+  float* ep = ws;  // (after the k loop) the accumulator tile [ROWS][kEpiPitch]
+  if constexpr (ROWS == 32) {
+    f32x16_t acc;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-  // lane l multiplies x row (l & 31) with weight row 32 * wave + (l & 31), at k
-  // slot (l >> 5) of each pair of k
-  const float* xa = xs + (lane & 31) * kPitch + (lane >> 5);
-  const float* wb = ws + (32 * wave + (lane & 31)) * kPitch + (lane >> 5);
-  load(0);
-  for (int64_t k0 = 0; k0 < a.K; k0 += kKT) {
-    stage();
-    __syncthreads();
-    if (k0 + kKT < a.K) load(k0 + kKT);
+    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+    // lane l multiplies x row (l & 31) with weight row 32 * wave + (l & 31), at k
+    // slot (l >> 5) of each pair of k
+    const float* xa = xs + (lane & 31) * kPitch + (lane >> 5);
+    const float* wb = ws + (32 * wave + (lane & 31)) * kPitch + (lane >> 5);
+    load(0);
+    for (int64_t k0 = 0; k0 < a.K; k0 += kKT) {
+      stage();
+      __syncthreads();
+      if (k0 + kKT < a.K) load(k0 + kKT);
 #pragma unroll
-    for (int kk = 0; kk < kKT / 2; ++kk)
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[2 * kk], wb[2 * kk], acc, 0, 0, 0);
-    __syncthreads();
+      for (int kk = 0; kk < kKT / 2; ++kk)
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[2 * kk], wb[2 * kk], acc, 0, 0, 0);
+      __syncthreads();
+    }
+    // accumulators -> LDS: acc[i] = C[8 * (i / 4) + 4 * (l >> 5) + i % 4][l & 31]
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      ep[(8 * (i >> 2) + 4 * (lane >> 5) + (i & 3)) * kEpiPitch + 32 * wave + (lane & 31)] = acc[i];
+  } else {
+    f32x4_t acc[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // lane l multiplies x row (l & 15) with weight rows 32 * wave + 16 b + (l & 15),
+    // at k slot (l >> 4) of each group of four k
+    const float* xa = xs + (lane & 15) * kPitch + (lane >> 4);
+    const float* wb = ws + (32 * wave + (lane & 15)) * kPitch + (lane >> 4);
+    load(0);
+    for (int64_t k0 = 0; k0 < a.K; k0 += kKT) {
+      stage();
+      __syncthreads();
+      if (k0 + kKT < a.K) load(k0 + kKT);
+#pragma unroll
+      for (int kk = 0; kk < kKT / 4; ++kk)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[4 * kk], wb[16 * b * kPitch + 4 * kk], acc[b], 0, 0, 0);
+      __syncthreads();
+    }
+    // accumulators -> LDS: acc[b][j] = C[4 * (l >> 4) + j][16 b + (l & 15)]
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        ep[(4 * (lane >> 4) + j) * kEpiPitch + 32 * wave + 16 * b + (lane & 15)] = acc[b][j];
   }
-
-  // accumulators -> LDS: acc[i] = C[8 * (i / 4) + 4 * (l >> 5) + i % 4][l & 31]
-  float* ep = ws;
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-    ep[(8 * (i >> 2) + 4 * (lane >> 5) + (i & 3)) * kEpiPitch + 32 * wave + (lane & 31)] = acc[i];
   __syncthreads();
 
-  // thread tid: row r = tid / 8, dims d = 8c .. 8c+7 and 64 + 8c .. (c = tid % 8)
+  // thread tid: row r = tid / 8, dims d = 8c .. 8c+7 and 64 + 8c .. (c = tid % 8);
+  // with 16-row tiles only the first two waves hold rows
   const int r = tid >> 3, c = tid & 7;
+  if (r >= ROWS) return;
   const int64_t t = row0 + r;
   float lo[8], hi[8];
 #pragma unroll
@@ -93,7 +129,7 @@ __global__ void __launch_bounds__(kThreads) f32_qkv_kernel(F32Args a, int xcds) 
     hi[i] = ep[r * kEpiPitch + kHalfDim + 8 * c + i];
   }
   if (proj < 2) {
-    // (every lane takes part in the 8-lane sum; rows past M hold zeros)
+    // (every lane of the row's 8-lane group takes part in the sum; rows past M hold zeros)
     const float ss = sum8_lanes(run_sumsq(lo, hi));
     const float rms = head_rms(ss, a.eps);
     if (t < a.M) {
@@ -122,11 +158,15 @@ __global__ void __launch_bounds__(kThreads) f32_qkv_kernel(F32Args a, int xcds) 
 
 }  // namespace
 
-hipError_t launch_f32_qkv(const F32Args& a, int xcds, hipStream_t stream) {
-  const int64_t n_rt = (a.M + kRows - 1) / kRows;
+hipError_t launch_f32_qkv(const F32Args& a, int rows, int xcds, hipStream_t stream) {
+  if (rows != 16 && rows != 32) return hipErrorInvalidValue;
+  const int64_t n_rt = (a.M + rows - 1) / rows;
   const int64_t blocks = n_rt * (a.Hq + 2 * a.Hkv);
   if (a.K % kKT != 0 || blocks <= 0 || blocks > (int64_t(1) << 31) - 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(f32_qkv_kernel, dim3(unsigned(blocks)), dim3(kThreads), 0, stream, a, xcds);
+  if (rows == 16)
+    hipLaunchKernelGGL(f32_qkv_kernel<16>, dim3(unsigned(blocks)), dim3(kThreads), 0, stream, a, xcds);
+  else
+    hipLaunchKernelGGL(f32_qkv_kernel<32>, dim3(unsigned(blocks)), dim3(kThreads), 0, stream, a, xcds);
   return hipGetLastError();
 }
 

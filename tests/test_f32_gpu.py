@@ -4,7 +4,8 @@ The reference op runs on fp32 tensors too (its fp32 layer is the
 CPU-runnable configuration, Qwen3-0.6B dims, B=1 x S=128): an fp32 GEMM
 (fused_qkv_rope.py:167-169), then the norm and RoPE of :84-127 in fp32 with
 fp32 stores.  The HIP path computes the projection on the fp32 matrix cores
-and the norm and RoPE in fp32.
+and the norm and RoPE in fp32, in 32-row tiles (v_mfma_f32_32x32x2_f32) or,
+when those would leave CUs idle, 16-row tiles (v_mfma_f32_16x16x4_f32).
 
 Tolerance, against the oracle in float64 on the same fp32 inputs: every
 product and partial sum of the projection rounds to fp32 (2^-24 relative), so
@@ -70,6 +71,8 @@ def _check(out, ref, label):
     (1, 40, 4096, 32, 8),    # Qwen3-8B dims
     (1, 64, 2048, 32, 4),    # GQA 8:1
     (3, 5, 2080, 2, 1),      # hidden a multiple of 32 only
+    (4, 128, 1024, 16, 8),   # enough 32-row tiles to fill the CUs (the others run 16-row tiles)
+    (1, 300, 2048, 32, 4),
 ])
 def test_f32_prefill(B, S, hidden, Hq, Hkv, device):
     import mqk
