@@ -143,3 +143,25 @@ def test_default_plan_other_shapes_matches_oracle(T, hidden, Hq, Hkv, plan, devi
     out = mqk.fused_qkv_rope(*args)
     torch.cuda.synchronize()
     _check_oracle(out, case, T, f"default plan T={T} hidden={hidden}")
+
+
+def test_split_tile_counts_recomputed_tiles(device):
+    """The statistics word counts the tiles a split-K launch finished on its
+    recompute path: none when every split ran on the XCD the grid assumes (an
+    unpartitioned MI355X), one per tile per call when the path is forced."""
+    import mqk
+    T, hidden, Hq, Hkv = 512, 4096, 32, 8
+    pos = torch.randint(0, 8192, (T,), generator=torch.Generator().manual_seed(77), dtype=torch.int32)
+    case = Case(1, T, hidden, Hq, Hkv, seed=2400, rows=8192, positions=pos)
+    args = case.args(device)
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        assert launched_kernels(lambda: mqk.fused_qkv_rope(*args)) == ["tile_split"]
+        want = mqk.fused_qkv_rope(*args)
+        natural = mqk.decode_recomputes(device, stream)
+        got = _with_options({"decode_force_recompute": 1}, lambda: [mqk.fused_qkv_rope(*args) for _ in range(2)])
+        after = mqk.decode_recomputes(device, stream)
+    assert natural == 0
+    assert after == 2 * (T // 128) * ((Hq + 2 * Hkv) // 3)  # 4 row tiles x 16 head tiles per call
+    for g in got:
+        assert all(torch.equal(a, b) for a, b in zip(g, want))
