@@ -49,7 +49,13 @@ constexpr int kDecRows = 64;            // token rows per block (one block per c
 constexpr int kDecMaxBlocks = 16;       // most 64-row blocks one launch streams the weights for
 constexpr int kDecThreads = 512;        // 8 waves; wave w owns columns [16w, 16w+16) of the head
 constexpr int kDecWaves = kDecThreads / 64;
-constexpr int kDecMaxNK = 16;           // largest k-range of one split, in 64-wide tiles
+constexpr int kDecMaxNK = 16;           // k tiles of one x slice in LDS (64-wide tiles)
+// Longest k range of a split in a launch of one block, bf16 weights: two x
+// slices, staged one after the other (wider models, e.g. hidden 5120 with 56
+// heads, then keep one workgroup per CU with 4 splits of 20 tiles instead of 5
+// splits over two rounds).  int4 weights keep one slice (the second slice's
+// dequantisation registers spill).
+constexpr int kDecLongMaxNK = 2 * kDecMaxNK;
 constexpr int kDecLookahead = 6;        // weight tiles in flight per wave
 // Longest k range (in 64-wide tiles) of a split in a launch of several blocks:
 // beyond it the held weights and the finisher no longer fit the 256 VGPRs of a
@@ -260,6 +266,44 @@ __device__ void partial_any(const ProblemArgs& p, const WeightArgs& w, int proj,
   }
 }
 
+// partial_any over a range longer than one x slice: slices of kDecMaxNK tiles,
+// each staged once every wave is done with the previous one, the tiles
+// accumulated in order into one sum (the arithmetic of the two-slice split).
+template <bool INT4, bool INORM>
+__device__ void partial_any_long(const ProblemArgs& p, const WeightArgs& w, int proj, int hh, int kt0, int nk,
+                                 const uint16_t* xs, uint32_t xs_lds, f32x4_t (&acc)[4], int r0) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c16 = lane & 15, g4 = lane >> 4;
+  const int64_t col = int64_t(hh) * kHeadDim + wave * 16 + c16;
+  zero_acc(acc);
+  for (int c0 = 0; c0 < nk; c0 += kDecMaxNK) {
+    const int cn = nk - c0 < kDecMaxNK ? nk - c0 : kDecMaxNK;
+    const int64_t kbeg = int64_t(kt0 + c0) * kBK;
+    if (c0 > 0) barrier();  // every wave is done with the previous slice
+    for (int t = 0; t < cn; ++t) stage_x_tile(p, kbeg, t, xs_lds, r0);
+    wait_vm<0>();
+    if (INORM) norm_x_tiles(p, const_cast<uint16_t*>(xs), kbeg, cn, r0);  // gamma is in LDS already
+    barrier();
+    for (int t = 0; t < cn; ++t) {
+      const int64_t k0 = kbeg + int64_t(t) * kBK;
+      u32x4_t b[2];
+      if constexpr (!INT4) {
+        const uint16_t* wp = w.w[proj] + col * p.K + k0 + g4 * 8;
+        b[0] = *reinterpret_cast<const u32x4_t*>(wp);
+        b[1] = *reinterpret_cast<const u32x4_t*>(wp + 32);
+      } else {
+        const Int4Col ic = int4_col(w, proj, col);
+        const int64_t grp = k0 / ic.group;
+        const uint32_t q[2] = {uint32_t(ic.qw[(k0 / 8 + g4) * ic.n + col]),
+                               uint32_t(ic.qw[(k0 / 8 + 4 + g4) * ic.n + col])};
+        dequant_tile(ic, q, ic.sc[grp * ic.n + col], uint32_t(ic.qz[grp * (ic.n / 8) + col / 8]), b);
+      }
+      mma_tile(xs, t, b, acc);
+    }
+  }
+}
+
 // What a workgroup works on: split `split` of head (128-column tile) `head`,
 // projection `proj` / head `hh` inside it, for the launch's `nblk` 64-row blocks.
 struct DecWork {
@@ -283,7 +327,7 @@ __device__ __forceinline__ bool any_foreign(uint32_t v) { return ((v >> 16) & 0x
 // in split order (RECOMPUTE: recomputes them all), applies RMSNorm + RoPE (Q/K),
 // stores the bf16 rows and resets the block's arrival counter.  prow / cslot:
 // RoPE-table offset and paged-cache slot of this thread's row of the block.
-template <bool INT4, bool INORM, bool MULTI, bool RECOMPUTE>
+template <bool INT4, bool INORM, bool MULTI, bool RECOMPUTE, bool LONG = false>
 __device__ __forceinline__ void finish_block(const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                                              const DecWork& d, int blk, const f32x4_t (&acc)[4], int64_t prow,
                                              int64_t cslot, uint16_t* xs, float* __restrict__ part,
@@ -363,7 +407,8 @@ __device__ __forceinline__ void finish_block(const ProblemArgs& p, const WeightA
       split_range(s, d.splits, nkt, s_kt0, s_nk);
       __syncthreads();  // every wave is done with the x slice of the previous split
       f32x4_t part_s[4];
-      partial_any<INT4, INORM>(p, w, d.proj, d.hh, s_kt0, s_nk, xs, xs_lds, part_s, blk * kDecRows);
+      if constexpr (LONG) partial_any_long<INT4, INORM>(p, w, d.proj, d.hh, s_kt0, s_nk, xs, xs_lds, part_s, blk * kDecRows);
+      else partial_any<INT4, INORM>(p, w, d.proj, d.hh, s_kt0, s_nk, xs, xs_lds, part_s, blk * kDecRows);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) sum[mb] += part_s[mb];
     }
@@ -589,7 +634,12 @@ __device__ __forceinline__ void block_rows(const EpilogueArgs& e, const DecWork&
 // One 64-row block (T <= 64): the split's partial, then the last split to arrive
 // finishes the head (from the partials, or by recomputation when some split ran
 // on another XCD).
-template <bool INT4, bool INORM, int NK>
+// A split of NK + NK2 tiles (NK2 > 0) runs as two slices: the second x slice is
+// staged once every wave is done with the first, and its tiles accumulate after
+// the first's, so the order of the sums is that of one NK + NK2 slice.
+// (LONG: some split of the launch is longer than one x slice, so the recompute
+// path runs every split's range in slices.)
+template <bool INT4, bool INORM, int NK, int NK2 = 0, bool LONG = (NK2 > 0)>
 __device__ __forceinline__ void run_split_single(const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                                                  const DecWork& d, int kt0, uint16_t* xs, uint32_t* arrival,
                                                  float* __restrict__ part, uint32_t* __restrict__ counters) {
@@ -599,6 +649,11 @@ __device__ __forceinline__ void run_split_single(const ProblemArgs& p, const Wei
   f32x4_t acc[4];
   zero_acc(acc);
   first_block<INT4, INORM, NK>(p, w, d, kt0, xs, hw, acc);
+  if constexpr (NK2 > 0) {
+    __syncthreads();  // every wave is done with the first x slice
+    HeldWeights<NK2> hw2;
+    first_block<INT4, INORM, NK2>(p, w, d, kt0 + NK, xs, hw2, acc);
+  }
   publish_partial(p, d, 0, acc, part);
   __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have reached the L2
   __syncthreads();                // ... and every thread's
@@ -606,8 +661,8 @@ __device__ __forceinline__ void run_split_single(const ProblemArgs& p, const Wei
   __syncthreads();
   const uint32_t seen = arrival[0];
   if (!all_arrived(seen, d.splits)) return;
-  if (any_foreign(seen)) finish_block<INT4, INORM, false, true>(p, w, e, d, 0, acc, prow, cslot, xs, part, counters);
-  else finish_block<INT4, INORM, false, false>(p, w, e, d, 0, acc, prow, cslot, xs, part, counters);
+  if (any_foreign(seen)) finish_block<INT4, INORM, false, true, LONG>(p, w, e, d, 0, acc, prow, cslot, xs, part, counters);
+  else finish_block<INT4, INORM, false, false, LONG>(p, w, e, d, 0, acc, prow, cslot, xs, part, counters);
 }
 
 // Several 64-row blocks.  Block 0 streams the weights into registers; each later
@@ -788,6 +843,33 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   }
 }
 
+// One 64-row block whose splits are longer than one x slice (bf16 weights,
+// kDecMaxNK < nk <= kDecLongMaxNK): a kernel of its own, so that the kernel
+// above keeps its code and register allocation.
+template <bool INORM>
+__global__ void __launch_bounds__(kDecThreads, 1)
+decode_long_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __restrict__ part,
+                   uint32_t* __restrict__ counters, int ctl) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[kDecRows * kDecKc];
+  __shared__ uint32_t arrival[2];
+  if ((blockIdx.x / p.xcds / splits) * p.xcds + blockIdx.x % p.xcds >= p.n_tiles) return;  // padding
+  int kt0, nk;
+  const DecWork d = dec_work(p, e, splits, ctl, kt0, nk);
+  switch (nk) {
+    // (balanced ranges: a launch whose longest split exceeds one slice has splits
+    // of at least kDecMaxNK tiles)
+    case kDecMaxNK: run_split_single<false, INORM, kDecMaxNK, 0, true>(p, w, e, d, kt0, xs, arrival, part, counters); break;
+#define MQK_DEC_LONG(n) \
+  case n: run_split_single<false, INORM, kDecMaxNK, n - kDecMaxNK>(p, w, e, d, kt0, xs, arrival, part, counters); break;
+    MQK_DEC_LONG(17) MQK_DEC_LONG(18) MQK_DEC_LONG(19) MQK_DEC_LONG(20)
+    MQK_DEC_LONG(21) MQK_DEC_LONG(22) MQK_DEC_LONG(23) MQK_DEC_LONG(24)
+    MQK_DEC_LONG(25) MQK_DEC_LONG(26) MQK_DEC_LONG(27) MQK_DEC_LONG(28)
+    MQK_DEC_LONG(29) MQK_DEC_LONG(30) MQK_DEC_LONG(31) MQK_DEC_LONG(32)
+#undef MQK_DEC_LONG
+    default: break;  // the launcher guarantees kDecMaxNK <= nk <= kDecLongMaxNK
+  }
+}
+
 // Several 64-row blocks, the weights held in registers across them.  Its splits
 // cover NKC or NKC - 1 k tiles (balanced ranges), and each NKC is its own kernel
 // so that the register allocation of the held weights fits the actual k range.
@@ -809,11 +891,12 @@ decode_multi_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, flo
 int g_decode_force_recompute = 0;
 int g_decode_max_spins = kDecMaxSpins;
 
-int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested, int cus, int xcds) {
+int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested, int cus, int xcds, bool int4) {
   (void)M;
   const int nkt = int(K / kBK);
   if (nkt < 1) return 0;
-  const int min_splits = (nkt + kDecMaxNK - 1) / kDecMaxNK;  // LDS bound on a split's k-range
+  const int max_nk = int4 ? kDecMaxNK : kDecLongMaxNK;
+  const int min_splits = (nkt + max_nk - 1) / max_nk;  // bound on a split's k-range
   int s = requested;
   if (s <= 0) {
     // one workgroup per CU: (heads per XCD) x splits <= CUs per XCD
@@ -857,7 +940,8 @@ hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, co
                          int splits, void* workspace, hipStream_t stream) {
   const int nkt = int(p.K / kBK);
   const int blocks = int((p.M + kDecRows - 1) / kDecRows);  // 64-row blocks of this launch
-  if (splits < 1 || splits > kDecMaxNK || splits > nkt || (nkt + splits - 1) / splits > kDecMaxNK ||
+  if (splits < 1 || splits > kDecMaxNK || splits > nkt ||
+      (nkt + splits - 1) / splits > (blocks > 1 ? kDecMultiMaxNK : (int4 ? kDecMaxNK : kDecLongMaxNK)) ||
       p.n_tiles > kMaxHeads || blocks < 1 || blocks > decode_max_blocks(p.n_tiles, p.K, splits, int4 && p.in_gamma) || p.xcds < 1)
     return hipErrorInvalidValue;
   uint32_t* counters = static_cast<uint32_t*>(workspace);
@@ -887,7 +971,8 @@ hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, co
 #undef MQK_MULTI
   const int variant = (int4 ? 2 : 0) + (p.in_gamma ? 1 : 0);
   const int nkc = (nkt + splits - 1) / splits;  // longest k range of a split, in tiles
-  Kernel kernel = blocks > 1 ? multi[nkc - 1][variant] : single[variant];
+  static const Kernel longk[2] = {decode_long_kernel<false>, decode_long_kernel<true>};
+  Kernel kernel = blocks > 1 ? multi[nkc - 1][variant] : (nkc > kDecMaxNK ? longk[p.in_gamma ? 1 : 0] : single[variant]);
   if (!kernel) return hipErrorInvalidValue;
   hipLaunchKernelGGL(kernel, grid, dim3(kDecThreads), dyn, stream, p, w, e, splits, part, counters, fr);
   return hipGetLastError();
