@@ -229,7 +229,10 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
   // (int4's first block is bound by the 64-k tiles each split dequantises and
   // multiplies, ~1.45 us each, over a ~14.5 us floor)
   const int64_t split_kt = blk_splits > 0 ? (K / 64 + blk_splits - 1) / blk_splits : 0;
-  const double dec_us = int4 ? std::max(14.5, 1.45 * double(split_kt)) : 14.2 + 0.187 * w_bytes * 1e-6;
+  // (splits longer than a launch of several blocks takes run one block per launch,
+  // each ~7.5 + 0.65 us per k tile: 20.5 / 21.3 / 25.1 us at 20 / 22 / 27 tiles)
+  const double dec_us = !int4 ? 14.2 + 0.187 * w_bytes * 1e-6
+                              : (split_kt > 13 ? 7.5 + 0.65 * double(split_kt) : std::max(14.5, 1.45 * double(split_kt)));
   const double pass_us = int4 ? 1.95 + 0.71 * double(K) / 1024.0 : 2.17 + 0.584 * double(K) / 1024.0;
   const double blocks_us = double(launches) * dec_us + double(nblk - launches) * pass_us;
   const double tile_us = int4 ? double(K) / 64.0 * 2.1 + 7.0 : double(K) / 64.0 * (n_tiles % 3 == 0 ? 1.15 : 1.27) + 5.0;

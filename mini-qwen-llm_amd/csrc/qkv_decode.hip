@@ -50,11 +50,10 @@ constexpr int kDecMaxBlocks = 16;       // most 64-row blocks one launch streams
 constexpr int kDecThreads = 512;        // 8 waves; wave w owns columns [16w, 16w+16) of the head
 constexpr int kDecWaves = kDecThreads / 64;
 constexpr int kDecMaxNK = 16;           // k tiles of one x slice in LDS (64-wide tiles)
-// Longest k range of a split in a launch of one block, bf16 weights: two x
-// slices, staged one after the other (wider models, e.g. hidden 5120 with 56
-// heads, then keep one workgroup per CU with 4 splits of 20 tiles instead of 5
-// splits over two rounds).  int4 weights keep one slice (the second slice's
-// dequantisation registers spill).
+// Longest k range of a split in a launch of one block: two x slices, staged
+// one after the other (wider models, e.g. hidden 5120 with 56 heads, then keep
+// one workgroup per CU with 4 splits of 20 tiles instead of 5 splits over two
+// rounds).
 constexpr int kDecLongMaxNK = 2 * kDecMaxNK;
 constexpr int kDecLookahead = 6;        // weight tiles in flight per wave
 // Longest k range (in 64-wide tiles) of a split in a launch of several blocks:
@@ -843,10 +842,10 @@ decode_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __
   }
 }
 
-// One 64-row block whose splits are longer than one x slice (bf16 weights,
-// kDecMaxNK < nk <= kDecLongMaxNK): a kernel of its own, so that the kernel
-// above keeps its code and register allocation.
-template <bool INORM>
+// One 64-row block whose splits are longer than one x slice
+// (kDecMaxNK < nk <= kDecLongMaxNK for the longest): a kernel of its own, so
+// that the kernel above keeps its code and register allocation.
+template <bool INT4, bool INORM>
 __global__ void __launch_bounds__(kDecThreads, 1)
 decode_long_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, float* __restrict__ part,
                    uint32_t* __restrict__ counters, int ctl) {
@@ -855,13 +854,17 @@ decode_long_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, floa
   if ((blockIdx.x / p.xcds / splits) * p.xcds + blockIdx.x % p.xcds >= p.n_tiles) return;  // padding
   int kt0, nk;
   const DecWork d = dec_work(p, e, splits, ctl, kt0, nk);
+  // bf16: a first slice of kDecMaxNK tiles; int4: two halves (a 16-tile first
+  // slice keeps too many packed words live and spills)
+  constexpr auto first = [](int n) { return INT4 ? (n + 1) / 2 : (n > kDecMaxNK ? kDecMaxNK : n); };
   switch (nk) {
     // (balanced ranges: a launch whose longest split exceeds one slice has splits
     // of at least kDecMaxNK tiles)
-    case kDecMaxNK: run_split_single<false, INORM, kDecMaxNK, 0, true>(p, w, e, d, kt0, xs, arrival, part, counters); break;
-#define MQK_DEC_LONG(n) \
-  case n: run_split_single<false, INORM, kDecMaxNK, n - kDecMaxNK>(p, w, e, d, kt0, xs, arrival, part, counters); break;
-    MQK_DEC_LONG(17) MQK_DEC_LONG(18) MQK_DEC_LONG(19) MQK_DEC_LONG(20)
+#define MQK_DEC_LONG(n)                                                                                          \
+  case n:                                                                                                         \
+    run_split_single<INT4, INORM, first(n), n - first(n), true>(p, w, e, d, kt0, xs, arrival, part, counters);   \
+    break;
+    MQK_DEC_LONG(16) MQK_DEC_LONG(17) MQK_DEC_LONG(18) MQK_DEC_LONG(19) MQK_DEC_LONG(20)
     MQK_DEC_LONG(21) MQK_DEC_LONG(22) MQK_DEC_LONG(23) MQK_DEC_LONG(24)
     MQK_DEC_LONG(25) MQK_DEC_LONG(26) MQK_DEC_LONG(27) MQK_DEC_LONG(28)
     MQK_DEC_LONG(29) MQK_DEC_LONG(30) MQK_DEC_LONG(31) MQK_DEC_LONG(32)
@@ -895,7 +898,8 @@ int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested, int cus,
   (void)M;
   const int nkt = int(K / kBK);
   if (nkt < 1) return 0;
-  const int max_nk = int4 ? kDecMaxNK : kDecLongMaxNK;
+  (void)int4;  // (both weight formats take splits of up to two x slices)
+  const int max_nk = kDecLongMaxNK;
   const int min_splits = (nkt + max_nk - 1) / max_nk;  // bound on a split's k-range
   int s = requested;
   if (s <= 0) {
@@ -941,7 +945,7 @@ hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, co
   const int nkt = int(p.K / kBK);
   const int blocks = int((p.M + kDecRows - 1) / kDecRows);  // 64-row blocks of this launch
   if (splits < 1 || splits > kDecMaxNK || splits > nkt ||
-      (nkt + splits - 1) / splits > (blocks > 1 ? kDecMultiMaxNK : (int4 ? kDecMaxNK : kDecLongMaxNK)) ||
+      (nkt + splits - 1) / splits > (blocks > 1 ? kDecMultiMaxNK : kDecLongMaxNK) ||
       p.n_tiles > kMaxHeads || blocks < 1 || blocks > decode_max_blocks(p.n_tiles, p.K, splits, int4 && p.in_gamma) || p.xcds < 1)
     return hipErrorInvalidValue;
   uint32_t* counters = static_cast<uint32_t*>(workspace);
@@ -971,8 +975,9 @@ hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, co
 #undef MQK_MULTI
   const int variant = (int4 ? 2 : 0) + (p.in_gamma ? 1 : 0);
   const int nkc = (nkt + splits - 1) / splits;  // longest k range of a split, in tiles
-  static const Kernel longk[2] = {decode_long_kernel<false>, decode_long_kernel<true>};
-  Kernel kernel = blocks > 1 ? multi[nkc - 1][variant] : (nkc > kDecMaxNK ? longk[p.in_gamma ? 1 : 0] : single[variant]);
+  static const Kernel longk[4] = {decode_long_kernel<false, false>, decode_long_kernel<false, true>,
+                                  decode_long_kernel<true, false>, decode_long_kernel<true, true>};
+  Kernel kernel = blocks > 1 ? multi[nkc - 1][variant] : (nkc > kDecMaxNK ? longk[variant] : single[variant]);
   if (!kernel) return hipErrorInvalidValue;
   hipLaunchKernelGGL(kernel, grid, dim3(kDecThreads), dyn, stream, p, w, e, splits, part, counters, fr);
   return hipGetLastError();

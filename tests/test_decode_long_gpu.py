@@ -82,3 +82,27 @@ def test_long_splits_with_input_norm(device):
     for a, b, c in zip(got, ref, rec):
         assert torch.equal(a, c)
         assert orc.max_abs(f32(a), f32(b)) <= 2e-2 and orc.rel_l2(f32(a), f32(b)) <= 1e-2
+
+
+@pytest.mark.parametrize("T,hidden,hq,hkv", [(64, 5120, 40, 8), (17, 4096, 64, 4)])
+def test_long_splits_int4(T, hidden, hq, hkv, device):
+    """int4 weights (dequantised per tile, splits run in two halves) against the
+    oracle, with the recompute and hand-off paths bit-identical."""
+    import mqk
+    case = _case(T, hidden, hq, hkv, seed=4200 + T)
+    args = case.args(device)
+    projs = [tuple(t.to(device) for t in mqk.per_group_minmax_quantize(w.float().T.contiguous(), 128, torch.bfloat16))
+             for w in (case.w_q, case.w_k, case.w_v)]
+    call = lambda: mqk.fused_qkv_rope_w4a16(args[0], *projs, *args[4:])
+    assert launched_kernels(call) == ["decode"]
+    want = _opts({}, call)
+    ref = orc.fused_qkv_rope_w4a16(f32(case.x).reshape(1, T, hidden), [p[0].cpu().numpy() for p in projs],
+                                   [p[1].float().cpu().numpy() for p in projs], [p[2].cpu().numpy() for p in projs],
+                                   f32(case.q_norm_w), f32(case.k_norm_w), f32(case.cos), f32(case.sin), hq, hkv,
+                                   positions=case.positions.numpy(), round_weight=True)
+    for name, o, r in zip("qkv", want, ref):
+        o = f32(o).reshape(r.shape)
+        assert orc.max_abs(o, r) <= 2e-2 and orc.rel_l2(o, r) <= 1e-2, name
+    for extra in ({"decode_force_recompute": 1}, {"decode_max_spins": 0}):
+        got = _opts(extra, call)
+        assert all(torch.equal(a, b) for a, b in zip(got, want)), extra

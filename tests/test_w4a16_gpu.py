@@ -193,7 +193,7 @@ def test_fused_w4a16(B, S, positions_mode, scale_dtype, device):
 
 
 @pytest.mark.parametrize("S,hidden,Hq,Hkv,plan", [
-    (256, 5120, 40, 8, ["decode"] * 4), (512, 5120, 40, 8, ["tile_w4"]), (1024, 1024, 16, 8, ["tile_w4"]),
+    (256, 5120, 40, 8, ["decode"] * 4), (768, 5120, 40, 8, ["tile_w4"]), (1024, 1024, 16, 8, ["tile_w4"]),
     (512, 1024, 16, 8, ["decode_multi"])])
 def test_fused_w4a16_default_plan_other_shapes(S, hidden, Hq, Hkv, plan, device):
     """The int4 planner's choices at the other Qwen3 attention shapes, with
