@@ -87,6 +87,14 @@ def test_noalloc_prefill_then_decode(device):
     _pair(_decode_case(40, 506, hidden=1024, Hq=16, Hkv=8), device)
 
 
+def test_noalloc_wide_model_decode(device):
+    """Qwen3-14B heads at hidden 5120 (the decode launch with splits of two x
+    slices: 56 heads x 4 splits, 7 MiB of partials, within the fixed scratch),
+    then a smaller call."""
+    _pair(_decode_case(64, 508, hidden=5120, Hq=40, Hkv=8), device)
+    _pair(_decode_case(9, 509, hidden=5120, Hq=40, Hkv=8), device)
+
+
 def test_noalloc_rejects_oversized_decode(device):
     """1024 heads at hidden 1024: one split each, 32 MiB of partials: rejected
     with MQK_ERR_WORKSPACE before any launch; the outputs stay untouched."""
