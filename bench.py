@@ -2,7 +2,7 @@
 """Benchmark of the fused QKV + QK-Norm + RoPE op on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
-    python bench.py --only {c1f32,c2f32,c2,c3,c4,c5,mid,mid256,mid128,gemm,copy} --steps K   # one workload, for profiler runs
+    python bench.py --only {c1f32,c2f32,d14b,c2,c3,c4,c5,mid,mid256,mid128,gemm,copy} --steps K   # one workload, for profiler runs
 
 Headline (``value``): BASELINE config 2, Qwen3-8B prefill B=4 x S=512 (2048
 tokens, hidden 4096, 32 Q heads, 8 KV heads, head_dim 128, bf16), tokens/s of
@@ -290,7 +290,7 @@ def copy_kernel(nbytes, steps, dev):
     torch.cuda.synchronize()
 
 
-WORKLOADS = ("c1f32", "c2f32", "c2", "c3", "c4", "c5", "mid", "mid256", "mid128", "gemm", "copy")
+WORKLOADS = ("c1f32", "c2f32", "d14b", "c2", "c3", "c4", "c5", "mid", "mid256", "mid128", "gemm", "copy")
 
 
 def run_only(name, steps, warmup, dev):
@@ -298,6 +298,8 @@ def run_only(name, steps, warmup, dev):
     B, S, hidden, Hq, Hkv = 4, 512, 4096, 32, 8
     if name == "c1f32":  # config 1 in fp32 (the fp32 front)
         ms, _ = bench_prefill(128, 1, 128, 1024, 16, 8, 0, steps, warmup, dev, fp32=True)
+    elif name == "d14b":  # a 64-token decode step at Qwen3-14B dims (splits of two x slices)
+        ms, _ = bench_decode(64, 5120, 40, 8, 2, steps, warmup, dev)
     elif name == "c2f32":  # config 2's shape in fp32 (the fp32 front at an MFMA-bound size)
         ms, _ = bench_prefill(B * S, B, S, hidden, Hq, Hkv, 1, steps, warmup, dev, fp32=True)
     elif name == "c2":
