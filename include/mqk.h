@@ -306,7 +306,8 @@ int mqk_fused_qkv_rope_ex_w4a16(const mqk_bf16* x, const int32_t* qw_q, const vo
  *   "decode_max_t"   largest T routed to the split-K decode kernel (0..64, default 64;
  *                    0 disables it)
  *   "decode_splits"  0 = auto, otherwise the split-K factor of the decode kernel (1..16,
- *                    at most 16 64-wide k tiles per split; otherwise the tile kernel runs)
+ *                    at most 32 64-wide k tiles per split, 13 when a launch covers several
+ *                    64-row blocks; otherwise the tile kernel runs)
  *   "group_m"        row tiles per tile-ordering group of the tile kernel (default 8)
  *   "tail_split"     1 (default): when the last, partial row tile of a prefill holds at most 64
  *                    rows and would cost a whole extra round of tiles over the CUs, those rows
