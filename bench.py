@@ -395,6 +395,13 @@ def main(argv=None) -> int:
                                      "frac": round(dgbs / PEAK_HBM_GBS, 4),
                                      "traffic": load_traffic("qkv_decode_c3_traffic")}
         log(f"[bench] config 3 decode: {dms * 1e3:.2f} us per launch, {dgbs:.0f} GB/s")
+        # a decode step of a wider model (Qwen3-14B heads, hidden 5120): splits of two x slices
+        wms, _ = bench_decode(64, 5120, 40, 8, 2, max(50, args.steps), 300, dev)
+        wgbs = decode_bytes(64, 5120, 56 * D) / (wms * 1e-3) / 1e9
+        sec["decode_qwen3_14b_b64"] = {"tokens_per_s": round(64 / (wms * 1e-3), 1), "ms_per_step": round(wms, 6),
+                                       "bound": "hbm", "achieved_GBps": round(wgbs, 1),
+                                       "frac": round(wgbs / PEAK_HBM_GBS, 4)}
+        log(f"[bench] Qwen3-14B decode: {wms * 1e3:.2f} us per launch, {wgbs:.0f} GB/s")
         # config 4: 30B-A3B attention shapes, S=8192
         h4, q4, kv4 = 2048, 32, 4
         n4 = (q4 + 2 * kv4) * D
