@@ -40,6 +40,40 @@ def test_graph_replay_matches_eager(B, S, device):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("int4", [False, True])
+def test_graph_replay_long_split_decode(int4, device):
+    """A decode step at Qwen3-14B dims (splits of two x slices, `decode_long_kernel`)
+    captured and replayed, bf16 and int4 weights."""
+    import mqk
+    from conftest import launched_kernels
+    case = Case(32, 1, 5120, 40, 8, seed=1990 + int4, rows=4096,
+                positions=torch.randint(0, 4096, (32,), generator=torch.Generator().manual_seed(7), dtype=torch.int32))
+    x, wq, wk, wv, gq, gk, cos, sin, pos = case.args(device)
+    if int4:
+        projs = [tuple(t.to(device) for t in mqk.per_group_minmax_quantize(w.float().T.contiguous(), 128,
+                                                                            torch.bfloat16))
+                 for w in (case.w_q, case.w_k, case.w_v)]
+        call = lambda: mqk.fused_qkv_rope_w4a16(x, *projs, gq, gk, cos, sin, pos)
+    else:
+        call = lambda: mqk.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin, pos)
+    assert launched_kernels(call) == ["decode"]
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        eager = call()
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = call()
+    for _ in range(3):
+        for t in out:
+            t.fill_(0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(out, eager))
+        call()  # eager work between replays
+        torch.cuda.synchronize()
+
+
 def test_graph_replay_split_tile(device):
     """The split-K tile launch (a bf16 call of 512 tokens at hidden 4096) in a graph:
     its arrival and exit words are re-armed by the launch itself, so replays, with
