@@ -197,7 +197,7 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
   Plan pl;
   const int64_t cus = topo.cus;
   if (use_decode(M) && aligned) {
-    pl.splits = decode_splits_for(M, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds, int4);
+    pl.splits = decode_splits_for(M, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds);
     if (pl.splits > 0) {
       pl.tail = M;
       return pl;
@@ -221,7 +221,7 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
   // block max(14.5, 1.45 * k tiles per split) us, each further block
   // 1.95 + 0.71 * K/1024 us, the tile kernel 2.1 us per stage + 7 us.
   const int64_t nblk = (M + 63) / 64;
-  const int blk_splits = decode_splits_for(64, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds, int4);
+  const int blk_splits = decode_splits_for(64, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds);
   const int64_t per_launch = std::max<int64_t>(
       1, std::min<int64_t>(g_decode_passes.load(), decode_max_blocks(n_tiles, K, blk_splits, int4 && in_norm)));
   const int64_t launches = (nblk + per_launch - 1) / per_launch;
@@ -263,7 +263,7 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
   const int64_t rounds_all = ((M + pl.v->bm - 1) / pl.v->bm * ct + cus - 1) / cus;
   const int64_t rounds_main = ((M - r) / pl.v->bm * ct + cus - 1) / cus;
   if (rounds_main >= rounds_all) return pl;
-  const int splits = decode_splits_for(r, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds, int4);
+  const int splits = decode_splits_for(r, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds);
   if (splits > 0) {
     pl.tail = r;
     pl.splits = splits;

@@ -125,7 +125,7 @@ int tile_dma_lds_bytes(int id);
 hipError_t launch_row_scale(const uint16_t* x, int64_t M, int64_t K, float eps, float* scale,
                             hipStream_t stream);
 
-int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested, int cus, int xcds, bool int4);
+int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested, int cus, int xcds);
 size_t decode_workspace_bytes(int n_tiles, int splits, int blocks = 1);
 // Most 64-row blocks one decode launch may cover with this many heads and splits
 // (one arrival counter per (head, block) in the workspace's counter region; one

@@ -268,6 +268,8 @@ __device__ void partial_any(const ProblemArgs& p, const WeightArgs& w, int proj,
 // partial_any over a range longer than one x slice: slices of kDecMaxNK tiles,
 // each staged once every wave is done with the previous one, the tiles
 // accumulated in order into one sum (the arithmetic of the two-slice split).
+// (A function of its own rather than a loop in partial_any: that keeps the code
+// of the one-slice kernels, C3's among them, exactly as it was.)
 template <bool INT4, bool INORM>
 __device__ void partial_any_long(const ProblemArgs& p, const WeightArgs& w, int proj, int hh, int kt0, int nk,
                                  const uint16_t* xs, uint32_t xs_lds, f32x4_t (&acc)[4], int r0) {
@@ -894,12 +896,11 @@ decode_multi_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int splits, flo
 int g_decode_force_recompute = 0;
 int g_decode_max_spins = kDecMaxSpins;
 
-int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested, int cus, int xcds, bool int4) {
+int decode_splits_for(int64_t M, int64_t K, int n_tiles, int requested, int cus, int xcds) {
   (void)M;
   const int nkt = int(K / kBK);
   if (nkt < 1) return 0;
-  (void)int4;  // (both weight formats take splits of up to two x slices)
-  const int max_nk = kDecLongMaxNK;
+  const int max_nk = kDecLongMaxNK;  // (both weight formats: splits of up to two x slices)
   const int min_splits = (nkt + max_nk - 1) / max_nk;  // bound on a split's k-range
   int s = requested;
   if (s <= 0) {
