@@ -17,6 +17,7 @@
  * Reference interface each entry point replaces (mini-qwen-llm):
  *   mqk_fused_qkv_rope_bf16   <- fused_qkv_rope()      mini_qwen/kernels/fused_qkv_rope.py:130-195
  *   mqk_fused_qkv_rope_f32    <- fused_qkv_rope() called with fp32 tensors (same lines)
+ *   mqk_fused_qkv_rope_f16    <- fused_qkv_rope() called with fp16 tensors (same lines)
  *   mqk_qk_norm_rope_bf16     <- _qk_norm_rope_kernel  mini_qwen/kernels/fused_qkv_rope.py:46-127
  *   mqk_w4a16_gemm(_ex)       <- w4a16_gemm()          mini_qwen/kernels/w4a16_gemm.py:194-247
  *   mqk_fused_qkv_rope_w4a16  <- the W4A16 attention front (3x LinearW4A16 + RMSNorm + RoPE),
@@ -37,6 +38,7 @@ extern "C" {
 #endif
 
 typedef uint16_t mqk_bf16;
+typedef uint16_t mqk_f16;  /* IEEE half */
 
 enum mqk_status {
   MQK_OK = 0,
@@ -109,6 +111,19 @@ int mqk_fused_qkv_rope_f32(const float* x, const float* w_q, const float* w_k, c
                            const float* q_gamma, const float* k_gamma, const float* cos, const float* sin,
                            const int32_t* positions, int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv,
                            int D, int64_t cos_rows, float eps, float* q, float* k, float* v, void* stream);
+
+/*
+ * fp16 twin of mqk_fused_qkv_rope_f32 (the reference op on fp16 tensors, e.g. a
+ * model loaded with dtype=float16, mini_qwen/model/loader.py:12-52): every
+ * float input fp16, q / k / v written in fp16.  The fp16 values are widened to
+ * fp32 when staged (their products are exact in fp32) and run through the fp32
+ * front's kernel; norm and RoPE in fp32; one fp16 rounding per output.  Same
+ * validation; no workspace.
+ */
+int mqk_fused_qkv_rope_f16(const mqk_f16* x, const mqk_f16* w_q, const mqk_f16* w_k, const mqk_f16* w_v,
+                           const mqk_f16* q_gamma, const mqk_f16* k_gamma, const mqk_f16* cos, const mqk_f16* sin,
+                           const int32_t* positions, int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv,
+                           int D, int64_t cos_rows, float eps, mqk_f16* q, mqk_f16* k, mqk_f16* v, void* stream);
 
 /* Workspace bytes needed by mqk_fused_qkv_rope_bf16 / _w4a16 for these sizes
  * (0 when the chosen kernels need none). */
@@ -326,7 +341,7 @@ int mqk_fused_qkv_rope_ex_w4a16(const mqk_bf16* x, const int32_t* qw_q, const vo
  *                    0 hands off at once; for tests of the hand-off).  The split-K tile
  *                    launch bounds each split's wait for the others the same way.
  *   "decode_force_recompute"  1: the decode kernel and the split-K tile launch take their
- *                    recompute path (used when a split ran on an unexpected XCD) for every
+ *                    recompute path (used when the splits of a head or tile ran on more than one XCD) for every
  *                    head / tile; for tests
  *   "tile_ksplit"    bf16 calls with fewer tiles than CUs (64 < T up to ~1000 tokens at
  *                    hidden 4096): 1 (default) = a split-K tile launch (each tile's K range

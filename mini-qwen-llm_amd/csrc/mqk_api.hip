@@ -516,10 +516,10 @@ int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
                          cos_rows, eps, q, k, v, nullptr, workspace, ws_bytes, stream);
 }
 
-int mqk_fused_qkv_rope_f32(const float* x, const float* w_q, const float* w_k, const float* w_v,
-                           const float* q_gamma, const float* k_gamma, const float* cos, const float* sin,
-                           const int32_t* positions, int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv,
-                           int D, int64_t cos_rows, float eps, float* q, float* k, float* v, void* stream) {
+static int fused_f32_impl(bool half, const void* x, const void* w_q, const void* w_k, const void* w_v,
+                          const void* q_gamma, const void* k_gamma, const void* cos, const void* sin,
+                          const int32_t* positions, int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                          int64_t cos_rows, float eps, void* q, void* k, void* v, void* stream) {
   if (T < 0 || hidden <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0)
     return fail(MQK_ERR_BAD_SHAPE, "need T >= 0, hidden > 0, Hq > 0, Hkv > 0, D > 0");
   if (D % 2 != 0) return fail(MQK_ERR_BAD_SHAPE, "head_dim must be even (RoPE rotate_half), got %d", D);
@@ -559,7 +559,24 @@ int mqk_fused_qkv_rope_f32(const float* x, const float* w_q, const float* w_k, c
   // 16-row tiles when 32-row tiles would leave CUs idle
   const Topology topo = device_topology();
   const int rows = (T + 31) / 32 * (Hq + 2 * Hkv) < topo.cus ? 16 : 32;
-  return hip_status(launch_f32_qkv(a, rows, topo.xcds, static_cast<hipStream_t>(stream)), "f32 front launch");
+  return hip_status(launch_f32_qkv(a, rows, half, topo.xcds, static_cast<hipStream_t>(stream)),
+                    half ? "f16 front launch" : "f32 front launch");
+}
+
+int mqk_fused_qkv_rope_f32(const float* x, const float* w_q, const float* w_k, const float* w_v,
+                           const float* q_gamma, const float* k_gamma, const float* cos, const float* sin,
+                           const int32_t* positions, int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv,
+                           int D, int64_t cos_rows, float eps, float* q, float* k, float* v, void* stream) {
+  return fused_f32_impl(false, x, w_q, w_k, w_v, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D,
+                        cos_rows, eps, q, k, v, stream);
+}
+
+int mqk_fused_qkv_rope_f16(const mqk_f16* x, const mqk_f16* w_q, const mqk_f16* w_k, const mqk_f16* w_v,
+                           const mqk_f16* q_gamma, const mqk_f16* k_gamma, const mqk_f16* cos, const mqk_f16* sin,
+                           const int32_t* positions, int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv,
+                           int D, int64_t cos_rows, float eps, mqk_f16* q, mqk_f16* k, mqk_f16* v, void* stream) {
+  return fused_f32_impl(true, x, w_q, w_k, w_v, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D,
+                        cos_rows, eps, q, k, v, stream);
 }
 
 // ---- allocation-free variant of mqk_fused_qkv_rope_bf16 ---------------------------------

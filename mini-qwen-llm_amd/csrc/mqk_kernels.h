@@ -163,29 +163,30 @@ extern int g_decode_max_spins;
 hipError_t launch_norm_rope(const uint16_t* q_raw, const uint16_t* k_raw, const EpilogueArgs& e,
                             int64_t T, hipStream_t stream);
 
-// fp32 front (fp32 x, weights, norm weights and RoPE tables; fp32 outputs).
+// fp32 / fp16 front: x, weights, norm weights and RoPE tables all fp32 (or all
+// fp16), outputs in the same type; products and sums in fp32.
 struct F32Args {
-  const float* x;       // [M, K]
-  const float* w[3];    // w_q [Hq*128, K], w_k / w_v [Hkv*128, K]
-  const float* q_gamma;
-  const float* k_gamma;
-  const float* cos;     // [cos_rows, 128]
-  const float* sin;
+  const void* x;        // [M, K]
+  const void* w[3];     // w_q [Hq*128, K], w_k / w_v [Hkv*128, K]
+  const void* q_gamma;
+  const void* k_gamma;
+  const void* cos;      // [cos_rows, 128]
+  const void* sin;
   const int32_t* positions;  // [M] or null: prefill, token t uses row t % S
   int64_t M, K, S, cos_rows;
   int Hq, Hkv;
   float eps;
-  float* q;             // [M, Hq, 128]
-  float* k;             // [M, Hkv, 128]
-  float* v;             // [M, Hkv, 128]
+  void* q;              // [M, Hq, 128]
+  void* k;              // [M, Hkv, 128]
+  void* v;              // [M, Hkv, 128]
   // (fields read by rope_row: no varlen, launch row 0 is token 0)
   const int32_t* cu_seqlens = nullptr;
   const int32_t* seq_pos0 = nullptr;
   int64_t n_seqs = 0;
   int64_t t0 = 0;
 };
-constexpr int kF32BK = 32;       // k extent of one staged fp32 tile
-// rows: token rows per workgroup, 32 or 16
-hipError_t launch_f32_qkv(const F32Args& a, int rows, int xcds, hipStream_t stream);
+constexpr int kF32BK = 32;       // k extent of one staged tile of the fp32 / fp16 front
+// rows: token rows per workgroup, 32 or 16; half: fp16 elements (else fp32)
+hipError_t launch_f32_qkv(const F32Args& a, int rows, bool half, int xcds, hipStream_t stream);
 
 }  // namespace mqk

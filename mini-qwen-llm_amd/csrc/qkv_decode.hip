@@ -67,7 +67,6 @@ constexpr int kMaxHeads = kDecodeMaxHeads;
 constexpr int kCounterBytes = int(kDecodeCounterBytes);
 constexpr int kTileFloats = kDecRows * kHeadDim;
 constexpr int kPitch = kHeadDim + 4;    // fp32 pitch of the finisher's LDS head tile
-constexpr uint32_t kForeignUnit = 1u << 16;  // arrival-counter increment of a misplaced split
 constexpr int kDecMaxSpins = 1 << 14;   // default polls (s_sleep 2 apart, ~1 ms) before a wait is handed off
 
 static_assert(kDecRows * kDecKc * 2 > 160 * 1024 / 2, "x slice must keep one workgroup per CU");
@@ -309,20 +308,34 @@ __device__ void partial_any_long(const ProblemArgs& p, const WeightArgs& w, int 
 // projection `proj` / head `hh` inside it, for the launch's `nblk` 64-row blocks.
 struct DecWork {
   int head, split, splits, proj, hh, nblk;
-  bool foreign;  // this workgroup runs on another XCD than the grid mapping assumes
+  uint32_t inc;  // this split's arrival increment (its XCD, and the forced flag for tests)
   int max_spins;  // polls of a designated finisher's final wait before it hands the block off
   int H;                  // heads of the projection (row stride of its output, in heads)
   const uint16_t* gamma;  // QK-Norm weights of the projection (Q or K)
   uint16_t* out;          // q / k / v (may be null: cache only)
 };
 
-// Arrival counter of a (head, block): bits 0-15 count the splits that have
-// published, bits 16-29 those that ran on another XCD than the grid assumes
-// (kForeignUnit each), and bit 30 marks a block whose designated finisher gave
-// up waiting for the others (see run_split).
+// Arrival counter of a (head, block), one atomic add per split: bits 0-4 count
+// the splits that have published (at most 16), bits 5-12 sum their XCDs x and
+// bits 13-22 sum x * x, bits 23-27 count splits forced onto the recompute path
+// (tests), and bit 30 marks a block whose designated finisher gave up waiting
+// for the others (see run_split).  The splits of a head are dispatched to one
+// XCD (workgroups go round-robin over the XCDs, from a starting XCD that
+// depends on the hardware queue), so their partials meet in one L2; the last
+// arrival checks that they did: n * sum(x^2) == sum(x)^2 exactly when all n
+// values of x are equal.
 constexpr uint32_t kAbandoned = 1u << 30;
-__device__ __forceinline__ bool all_arrived(uint32_t v, int splits) { return (v & 0xFFFFu) == uint32_t(splits); }
-__device__ __forceinline__ bool any_foreign(uint32_t v) { return ((v >> 16) & 0x3FFFu) != 0; }
+constexpr uint32_t kForcedUnit = 1u << 23;
+__device__ __forceinline__ uint32_t arrival_inc(int x, bool forced) {
+  return 1u + (uint32_t(x) << 5) + (uint32_t(x * x) << 13) + (forced ? kForcedUnit : 0u);
+}
+__device__ __forceinline__ bool all_arrived(uint32_t v, int splits) { return (v & 0x1Fu) == uint32_t(splits); }
+// some split ran on another XCD than the others (or was forced to recompute)
+__device__ __forceinline__ bool any_foreign(uint32_t v, int splits) {
+  v = __builtin_amdgcn_readfirstlane(v);  // (the same in every lane: scalar arithmetic)
+  const uint32_t sx = (v >> 5) & 0xFFu, sxx = (v >> 13) & 0x3FFu;
+  return ((v >> 23) & 0x1Fu) != 0 || uint32_t(splits) * sxx != sx * sx;
+}
 
 // Finishes 64-row block `blk` of the workgroup's head: sums every split's partial
 // in split order (RECOMPUTE: recomputes them all), applies RMSNorm + RoPE (Q/K),
@@ -620,8 +633,7 @@ __device__ __forceinline__ void publish_partial(const ProblemArgs& p, const DecW
 }
 
 __device__ __forceinline__ uint32_t arrive(uint32_t* counter, const DecWork& d) {
-  const uint32_t inc = 1u + (d.foreign ? kForeignUnit : 0u);
-  return __hip_atomic_fetch_add(counter, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
+  return __hip_atomic_fetch_add(counter, d.inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + d.inc;
 }
 
 // RoPE-table offset and paged-cache slot of this thread's row (tid / 8) of block b.
@@ -662,7 +674,7 @@ __device__ __forceinline__ void run_split_single(const ProblemArgs& p, const Wei
   __syncthreads();
   const uint32_t seen = arrival[0];
   if (!all_arrived(seen, d.splits)) return;
-  if (any_foreign(seen)) finish_block<INT4, INORM, false, true, LONG>(p, w, e, d, 0, acc, prow, cslot, xs, part, counters);
+  if (any_foreign(seen, d.splits)) finish_block<INT4, INORM, false, true, LONG>(p, w, e, d, 0, acc, prow, cslot, xs, part, counters);
   else finish_block<INT4, INORM, false, false, LONG>(p, w, e, d, 0, acc, prow, cslot, xs, part, counters);
 }
 
@@ -700,7 +712,7 @@ __device__ __forceinline__ void run_split_multi(const ProblemArgs& p, const Weig
 
   // Finish block b (counter value v, every split arrived), or defer it.
   auto finish_or_defer = [&](int b, uint32_t v) {
-    if (any_foreign(v)) {
+    if (any_foreign(v, d.splits)) {
       deferred |= 1u << b;
     } else {
       int64_t b_prow, b_cslot;
@@ -816,7 +828,7 @@ __device__ __forceinline__ DecWork dec_work(const ProblemArgs& p, const Epilogue
   d.gamma = pick3(d.proj, e.q_gamma, e.k_gamma, e.k_gamma);
   d.out = pick3(d.proj, e.q, e.k, e.v);
   // (XCC_ID is the physical XCD; a partition of the GPU holds xcds of them)
-  d.foreign = (ctl & 1) || xcc_id() % xcds != bid % xcds;
+  d.inc = arrival_inc(xcc_id() % xcds, (ctl & 1) != 0);
   d.max_spins = ctl >> 1;
   split_range(d.split, splits, int(p.K / kBK), kt0, nk);
   return d;
@@ -945,7 +957,8 @@ hipError_t launch_decode(int int4, const ProblemArgs& p, const WeightArgs& w, co
                          int splits, void* workspace, hipStream_t stream) {
   const int nkt = int(p.K / kBK);
   const int blocks = int((p.M + kDecRows - 1) / kDecRows);  // 64-row blocks of this launch
-  if (splits < 1 || splits > kDecMaxNK || splits > nkt ||
+  // (p.xcds <= 8: the arrival counter's XCD sums hold x < 8)
+  if (splits < 1 || splits > kDecMaxNK || splits > nkt || p.xcds > 8 ||
       (nkt + splits - 1) / splits > (blocks > 1 ? kDecMultiMaxNK : kDecLongMaxNK) ||
       p.n_tiles > kMaxHeads || blocks < 1 || blocks > decode_max_blocks(p.n_tiles, p.K, splits, int4 && p.in_gamma) || p.xcds < 1)
     return hipErrorInvalidValue;

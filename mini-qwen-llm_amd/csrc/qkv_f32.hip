@@ -26,7 +26,40 @@ static_assert(kHeadDim * kPitch >= 32 * kEpiPitch, "the accumulator tile reuses 
 // ROWS = 32: each wave runs v_mfma_f32_32x32x2_f32 on its 32 x 32 block.
 // ROWS = 16 (launches whose 32-row tiles would leave CUs idle): each wave runs
 // v_mfma_f32_16x16x4_f32 on two 16 x 16 blocks.
-template <int ROWS>
+// Element type T: float, or _Float16 (converted to fp32 when loaded; fp16
+// products are exact in fp32).
+template <class T>
+__device__ __forceinline__ float elem(const void* p, int64_t i) {
+  return float(static_cast<const T*>(p)[i]);
+}
+// 4 consecutive elements as fp32 (16-byte or 8-byte loads)
+template <class T>
+__device__ __forceinline__ f32x4_t load4(const T* p) {
+  if constexpr (sizeof(T) == 4) {
+    return *reinterpret_cast<const f32x4_t*>(p);
+  } else {
+    typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+    const h4_t h = *reinterpret_cast<const h4_t*>(p);
+    return f32x4_t{float(h.x), float(h.y), float(h.z), float(h.w)};
+  }
+}
+// 8 values stored as 8 consecutive elements
+template <class T>
+__device__ __forceinline__ void store8(void* dst, const float (&v)[8], int i0) {
+  if constexpr (sizeof(T) == 4) {
+    float* d = static_cast<float*>(dst);
+    *reinterpret_cast<f32x4_t*>(d) = f32x4_t{v[i0], v[i0 + 1], v[i0 + 2], v[i0 + 3]};
+    *reinterpret_cast<f32x4_t*>(d + 4) = f32x4_t{v[i0 + 4], v[i0 + 5], v[i0 + 6], v[i0 + 7]};
+  } else {
+    typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+    h8_t h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = _Float16(v[i0 + i]);
+    *static_cast<h8_t*>(dst) = h;
+  }
+}
+
+template <int ROWS, class T>
 __global__ void __launch_bounds__(kThreads) f32_qkv_kernel(F32Args a, int xcds) {
   static_assert(ROWS == 16 || ROWS == 32, "row tile");
   __shared__ float xs[ROWS * kPitch];
@@ -37,7 +70,7 @@ __global__ void __launch_bounds__(kThreads) f32_qkv_kernel(F32Args a, int xcds) 
   const int h = tile / n_rt;
   int proj, hh;
   split_head(h, a.Hq, a.Hkv, proj, hh);
-  const float* W = a.w[proj] + int64_t(hh) * kHeadDim * a.K;
+  const T* W = static_cast<const T*>(a.w[proj]) + int64_t(hh) * kHeadDim * a.K;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row0 = int64_t(rt) * ROWS;
 
@@ -46,13 +79,13 @@ __global__ void __launch_bounds__(kThreads) f32_qkv_kernel(F32Args a, int xcds) 
   const int sr = tid >> 3, sk = (tid & 7) * 4;
   const bool x_row = sr < ROWS;
   const bool x_in = x_row && row0 + sr < a.M;
-  const float* xp = a.x + (x_in ? (row0 + sr) * a.K : 0) + sk;
-  const float* wp = W + int64_t(sr) * a.K + sk;
+  const T* xp = static_cast<const T*>(a.x) + (x_in ? (row0 + sr) * a.K : 0) + sk;
+  const T* wp = W + int64_t(sr) * a.K + sk;
   f32x4_t xr, wr[4];
   auto load = [&](int64_t k0) {
-    xr = x_in ? *reinterpret_cast<const f32x4_t*>(xp + k0) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    xr = x_in ? load4<T>(xp + k0) : f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) wr[j] = *reinterpret_cast<const f32x4_t*>(wp + int64_t(32 * j) * a.K + k0);
+    for (int j = 0; j < 4; ++j) wr[j] = load4<T>(wp + int64_t(32 * j) * a.K + k0);
   };
   auto stage = [&]() {
     if (x_row) {
@@ -133,40 +166,38 @@ __global__ void __launch_bounds__(kThreads) f32_qkv_kernel(F32Args a, int xcds) 
     const float ss = sum8_lanes(run_sumsq(lo, hi));
     const float rms = head_rms(ss, a.eps);
     if (t < a.M) {
-      const float* g = proj == 0 ? a.q_gamma : a.k_gamma;
+      const void* g = proj == 0 ? a.q_gamma : a.k_gamma;
       const int64_t prow = rope_row(a, t) * kHeadDim;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
 #pragma clang fp contract(off)
         const int d = 8 * c + i;
-        const float x1n = lo[i] * rms * g[d];
-        const float x2n = hi[i] * rms * g[d + kHalfDim];
-        lo[i] = __builtin_fmaf(x1n, a.cos[prow + d], -(x2n * a.sin[prow + d]));
-        hi[i] = __builtin_fmaf(x2n, a.cos[prow + d + kHalfDim], x1n * a.sin[prow + d + kHalfDim]);
+        const float x1n = lo[i] * rms * elem<T>(g, d);
+        const float x2n = hi[i] * rms * elem<T>(g, d + kHalfDim);
+        lo[i] = __builtin_fmaf(x1n, elem<T>(a.cos, prow + d), -(x2n * elem<T>(a.sin, prow + d)));
+        hi[i] = __builtin_fmaf(x2n, elem<T>(a.cos, prow + d + kHalfDim), x1n * elem<T>(a.sin, prow + d + kHalfDim));
       }
     }
   }
   if (t < a.M) {
     const int H = proj == 0 ? a.Hq : a.Hkv;
-    float* dst = pick3(proj, a.q, a.k, a.v) + (t * H + hh) * kHeadDim + 8 * c;
-    *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{lo[0], lo[1], lo[2], lo[3]};
-    *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{lo[4], lo[5], lo[6], lo[7]};
-    *reinterpret_cast<f32x4_t*>(dst + kHalfDim) = f32x4_t{hi[0], hi[1], hi[2], hi[3]};
-    *reinterpret_cast<f32x4_t*>(dst + kHalfDim + 4) = f32x4_t{hi[4], hi[5], hi[6], hi[7]};
+    T* dst = static_cast<T*>(pick3(proj, a.q, a.k, a.v)) + (t * H + hh) * kHeadDim + 8 * c;
+    store8<T>(dst, lo, 0);
+    store8<T>(dst + kHalfDim, hi, 0);
   }
 }
 
 }  // namespace
 
-hipError_t launch_f32_qkv(const F32Args& a, int rows, int xcds, hipStream_t stream) {
+hipError_t launch_f32_qkv(const F32Args& a, int rows, bool half, int xcds, hipStream_t stream) {
   if (rows != 16 && rows != 32) return hipErrorInvalidValue;
   const int64_t n_rt = (a.M + rows - 1) / rows;
   const int64_t blocks = n_rt * (a.Hq + 2 * a.Hkv);
   if (a.K % kKT != 0 || blocks <= 0 || blocks > (int64_t(1) << 31) - 1) return hipErrorInvalidValue;
-  if (rows == 16)
-    hipLaunchKernelGGL(f32_qkv_kernel<16>, dim3(unsigned(blocks)), dim3(kThreads), 0, stream, a, xcds);
-  else
-    hipLaunchKernelGGL(f32_qkv_kernel<32>, dim3(unsigned(blocks)), dim3(kThreads), 0, stream, a, xcds);
+  using Kernel = void (*)(F32Args, int);
+  const Kernel k = rows == 16 ? (half ? f32_qkv_kernel<16, _Float16> : f32_qkv_kernel<16, float>)
+                              : (half ? f32_qkv_kernel<32, _Float16> : f32_qkv_kernel<32, float>);
+  hipLaunchKernelGGL(k, dim3(unsigned(blocks)), dim3(kThreads), 0, stream, a, xcds);
   return hipGetLastError();
 }
 

@@ -365,7 +365,7 @@ struct TileSplit {
   uint32_t* counters;  // arrival counter per tile; kDecodeRecomputeWord counts recomputed tiles
 };
 
-constexpr uint32_t kSplitForeign = 1u << 24;  // arrival increment of a split on an unexpected XCD
+constexpr uint64_t kSplitForced = uint64_t(1) << 24;  // arrival increment of a split forced to recompute
 
 __device__ __forceinline__ int hw_xcc_id() {
   return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11));  // hwreg(HW_REG_XCC_ID, 0, 4)
@@ -541,11 +541,13 @@ tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp)
   const int n_mt = int((p.M + BM - 1) / BM);
   const int n_ht = p.n_tiles / NH;
   int mt, ht, split = 0, tile = 0;
-  bool foreign = false;
+  int hw_xcd = 0;
   {
-    // Workgroup b runs on XCD b % X.  XCD x takes tiles [x*tpx, (x+1)*tpx), all
-    // splits of each (so a tile's partials meet in one L2); row tiles vary
-    // fastest, so an XCD's tiles share weight panels.
+    // Workgroups go round-robin over the X XCDs (from a starting XCD that depends
+    // on the hardware queue), so the workgroups b with one b % X share an XCD.
+    // That group takes tiles [x*tpx, (x+1)*tpx), x = b % X, all splits of each (so
+    // a tile's partials meet in one L2); row tiles vary fastest, so an XCD's
+    // tiles share weight panels.
     const int X = p.xcds;
     const int tiles = n_mt * n_ht;
     const int tpx = (tiles + X - 1) / X;
@@ -557,7 +559,7 @@ tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp)
     if (slot >= tpx || tile >= tiles) return;  // grid padding
     mt = tile % n_mt;
     ht = tile / n_mt;
-    foreign = (sp.ctl & 1) || hw_xcc_id() % X != xcd;
+    hw_xcd = hw_xcc_id() % X;
   }
   const int64_t m0 = int64_t(mt) * BM;
 
@@ -709,27 +711,36 @@ tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp)
     // The tile's rows form U = WM * MB units of 32 (unit u: rows [32u, 32u+32),
     // held by waves wm = u / MB in accumulator block mb = u % MB).  Split s
     // finishes units [s*U/ns, (s+1)*U/ns) once every split has arrived, reading
-    // only those rows of the ns partials.  Arrival word: bits 0-7 count the
-    // splits, bits 8-23 mark splits whose wait ran out (their units go to the last
-    // arrival), bits 24-31 count splits that ran on an unexpected XCD (then the
-    // last arrival recomputes the whole tile and the others leave).  The
+    // only those rows of the ns partials.  Arrival word (64-bit): bits 0-7 count
+    // the splits, bits 8-23 mark splits whose wait ran out (their units go to the
+    // last arrival), bits 24-31 count splits forced onto the recompute path, and
+    // bits 32-49 sum the splits' XCDs and their squares; when some split ran on
+    // another XCD than the others (or was forced), the last arrival recomputes the
+    // whole tile and the others leave.  The
     // recomputation reuses the one main loop below (a second inlined copy of it
     // would spill).
     constexpr int U = WM * S::kMB;
-    uint32_t* arrive_word =
-        reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(sp.counters) + kSplitWordsOffset + tile * kSplitLineBytes);
-    uint32_t* exit_word = arrive_word + 1;
-    __shared__ uint32_t seen_word;
+    uint64_t* arrive_word =
+        reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(sp.counters) + kSplitWordsOffset + tile * kSplitLineBytes);
+    uint32_t* exit_word = reinterpret_cast<uint32_t*>(arrive_word + 1);
+    __shared__ uint64_t seen_word;
     // Every split leaves through here once it no longer reads the arrival word;
     // the last to leave re-arms both words for the next launch.
     auto leave = [&]() {
       if (tid == 0 && __hip_atomic_fetch_add(exit_word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u ==
                           uint32_t(ns)) {
-        __hip_atomic_store(arrive_word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(arrive_word, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(exit_word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     };
-    auto arrived = [&](uint32_t w_) { return (w_ & 0xFFu) == uint32_t(ns); };
+    auto arrived = [&](uint64_t w_) { return (w_ & 0xFFu) == uint64_t(ns); };
+    // some split ran on another XCD than the others, or was forced to recompute:
+    // the arrival sums the splits' XCDs x (bits 32-39) and x * x (bits 40-49), and
+    // n * sum(x^2) == sum(x)^2 exactly when all n values are equal
+    auto misplaced = [&](uint64_t w_) {
+      const uint64_t sx = (w_ >> 32) & 0xFFu, sxx = (w_ >> 40) & 0x3FFu;
+      return ((w_ >> 24) & 0xFFu) != 0 || uint64_t(ns) * sxx != sx * sx;
+    };
     auto units_of = [&](int sidx) {
       const int u0 = sidx * U / ns, u1 = (sidx + 1) * U / ns;
       return u1 > u0 ? ((1u << u1) - 1u) & ~((1u << u0) - 1u) : 0u;
@@ -750,11 +761,12 @@ tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp)
         break;
       }
       __syncthreads();  // ... and every thread's
-      const uint32_t inc = 1u + (foreign ? kSplitForeign : 0u);
+      const uint64_t inc = 1u + ((sp.ctl & 1) ? kSplitForced : 0u) + (uint64_t(hw_xcd) << 32) +
+                           (uint64_t(hw_xcd * hw_xcd) << 40);
       if (tid == 0)
         seen_word = __hip_atomic_fetch_add(arrive_word, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
       __syncthreads();
-      uint32_t v = seen_word;
+      uint64_t v = seen_word;
       units = units_of(split);
       if (!arrived(v)) {
         if (units == 0) {  // nothing of this tile to finish here
@@ -778,17 +790,18 @@ tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp)
           __builtin_amdgcn_s_waitcnt(0);
           __syncthreads();
           if (tid == 0)
-            seen_word = __hip_atomic_fetch_or(arrive_word, 1u << (8 + split), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            seen_word = __hip_atomic_fetch_or(arrive_word, uint64_t(1) << (8 + split), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
           __syncthreads();
           v = seen_word;
         }
-        if (!arrived(v) || (v >> 24) != 0) {  // handed off, or the last arrival recomputes
+        if (!arrived(v) || misplaced(v)) {  // handed off, or the last arrival recomputes
           leave();
           return;
         }
         break;
       }
-      if ((v >> 24) != 0) {
+      if (misplaced(v)) {
         // A split ran on another XCD, so its partial may not be visible through
         // this L2: recompute every split here and publish each into this L2.
         if (tid == 0)
@@ -923,7 +936,8 @@ hipError_t launch_dma_split(const ProblemArgs& p, const WeightArgs& w, const Epi
   const int X = p.xcds > 0 ? p.xcds : 1;
   const int tpx = (tiles + X - 1) / X;
   const size_t dyn = p.in_gamma ? size_t(p.K) * 2 : 0;
-  if (S::kLdsBytes + dyn > 160 * 1024 || ksplit < 2 || ksplit > 16 || tiles > kSplitMaxTiles ||
+  // (p.xcds <= 8: the arrival word's XCD sums hold x < 8)
+  if (S::kLdsBytes + dyn > 160 * 1024 || ksplit < 2 || ksplit > 16 || tiles > kSplitMaxTiles || p.xcds > 8 ||
       p.K / SBK < ksplit)
     return hipErrorInvalidValue;
   TileSplit sp;

@@ -76,6 +76,12 @@ SIGNATURES = {
          _I64, _I64, _I64, _I, _I, _I,           # T S hidden Hq Hkv D
          _I64, _F, _P, _P, _P, _P],              # cos_rows eps q k v stream
     ),
+    "mqk_fused_qkv_rope_f16": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P,     # x w_q w_k w_v q_gamma k_gamma cos sin positions
+         _I64, _I64, _I64, _I, _I, _I,           # T S hidden Hq Hkv D
+         _I64, _F, _P, _P, _P, _P],              # cos_rows eps q k v stream
+    ),
     "mqk_fused_qkv_rope_workspace_size": (_SZ, [_I64, _I, _I, _I64]),
     "mqk_fused_qkv_rope_bf16_noalloc": (
         _I,

@@ -25,13 +25,15 @@ Differences from the reference, all deliberate:
     bit-equality with torch's own GEMM, which no independent kernel can give);
   * positions outside ``[0, cos.shape[0])`` are clamped instead of read out of
     bounds; int64 positions are accepted and converted;
-  * inputs must be CUDA/HIP tensors, either all bf16 or all fp32 (TypeError /
+  * inputs must be CUDA/HIP tensors, all bf16, all fp32 or all fp16 (TypeError /
     ValueError otherwise); non-contiguous inputs are made contiguous.
 
 fp32 inputs (the dtype of the reference's CPU-runnable fp32 layer) take a
 separate kernel: an fp32 projection on the matrix cores (fp32 products and
 sums), norm and RoPE in fp32, fp32 outputs, as the reference computes for fp32
-tensors (an fp32 GEMM, then its kernel loads and stores fp32).
+tensors (an fp32 GEMM, then its kernel loads and stores fp32).  fp16 inputs (a
+model loaded in fp16) take the same kernel: widened to fp32 when staged,
+products exact in fp32, fp16 outputs.
 """
 from __future__ import annotations
 
@@ -101,7 +103,7 @@ def fused_qkv_rope(
     H_KV = w_k.shape[0] // D
     assert D % 2 == 0, "head_dim must be even (RoPE rotate_half)"
     device = x.device
-    dtype = torch.float32 if isinstance(x, torch.Tensor) and x.dtype == torch.float32 else torch.bfloat16
+    dtype = x.dtype if isinstance(x, torch.Tensor) and x.dtype in (torch.float32, torch.float16) else torch.bfloat16
     x = _require(x, "x", device, dtype)
     w_q = _require(w_q, "w_q", device, dtype)
     w_k = _require(w_k, "w_k", device, dtype)
@@ -126,14 +128,15 @@ def fused_qkv_rope(
 
     lib = _native.library()
     stream = _native.stream_handle(device)
-    if dtype == torch.float32:
+    if dtype != torch.bfloat16:
+        entry = "mqk_fused_qkv_rope_f32" if dtype == torch.float32 else "mqk_fused_qkv_rope_f16"
         status = _native.call(
-            device, lib.mqk_fused_qkv_rope_f32,
+            device, getattr(lib, entry),
             x.data_ptr(), w_q.data_ptr(), w_k.data_ptr(), w_v.data_ptr(),
             q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), _native.ptr(pos),
             T, S, H, H_Q, H_KV, D, cos.shape[0], EPS,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), stream)
-        _native.check(status, "mqk_fused_qkv_rope_f32")
+        _native.check(status, entry)
         return q, k, v
     nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, H_Q, H_KV, H))
     ws = _native.workspace(device, stream, nbytes)
@@ -211,7 +214,7 @@ def fused_qkv_rope_paged(
     H_KV = w_k.shape[0] // D
     assert D % 2 == 0, "head_dim must be even (RoPE rotate_half)"
     device = x.device
-    dtype = torch.float32 if isinstance(x, torch.Tensor) and x.dtype == torch.float32 else torch.bfloat16
+    dtype = torch.bfloat16  # (the paged and extended forms run the bf16 kernels only)
     x = _require(x, "x", device, dtype)
     w_q = _require(w_q, "w_q", device, dtype)
     w_k = _require(w_k, "w_k", device, dtype)
@@ -346,7 +349,7 @@ def fused_qkv_rope_ex(
     H_KV = w_k.shape[0] // D
     assert D % 2 == 0, "head_dim must be even (RoPE rotate_half)"
     device = x.device
-    dtype = torch.float32 if isinstance(x, torch.Tensor) and x.dtype == torch.float32 else torch.bfloat16
+    dtype = torch.bfloat16  # (the paged and extended forms run the bf16 kernels only)
     x = _require(x, "x", device, dtype)
     w_q = _require(w_q, "w_q", device, dtype)
     w_k = _require(w_k, "w_k", device, dtype)

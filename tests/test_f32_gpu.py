@@ -124,7 +124,7 @@ def test_f32_mixed_dtypes_rejected(device):
     args, _ = _inputs(1, 8, 1024, 16, 8, seed=315)
     dev = [a.to(device) for a in args]
     dev[1] = dev[1].bfloat16()
-    with pytest.raises(TypeError, match="w_q must be torch.float32"):
+    with pytest.raises(TypeError, match="w_q must be torch.float32"):  # (fp32 x, bf16 w_q)
         mqk.fused_qkv_rope(*dev)
     dev = [a.to(device) for a in args]
     dev[6] = dev[6].bfloat16()
@@ -138,3 +138,41 @@ def test_f32_is_one_native_launch(device):
     args, _ = _inputs(1, 128, 1024, 16, 8, seed=316)
     dev = [a.to(device) for a in args]
     assert launched_kernels(lambda: mqk.fused_qkv_rope(*dev)) == ["f32"]
+
+
+# ── fp16 tensors (a model loaded with dtype=float16, loader.py:12-52) ────────
+
+@pytest.mark.parametrize("B,S,hidden,Hq,Hkv,positions", [
+    (1, 128, 1024, 16, 8, False), (64, 1, 4096, 32, 8, True), (4, 128, 1024, 16, 8, False)])
+def test_f16_matches_oracle(B, S, hidden, Hq, Hkv, positions, device):
+    """fp16 inputs widened to fp32 (their products are exact), fp32 sums, norm
+    and RoPE, one fp16 rounding per output: against the oracle on the same fp16
+    values, within half an fp16 ulp of the output plus the fp32 summation error
+    (max-abs <= 4e-3 at outputs below 8; rel-L2 <= 1e-3)."""
+    import mqk
+    from oracle import qkv_rope_oracle as orc
+    g = torch.Generator().manual_seed(320 + B)
+    rows = 8192 if positions else S
+    pos = torch.randint(0, rows, (B * S,), generator=g, dtype=torch.int32) if positions else None
+    args, _ = _inputs(B, S, hidden, Hq, Hkv, seed=321 + B, rows=rows)
+    args = [a.half() for a in args]
+    out = mqk.fused_qkv_rope(*(a.to(device) for a in args), None if pos is None else pos.to(device))
+    torch.cuda.synchronize()
+    ref = _oracle([a.float() for a in args], pos, S)
+    for name, o, r in zip("qkv", out, ref):
+        assert o.dtype == torch.float16
+        o = o.float().cpu().numpy().reshape(r.shape)
+        ma, rl = orc.max_abs(o, r), orc.rel_l2(o, r)
+        assert np.abs(r).max() < 8 and ma <= 4e-3 and rl <= 1e-3, f"{name}: {ma:.2e} {rl:.2e}"
+
+
+def test_f32_and_f16_rejected_by_the_bf16_only_forms(device):
+    """The paged and extended forms run bf16 kernels only: fp32 or fp16 inputs
+    raise TypeError there, whatever the dtype of cos / sin."""
+    import mqk
+    args, _ = _inputs(1, 8, 1024, 16, 8, seed=322)
+    for dt in (torch.float32, torch.float16):
+        dev = [a.to(device).to(dt) for a in args]
+        dev[6], dev[7] = dev[6].bfloat16(), dev[7].bfloat16()
+        with pytest.raises(TypeError, match="x must be torch.bfloat16"):
+            mqk.fused_qkv_rope_ex(*dev)

@@ -520,3 +520,14 @@ def test_stream_handle_falls_back_to_the_public_api(monkeypatch):
     assert _native.stream_handle(torch.device("cuda", 0)) == 12345
     monkeypatch.setattr(_native, "_raw_stream", lambda idx: 777 + idx)
     assert _native.stream_handle(torch.device("cuda", 1)) == 778
+
+
+def test_f16_validation(lib):
+    """The fp16 entry point's checks run before any launch (fake pointers)."""
+    fake = 1 << 20
+    f = lambda T=4, hidden=1024, D=128, x=fake: lib.mqk_fused_qkv_rope_f16(
+        x, fake, fake, fake, fake, fake, fake, fake, None, T, 4, hidden, 2, 1, D, 8, 1e-6, fake, fake, fake, None)
+    assert f(D=96) == -3
+    assert f(hidden=48) == -3
+    assert f(x=None) == -1
+    assert f(T=0) == 0
