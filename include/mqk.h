@@ -115,10 +115,9 @@ int mqk_fused_qkv_rope_f32(const float* x, const float* w_q, const float* w_k, c
 /*
  * fp16 twin of mqk_fused_qkv_rope_f32 (the reference op on fp16 tensors, e.g. a
  * model loaded with dtype=float16, mini_qwen/model/loader.py:12-52): every
- * float input fp16, q / k / v written in fp16.  The fp16 values are widened to
- * fp32 when staged (their products are exact in fp32) and run through the fp32
- * front's kernel; norm and RoPE in fp32; one fp16 rounding per output.  Same
- * validation; no workspace.
+ * float input fp16, q / k / v written in fp16.  The fp32 front's kernel with
+ * fp16 tiles on the fp16 matrix cores (exact products, fp32 sums); norm and
+ * RoPE in fp32; one fp16 rounding per output.  Same validation; no workspace.
  */
 int mqk_fused_qkv_rope_f16(const mqk_f16* x, const mqk_f16* w_q, const mqk_f16* w_k, const mqk_f16* w_v,
                            const mqk_f16* q_gamma, const mqk_f16* k_gamma, const mqk_f16* cos, const mqk_f16* sin,

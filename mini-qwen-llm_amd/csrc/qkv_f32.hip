@@ -20,14 +20,15 @@ namespace {
 constexpr int kKT = kF32BK;
 constexpr int kPitch = kKT + 1;          // LDS row pitch of the staged tiles (odd: no bank conflicts)
 constexpr int kEpiPitch = kHeadDim + 4;  // LDS row pitch of the accumulator tile
+constexpr int kHPitch = kKT + 4;         // LDS row pitch (halves) of the fp16 staged tiles
 constexpr int kThreads = 256;
 static_assert(kHeadDim * kPitch >= 32 * kEpiPitch, "the accumulator tile reuses the weight tile's LDS");
 
 // ROWS = 32: each wave runs v_mfma_f32_32x32x2_f32 on its 32 x 32 block.
 // ROWS = 16 (launches whose 32-row tiles would leave CUs idle): each wave runs
 // v_mfma_f32_16x16x4_f32 on two 16 x 16 blocks.
-// Element type T: float, or _Float16 (converted to fp32 when loaded; fp16
-// products are exact in fp32).
+// Element type T: float, or _Float16 (the norm weights and RoPE tables are
+// read as fp32; fp16 tiles go to the fp16 matrix cores, see the kernel).
 template <class T>
 __device__ __forceinline__ float elem(const void* p, int64_t i) {
   return float(static_cast<const T*>(p)[i]);
@@ -99,7 +100,73 @@ __global__ void __launch_bounds__(kThreads) f32_qkv_kernel(F32Args a, int xcds) 
   };
 
   float* ep = ws;  // (after the k loop) the accumulator tile [ROWS][kEpiPitch]
-  if constexpr (ROWS == 32) {
+  if constexpr (sizeof(T) == 2) {
+    // fp16: the tiles stay fp16 in LDS (row pitch kHPitch halves: 8-byte reads
+    // free of bank conflicts) and run on the fp16 matrix cores, whose products
+    // are exact and sums fp32
+    typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+    _Float16* xh = reinterpret_cast<_Float16*>(xs);
+    _Float16* wh = reinterpret_cast<_Float16*>(ws);
+    h4_t xr4, wr4[4];
+    auto hload = [&](int64_t k0) {
+      xr4 = x_in ? *reinterpret_cast<const h4_t*>(xp + k0) : h4_t{};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wr4[j] = *reinterpret_cast<const h4_t*>(wp + int64_t(32 * j) * a.K + k0);
+    };
+    auto hstage = [&]() {
+      if (x_row) *reinterpret_cast<h4_t*>(xh + sr * kHPitch + sk) = xr4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<h4_t*>(wh + (sr + 32 * j) * kHPitch + sk) = wr4[j];
+    };
+    if constexpr (ROWS == 32) {
+      f32x16_t acc;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+      // lane l: x row (l & 31), weight row 32 * wave + (l & 31), k 4 (l >> 5) .. +4 of each 8
+      const _Float16* xa = xh + (lane & 31) * kHPitch + 4 * (lane >> 5);
+      const _Float16* wb = wh + (32 * wave + (lane & 31)) * kHPitch + 4 * (lane >> 5);
+      hload(0);
+      for (int64_t k0 = 0; k0 < a.K; k0 += kKT) {
+        hstage();
+        __syncthreads();
+        if (k0 + kKT < a.K) hload(k0 + kKT);
+#pragma unroll
+        for (int kk = 0; kk < kKT / 8; ++kk)
+          acc = __builtin_amdgcn_mfma_f32_32x32x8f16(*reinterpret_cast<const h4_t*>(xa + 8 * kk),
+                                                      *reinterpret_cast<const h4_t*>(wb + 8 * kk), acc, 0, 0, 0);
+        __syncthreads();
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        ep[(8 * (i >> 2) + 4 * (lane >> 5) + (i & 3)) * kEpiPitch + 32 * wave + (lane & 31)] = acc[i];
+    } else {
+      f32x4_t acc[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      // lane l: x row (l & 15), weight rows 32 * wave + 16 b + (l & 15), k 4 (l >> 4) .. +4 of each 16
+      const _Float16* xa = xh + (lane & 15) * kHPitch + 4 * (lane >> 4);
+      const _Float16* wb = wh + (32 * wave + (lane & 15)) * kHPitch + 4 * (lane >> 4);
+      hload(0);
+      for (int64_t k0 = 0; k0 < a.K; k0 += kKT) {
+        hstage();
+        __syncthreads();
+        if (k0 + kKT < a.K) hload(k0 + kKT);
+#pragma unroll
+        for (int kk = 0; kk < kKT / 16; ++kk)
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+            acc[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                *reinterpret_cast<const h4_t*>(xa + 16 * kk),
+                *reinterpret_cast<const h4_t*>(wb + 16 * b * kHPitch + 16 * kk), acc[b], 0, 0, 0);
+        __syncthreads();
+      }
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          ep[(4 * (lane >> 4) + j) * kEpiPitch + 32 * wave + 16 * b + (lane & 15)] = acc[b][j];
+    }
+  } else if constexpr (ROWS == 32) {
     f32x16_t acc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.f;

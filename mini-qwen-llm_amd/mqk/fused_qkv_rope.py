@@ -32,8 +32,8 @@ fp32 inputs (the dtype of the reference's CPU-runnable fp32 layer) take a
 separate kernel: an fp32 projection on the matrix cores (fp32 products and
 sums), norm and RoPE in fp32, fp32 outputs, as the reference computes for fp32
 tensors (an fp32 GEMM, then its kernel loads and stores fp32).  fp16 inputs (a
-model loaded in fp16) take the same kernel: widened to fp32 when staged,
-products exact in fp32, fp16 outputs.
+model loaded in fp16) take the same kernel on the fp16 matrix cores (exact
+products, fp32 sums), with fp16 outputs.
 """
 from __future__ import annotations
 

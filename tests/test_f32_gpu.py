@@ -145,7 +145,7 @@ def test_f32_is_one_native_launch(device):
 @pytest.mark.parametrize("B,S,hidden,Hq,Hkv,positions", [
     (1, 128, 1024, 16, 8, False), (64, 1, 4096, 32, 8, True), (4, 128, 1024, 16, 8, False)])
 def test_f16_matches_oracle(B, S, hidden, Hq, Hkv, positions, device):
-    """fp16 inputs widened to fp32 (their products are exact), fp32 sums, norm
+    """fp16 inputs on the fp16 matrix cores (exact products), fp32 sums, norm
     and RoPE, one fp16 rounding per output: against the oracle on the same fp16
     values, within half an fp16 ulp of the output plus the fp32 summation error
     (max-abs <= 4e-3 at outputs below 8; rel-L2 <= 1e-3)."""
