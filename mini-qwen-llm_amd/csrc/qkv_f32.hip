@@ -1,5 +1,6 @@
-// The fused front for fp32 callers: fp32 x, weights, norm weights and RoPE
-// tables in, fp32 q / k / v out.  The reference op accepts fp32 tensors too:
+// The fused front for fp32 (and fp16) callers: x, weights, norm weights and
+// RoPE tables in that type, q / k / v out in it.  The reference op accepts fp32
+// tensors too:
 // its GEMM is then an fp32 matmul and its Triton kernel loads, normalises,
 // rotates and stores in fp32 (mini_qwen/kernels/fused_qkv_rope.py:84-127,
 // :167-173; the fp32 layer of the reference's CPU-runnable configuration).
@@ -10,7 +11,8 @@
 // registers under the current tile's MFMAs.
 // The accumulators then go through LDS so that eight threads hold a row's
 // 128 dims (each the RoPE pairs d, d+64 for eight d), apply RMSNorm and RoPE
-// in fp32, and store.
+// in fp32, and store.  fp16 tiles stay fp16 in LDS and run on the fp16 matrix
+// cores (exact products, fp32 sums).
 #include "mqk_device.h"
 #include "mqk_kernels.h"
 
