@@ -310,9 +310,9 @@ def run_only(name, steps, warmup, dev):
         ms, _ = bench_prefill(8192, 1, 8192, 2048, 32, 4, 3, steps, warmup, dev)
     elif name == "c5":
         ms, _ = bench_w4a16(hidden, Hq, Hkv, 4, steps, warmup, dev)
-    elif name == "mid":  # a 512-token call (random positions): the split-K tile launch
+    elif name == "mid":  # a 512-token call (random positions): one round of 128 x 128 single-head tiles
         ms, _ = bench_decode(512, hidden, Hq, Hkv, 2, steps, warmup, dev)
-    elif name == "mid256":  # a 256-token call: the split-K tile launch
+    elif name == "mid256":  # a 256-token call: one round of 64 x 128 single-head tiles
         ms, _ = bench_decode(256, hidden, Hq, Hkv, 2, steps, warmup, dev)
     elif name == "mid128":  # a 128-token call: one decode launch covering two 64-row blocks
         ms, _ = bench_decode(128, hidden, Hq, Hkv, 2, steps, warmup, dev)
@@ -334,6 +334,8 @@ def main(argv=None) -> int:
     ap.add_argument("--only", choices=WORKLOADS,
                     help="run one workload alone (profiler runs; 'copy' = 256 MiB calibration copy)")
     ap.add_argument("--tile", type=int, default=0, help="force a prefill tile variant (mqk.tile_variants())")
+    ap.add_argument("--no-head-tiles", action="store_true",
+                    help="plan without single-head tiles (mid token counts then take the split-K tile launch)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the op has no multi-GPU path); "
@@ -349,6 +351,8 @@ def main(argv=None) -> int:
     mqk.library()  # fail loudly before any timing if libmqk.so is missing
     if args.tile:
         mqk.set_option("prefill_tile", args.tile)
+    if args.no_head_tiles:
+        mqk.set_option("head_tiles", 0)
     if args.only:
         run_only(args.only, args.steps, args.warmup, dev)
         return 0
@@ -413,7 +417,7 @@ def main(argv=None) -> int:
         log(f"[bench] config 4: {ms4 * 1e3:.1f} us/step, {a4:.0f} TFLOP/s")
         # mid token counts: Qwen3-8B prefill of B=1 x S=512 (the reference's smallest
         # published (B, S) point, docs/02_fused_qkv_rope.md:69-81, there at 0.6B shapes
-        # with paged attention included, so not comparable): the split-K tile launch
+        # with paged attention included, so not comparable): one round of single-head tiles
         msm, _ = bench_prefill(512, 1, 512, hidden, Hq, Hkv, 5, max(100, args.steps), 200, dev)
         am = flops(512, hidden, N) / (msm * 1e-3) / 1e12
         sec["mid_qwen3_8b_b1_s512"] = {"tokens_per_s": round(512 / (msm * 1e-3), 1),

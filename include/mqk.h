@@ -347,6 +347,10 @@ int mqk_fused_qkv_rope_ex_w4a16(const mqk_bf16* x, const int32_t* qw_q, const vo
  *                    over several workgroups of one XCD, fp32 partials in the workspace)
  *                    where a cost model prefers it to the decode blocks and the plain tile
  *                    launch; 0 = never; 2..16 = that split count whenever a split launch fits
+ *   "head_tiles"     1 (default): bf16 calls whose single-head tiles (64 x 128, else
+ *                    128 x 128) fill at most one round over the CUs run as one such tile
+ *                    launch where the cost model prefers it to the decode blocks and the
+ *                    split-K tile launch; 0: never
  * Returns MQK_OK or MQK_ERR_BAD_OPTION.  mqk_get_option also reads "device_cus" and
  * "device_xcds": the compute units and XCDs of the current device, as the planner and
  * the decode kernel's grid use them (hipDeviceGetAttribute; -1 for unknown names).

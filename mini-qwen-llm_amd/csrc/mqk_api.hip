@@ -48,6 +48,7 @@ std::atomic<int64_t> g_tail_split{1};
 std::atomic<int64_t> g_decode_blocks{16};  // most 64-row decode blocks for one call (T > 64)
 std::atomic<int64_t> g_decode_cost_model{1};  // 0: decode blocks whenever eligible (measurements)
 std::atomic<int64_t> g_decode_passes{16};  // most 64-row blocks one decode launch covers (1..16)
+std::atomic<int64_t> g_head_tiles{1};  // one round of single-head tiles where the planner models them fastest
 std::atomic<int64_t> g_tile_ksplit{1};  // split-K tile launches: 0 off, 1 by cost model, >= 2 that split count
 
 constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace (per head)
@@ -241,18 +242,38 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
   const TileVariant* sv = nullptr;
   double split_us = 1e30;
   const int ksplit = (!int4 && aligned && allow_split && M > 64) ? plan_tile_split(M, K, n_tiles, topo, sv, split_us) : 0;
+  // One round of single-head tiles (bf16): 64 x 128 (id 20) while ceil(M/64) x heads
+  // fit the CUs, else 128 x 128 with 8 waves (id 21) while ceil(M/128) x heads do.
+  // Neither needs a partial exchange.  Fitted on MI355X over hidden 2048 / 4096 /
+  // 5120 (40 / 48 / 56 heads, T = 128 .. 1024; within ~6 %): id 20 about
+  // 2 + 0.5 us per 64-k stage, id 21 about 2.5 + (0.6 + 0.0002 * tiles) us per stage.
+  const TileVariant* hv = nullptr;
+  double head_us = 1e30;
+  if (!int4 && aligned && M > 64 && g_prefill_tile.load() == 0 && g_head_tiles.load() != 0) {
+    const int64_t t20 = (M + 63) / 64 * n_tiles, t21 = (M + 127) / 128 * n_tiles;
+    const double stages = double(K / 64);
+    const int id = t20 <= cus ? 20 : (t21 <= cus ? 21 : 0);
+    for (int i = 0; id != 0 && i < tile_variant_count(); ++i)
+      if (tile_variant(i)->id == id) hv = tile_variant(i);
+    if (hv) head_us = id == 20 ? 2.0 + 0.5 * stages : 2.5 + stages * (0.6 + 0.0002 * double(t21));
+  }
   const bool blocks_ok = allow_blocks && aligned && M > 64 && g_prefill_tile.load() == 0 &&
                          g_decode_max_t.load() >= 64 && nblk <= g_decode_blocks.load() && blk_splits > 0;
   const bool forced_split = ksplit > 0 && g_tile_ksplit.load() >= 2;
-  if (blocks_ok && !forced_split && (!g_decode_cost_model.load() || (blocks_us <= tile_us && blocks_us <= split_us))) {
+  if (blocks_ok && !forced_split &&
+      (!g_decode_cost_model.load() || (blocks_us <= tile_us && blocks_us <= split_us && blocks_us <= head_us))) {
     pl.splits = blk_splits;
     pl.tail = M;
     pl.passes = int(std::min<int64_t>(per_launch, nblk));
     return pl;
   }
-  if (ksplit > 0 && (forced_split || split_us < tile_us)) {
+  if (ksplit > 0 && (forced_split || (split_us < tile_us && split_us <= head_us))) {
     pl.v = sv;
     pl.ksplit = ksplit;
+    return pl;
+  }
+  if (hv && head_us < tile_us) {
+    pl.v = hv;
     return pl;
   }
   pl.v = choose_tile_variant(int(g_prefill_tile.load()), M, n_tiles, int4, topo.cus);
@@ -916,6 +937,9 @@ int mqk_set_option(const char* name, int64_t value) {
   } else if (!strcmp(name, "decode_cost_model")) {
     if (value != 0 && value != 1) return fail(MQK_ERR_BAD_OPTION, "decode_cost_model must be 0 or 1");
     g_decode_cost_model = value;
+  } else if (!strcmp(name, "head_tiles")) {
+    if (value != 0 && value != 1) return fail(MQK_ERR_BAD_OPTION, "head_tiles must be 0 or 1");
+    g_head_tiles = value;
   } else if (!strcmp(name, "tile_ksplit")) {
     if (value < 0 || value > 16) return fail(MQK_ERR_BAD_OPTION, "tile_ksplit must be in [0, 16]");
     g_tile_ksplit = value;
@@ -939,6 +963,7 @@ int64_t mqk_get_option(const char* name) {
   if (!strcmp(name, "decode_passes")) return g_decode_passes.load();
   if (!strcmp(name, "decode_cost_model")) return g_decode_cost_model.load();
   if (!strcmp(name, "tile_ksplit")) return g_tile_ksplit.load();
+  if (!strcmp(name, "head_tiles")) return g_head_tiles.load();
   if (!strcmp(name, "decode_force_recompute")) return g_decode_force_recompute;
   if (!strcmp(name, "decode_max_spins")) return g_decode_max_spins;
   if (!strcmp(name, "device_cus")) return device_topology().cus;    // read-only: the current device's

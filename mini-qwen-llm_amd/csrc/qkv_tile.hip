@@ -381,7 +381,7 @@ hipError_t launch_dispatch(int int4, const ProblemArgs& p, const WeightArgs& w,
 }
 
 // ids 1-5: register-staged kernel above (bf16 and int4 weights);
-// ids 10-18: direct-to-LDS pipelined kernel (qkv_tile_dma.hip, bf16 weights only);
+// ids 10-21: direct-to-LDS pipelined kernel (qkv_tile_dma.hip, bf16 weights only);
 // ids 30-33: its int4-weight twin (W4A16 only).
 const TileVariant kVariants[] = {
     {1, 128, 1, 2, 256},
@@ -398,6 +398,9 @@ const TileVariant kVariants[] = {
     {16, 128, 3, 0, 512},
     {17, 256, 2, 0, 512},
     {18, 256, 2, 0, 512},
+    {19, 128, 1, 0, 256},
+    {20, 64, 1, 0, 256},
+    {21, 128, 1, 0, 512},
     {30, 128, 3, 0, 512},
     {31, 256, 2, 0, 512},
     {32, 128, 2, 0, 256},

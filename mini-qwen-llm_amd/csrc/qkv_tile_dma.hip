@@ -1213,6 +1213,9 @@ hipError_t launch_tile_dma(int id, const ProblemArgs& p, const WeightArgs& w, co
     case 16: return launch_dma<128, 3, 2, 4, 2, 64>(p, w, e, group_m, stream);  // 128x384, 2 stages of 64 k
     case 17: return launch_dma<256, 2, 4, 2, 2, 64>(p, w, e, group_m, stream);  // 256x256, 2 stages of 64 k
     case 18: return launch_dma<256, 2, 2, 4, 2, 64>(p, w, e, group_m, stream);  // 256x256 (128x64 waves), 64 k
+    case 19: return launch_dma<128, 1, 2, 2, 4, 64>(p, w, e, group_m, stream);  // 128x128, 4 waves, 4 stages of 64 k
+    case 20: return launch_dma<64, 1, 1, 4, 4, 64>(p, w, e, group_m, stream);   // 64x128, 4 waves (64x32)
+    case 21: return launch_dma<128, 1, 2, 4, 4, 64>(p, w, e, group_m, stream);  // 128x128, 8 waves (64x32)
     default: return hipErrorInvalidValue;
   }
 }
@@ -1228,6 +1231,9 @@ int tile_dma_lds_bytes(int id) {
     case 16: return DmaShape<128, 3, 2, 4, 2, 64>::kLdsBytes;
     case 17: return DmaShape<256, 2, 4, 2, 2, 64>::kLdsBytes;
     case 18: return DmaShape<256, 2, 2, 4, 2, 64>::kLdsBytes;
+    case 19: return DmaShape<128, 1, 2, 2, 4, 64>::kLdsBytes;
+    case 20: return DmaShape<64, 1, 1, 4, 4, 64>::kLdsBytes;
+    case 21: return DmaShape<128, 1, 2, 4, 4, 64>::kLdsBytes;
     case 30: return W4Shape<128, 3, 2, 4, 4>::kLdsBytes;
     case 31: return W4Shape<256, 2, 2, 4, 3>::kLdsBytes;
     case 32: return W4Shape<128, 2, 2, 2, 4>::kLdsBytes;

@@ -1,7 +1,7 @@
 """Shared test setup: import paths, the ``gpu`` marker, seeded input builders."""
 from __future__ import annotations
 
-
+import re
 import sys
 from pathlib import Path
 
@@ -97,6 +97,8 @@ _KERNEL_NAMES = (("decode_multi_kernel", "decode_multi"), ("decode_long_kernel",
 
 
 def _short_kernel_name(name: str):
+    if re.search(r"tile_dma_kernel(<\d+, 1,|ILi\d+ELi1E)", name):
+        return "tile_head"  # single-head tiles (64 x 128 or 128 x 128)
     for key, short in _KERNEL_NAMES:
         if key in name:
             return short
@@ -106,7 +108,7 @@ def _short_kernel_name(name: str):
 def launched_kernels(fn, *, warm=True):
     """The library kernels one call of ``fn`` launches, in launch order, as
     short names ("decode" = one 64-row block, "decode_multi" = several blocks,
-    "tile", "tile_split" = split-K tile, "tile_w4", "tile_reg", "row_scale", "norm_rope",
+    "tile", "tile_head" = single-head tiles, "tile_split" = split-K tile, "tile_w4", "tile_reg", "row_scale", "norm_rope",
     "f32" = the fp32 front), recorded with torch.profiler (the reference counts its
     kernels the same way, tests/test_fused_qkv_rope.py:287-311).  Other
     kernels (torch's own fills and copies) are left out."""

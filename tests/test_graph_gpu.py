@@ -86,6 +86,14 @@ def test_graph_replay_split_tile(device):
     args = case.args(device)
     small = Case(1, 64, 4096, 32, 8, seed=998, rows=8192,
                  positions=torch.arange(64, dtype=torch.int32)).args(device)
+    mqk.set_option("head_tiles", 0)  # (one round of single-head tiles would take this call)
+    try:
+        _replay_split_tile(mqk, launched_kernels, args, small, device)
+    finally:
+        mqk.set_option("head_tiles", 1)
+
+
+def _replay_split_tile(mqk, launched_kernels, args, small, device):
     assert launched_kernels(lambda: mqk.fused_qkv_rope(*args)) == ["tile_split"]
     stream = torch.cuda.Stream(device)
     with torch.cuda.stream(stream):

@@ -116,6 +116,38 @@ def test_decode_needs_workspace(lib):
     assert "workspace" in lib.mqk_last_error_detail().decode()
 
 
+@pytest.fixture
+def no_head_tiles():
+    """Plan without single-head tiles, so the split-K and decode-block models
+    below are the ones that decide."""
+    from mqk import _native
+    _native.set_option("head_tiles", 0)
+    yield
+    _native.set_option("head_tiles", 1)
+
+
+def test_head_tile_plan(lib):
+    """With single-head tiles (the default) a bf16 call whose 64 x 128 or
+    128 x 128 tiles fit one round over the CUs takes that launch and needs no
+    workspace: T = 256 and 512 at Qwen3-8B dims (48 heads: 192 tiles), and
+    hidden 2048 at T = 768 (40 heads, 6 x 40 = 240 tiles of 128 x 128).  At
+    T = 1024 (8 x 48 = 384 tiles) the split-K launch keeps the call."""
+    from mqk import _native
+    if _native.get_option("device_cus") != 256:
+        pytest.skip("the plan depends on the device's CU count (256 on MI355X)")
+    C = 4096 + 256 + 512 * 128
+    part = 128 * 384 * 4
+    _native.set_option("decode_blocks", 0)  # int4 then takes its tile kernel: no workspace
+    try:
+        assert lib.mqk_fused_qkv_rope_workspace_size(256, 32, 8, 4096) == 0
+        assert lib.mqk_fused_qkv_rope_workspace_size(512, 32, 8, 4096) == 0
+        assert lib.mqk_fused_qkv_rope_workspace_size(768, 32, 4, 2048) == 0
+        assert lib.mqk_fused_qkv_rope_workspace_size(1024, 32, 8, 4096) == C + 128 * 2 * part
+    finally:
+        _native.set_option("decode_blocks", 16)
+
+
+@pytest.mark.usefixtures("no_head_tiles")
 def test_workspace_size(lib):
     assert lib.mqk_fused_qkv_rope_workspace_size(2048, 32, 8, 4096) == 0     # tile kernel only
     assert lib.mqk_fused_qkv_rope_workspace_size(0, 32, 8, 4096) == 0
@@ -159,6 +191,7 @@ def test_workspace_size(lib):
         _native.set_option("decode_blocks", 16)
 
 
+@pytest.mark.usefixtures("no_head_tiles")
 def test_split_tile_plan(lib):
     """The planner's split-K tile model at Qwen3-8B dims (bf16 needs the split
     workspace; int4 keeps its decode blocks, so the size is the larger need):
@@ -181,6 +214,7 @@ def test_split_tile_plan(lib):
         _native.set_option("decode_blocks", 16)
 
 
+@pytest.mark.usefixtures("no_head_tiles")
 def test_split_tile_plan_other_shapes(lib):
     """The split-K model for 256 x 256 tiles, refitted on MI355X measurements at
     hidden 1024 / 2048 / 5120: the split counts it picks (shown by the partials'

@@ -52,25 +52,28 @@ def test_mid_t_decode_block_launches(T, plan, device):
         mqk.set_option("decode_cost_model", 1)
 
 
-@pytest.mark.parametrize("T,plan", [(128, ["decode_multi"]), (192, ["decode_multi"]), (256, ["tile_split"]),
-                                    (512, ["tile_split"]), (1024, ["tile_split"]), (2048, ["tile"])])
+@pytest.mark.parametrize("T,plan", [(128, ["decode_multi"]), (192, ["decode_multi"]), (256, ["tile_head"]),
+                                    (512, ["tile_head"]), (640, ["tile_head"]), (1024, ["tile_split"]),
+                                    (2048, ["tile"])])
 def test_default_plan_by_token_count(T, plan, device):
     """The default planner at hidden 4096 (bf16): decode blocks for a few 64-row
-    blocks, the split-K tile launch from about 200 tokens while tiles are fewer
-    than CUs, one tile per workgroup once the tiles fill the CUs."""
+    blocks, one round of single-head tiles from about 200 tokens while those fit
+    the CUs, the split-K tile launch beyond, one tile per workgroup once the
+    tiles fill the CUs."""
     case = Case(1, T, HID, HQ, HKV, seed=15 + T)
     assert launched_kernels(_bf16_call(case, device)) == plan
 
 
 @pytest.mark.parametrize("hidden,hq,hkv,T,plan", [
-    (1024, 16, 8, 128, ["decode_multi"]), (1024, 16, 8, 1024, ["tile"]),
-    (2048, 32, 4, 128, ["decode_multi"]), (2048, 32, 4, 512, ["tile_split"]), (2048, 32, 4, 1536, ["tile"]),
-    (5120, 40, 8, 1024, ["tile_split"])])
+    (1024, 16, 8, 128, ["tile_head"]), (1024, 16, 8, 1024, ["tile_head"]), (1024, 16, 8, 2048, ["tile"]),
+    (2048, 32, 4, 128, ["tile_head"]), (2048, 32, 4, 512, ["tile_head"]), (2048, 32, 4, 1536, ["tile"]),
+    (5120, 40, 8, 512, ["tile_head"]), (5120, 40, 8, 1024, ["tile_split"])])
 def test_default_plan_other_shapes(hidden, hq, hkv, T, plan, device):
     """The planner at the other Qwen3 attention shapes takes the kernel family
-    measured fastest on MI355X (bf16): e.g. hidden 2048 at T = 512 as split-K tiles
-    (32.7 us against 42.0 for decode blocks), hidden 5120 at T = 1024 as split-K
-    tiles (94.6 us against 117.2 for one tile per workgroup)."""
+    measured fastest on MI355X (bf16): e.g. hidden 2048 at T = 512 as one round of
+    128 x 128 single-head tiles (22.9 us against 31.9 for split-K tiles), hidden
+    5120 at T = 1024 as split-K tiles (94.6 us against 117.2 for one tile per
+    workgroup)."""
     case = Case(1, T, hidden, hq, hkv, seed=17 + T)
     assert launched_kernels(_bf16_call(case, device)) == plan
 
@@ -91,7 +94,7 @@ def test_tail_split_adds_one_decode_launch(device):
 
 
 @pytest.mark.parametrize("B,S,plan", [(64, 1, ["row_scale", "decode"]), (4, 512, ["row_scale", "tile"]),
-                                      (1, 128, ["row_scale", "decode_multi"]), (1, 256, ["row_scale", "tile_split"])])
+                                      (1, 128, ["row_scale", "decode_multi"]), (1, 256, ["row_scale", "tile_head"])])
 def test_input_norm_adds_its_pre_pass(B, S, plan, device):
     g = torch.Generator().manual_seed(15)
     pos = torch.randint(0, 4096, (B * S,), generator=g, dtype=torch.int32) if S == 1 else None

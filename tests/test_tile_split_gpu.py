@@ -129,8 +129,9 @@ def test_split_tile_varlen_paged_input_norm(device):
 
 @pytest.mark.parametrize("T,hidden,Hq,Hkv,plan", [
     (128, 5120, 40, 8, "tile_split"), (768, 5120, 40, 8, "tile_split"), (1024, 5120, 40, 8, "tile_split"),
-    (512, 2048, 32, 4, "tile_split"), (1024, 2048, 32, 4, "tile_split"), (256, 1024, 16, 8, "tile_split"),
-    (384, 1024, 16, 8, "tile")])
+    (512, 2048, 32, 4, "tile_head"), (1024, 2048, 32, 4, "tile_split"), (256, 1024, 16, 8, "tile_head"),
+    (384, 1024, 16, 8, "tile_head"), (320, 4096, 32, 8, "tile_head"), (640, 4096, 32, 8, "tile_head"),
+    (512, 5120, 40, 8, "tile_head")])
 def test_default_plan_other_shapes_matches_oracle(T, hidden, Hq, Hkv, plan, device):
     """The planner's own choices at the other Qwen3 attention shapes (Qwen3-14B
     heads at hidden 5120, 30B-A3B at 2048, 0.6B at 1024), decode-style positions,
@@ -159,10 +160,12 @@ def test_split_tile_counts_recomputed_tiles(device):
         # (torch pools its streams, so this stream's workspace may carry counts of
         # earlier calls: the test counts differences)
         start = mqk.decode_recomputes(device, stream)
-        assert launched_kernels(lambda: mqk.fused_qkv_rope(*args)) == ["tile_split"]
-        want = mqk.fused_qkv_rope(*args)
+        split = {"head_tiles": 0}  # (single-head tiles would take this call)
+        assert launched_kernels(lambda: _with_options(split, lambda: mqk.fused_qkv_rope(*args))) == ["tile_split"]
+        want = _with_options(split, lambda: mqk.fused_qkv_rope(*args))
         natural = mqk.decode_recomputes(device, stream)
-        got = _with_options({"decode_force_recompute": 1}, lambda: [mqk.fused_qkv_rope(*args) for _ in range(2)])
+        got = _with_options({"decode_force_recompute": 1, "head_tiles": 0},
+                            lambda: [mqk.fused_qkv_rope(*args) for _ in range(2)])
         after = mqk.decode_recomputes(device, stream)
     assert natural == start
     assert after - natural == 2 * (T // 128) * ((Hq + 2 * Hkv) // 3)  # 4 row tiles x 16 head tiles per call
