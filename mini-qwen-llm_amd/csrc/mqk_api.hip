@@ -242,20 +242,27 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
   const TileVariant* sv = nullptr;
   double split_us = 1e30;
   const int ksplit = (!int4 && aligned && allow_split && M > 64) ? plan_tile_split(M, K, n_tiles, topo, sv, split_us) : 0;
-  // One round of single-head tiles (bf16): 64 x 128 (id 20) while ceil(M/64) x heads
-  // fit the CUs, else 128 x 128 with 8 waves (id 21) while ceil(M/128) x heads do.
-  // Neither needs a partial exchange.  Fitted on MI355X over hidden 2048 / 4096 /
-  // 5120 (40 / 48 / 56 heads, T = 128 .. 1024; within ~6 %): id 20 about
-  // 2 + 0.5 us per 64-k stage, id 21 about 2.5 + (0.6 + 0.0002 * tiles) us per stage.
+  // One round of single-head tiles: 64 x 128 while ceil(M/64) x heads fit the CUs,
+  // else 128 x 128 with 8 waves while ceil(M/128) x heads do.  Neither needs a
+  // partial exchange.  Fitted on MI355X over hidden 2048 / 4096 / 5120 (40 / 48 / 56
+  // heads, T = 128 .. 1024; within ~6 %), per 64-k stage:
+  //   bf16 (ids 20 / 21): 2 + 0.5 us, and 2.5 + (0.6 + 0.0002 * tiles) us;
+  //   int4 (ids 35 / 34): 3.5 + 1.0 us, and 2.5 + 1.2 us (the dequantisation bounds
+  //   them: they win only where the decode blocks' long splits run one block per
+  //   launch, e.g. hidden 5120 at T = 384 / 512: 98 us against 119 / 158).
   const TileVariant* hv = nullptr;
   double head_us = 1e30;
-  if (!int4 && aligned && M > 64 && g_prefill_tile.load() == 0 && g_head_tiles.load() != 0) {
-    const int64_t t20 = (M + 63) / 64 * n_tiles, t21 = (M + 127) / 128 * n_tiles;
+  if (aligned && M > 64 && g_prefill_tile.load() == 0 && g_head_tiles.load() != 0) {
+    const int64_t t64 = (M + 63) / 64 * n_tiles, t128 = (M + 127) / 128 * n_tiles;
     const double stages = double(K / 64);
-    const int id = t20 <= cus ? 20 : (t21 <= cus ? 21 : 0);
+    const bool one64 = t64 <= cus, one128 = t128 <= cus;
+    const int id = one64 ? (int4 ? 35 : 20) : (one128 ? (int4 ? 34 : 21) : 0);
     for (int i = 0; id != 0 && i < tile_variant_count(); ++i)
       if (tile_variant(i)->id == id) hv = tile_variant(i);
-    if (hv) head_us = id == 20 ? 2.0 + 0.5 * stages : 2.5 + stages * (0.6 + 0.0002 * double(t21));
+    if (hv) {
+      if (int4) head_us = one64 ? 3.5 + 1.0 * stages : 2.5 + 1.2 * stages;
+      else head_us = one64 ? 2.0 + 0.5 * stages : 2.5 + stages * (0.6 + 0.0002 * double(t128));
+    }
   }
   const bool blocks_ok = allow_blocks && aligned && M > 64 && g_prefill_tile.load() == 0 &&
                          g_decode_max_t.load() >= 64 && nblk <= g_decode_blocks.load() && blk_splits > 0;

@@ -1216,6 +1216,8 @@ hipError_t launch_tile_dma(int id, const ProblemArgs& p, const WeightArgs& w, co
     case 19: return launch_dma<128, 1, 2, 2, 4, 64>(p, w, e, group_m, stream);  // 128x128, 4 waves, 4 stages of 64 k
     case 20: return launch_dma<64, 1, 1, 4, 4, 64>(p, w, e, group_m, stream);   // 64x128, 4 waves (64x32)
     case 21: return launch_dma<128, 1, 2, 4, 4, 64>(p, w, e, group_m, stream);  // 128x128, 8 waves (64x32)
+    case 22: return launch_dma<256, 1, 4, 2, 3, 64>(p, w, e, group_m, stream);  // 256x128, 8 waves (64x64), 3 stages
+    case 23: return launch_dma<128, 2, 2, 4, 3, 64>(p, w, e, group_m, stream);  // 128x256, 8 waves (64x64), 3 stages
     default: return hipErrorInvalidValue;
   }
 }
@@ -1234,10 +1236,14 @@ int tile_dma_lds_bytes(int id) {
     case 19: return DmaShape<128, 1, 2, 2, 4, 64>::kLdsBytes;
     case 20: return DmaShape<64, 1, 1, 4, 4, 64>::kLdsBytes;
     case 21: return DmaShape<128, 1, 2, 4, 4, 64>::kLdsBytes;
+    case 22: return DmaShape<256, 1, 4, 2, 3, 64>::kLdsBytes;
+    case 23: return DmaShape<128, 2, 2, 4, 3, 64>::kLdsBytes;
     case 30: return W4Shape<128, 3, 2, 4, 4>::kLdsBytes;
     case 31: return W4Shape<256, 2, 2, 4, 3>::kLdsBytes;
     case 32: return W4Shape<128, 2, 2, 2, 4>::kLdsBytes;
     case 33: return W4Shape<256, 2, 1, 8, 3>::kLdsBytes;
+    case 34: return W4Shape<128, 1, 2, 4, 4>::kLdsBytes;
+    case 35: return W4Shape<64, 1, 1, 4, 4>::kLdsBytes;
     default: return 0;
   }
 }
@@ -1268,6 +1274,8 @@ hipError_t launch_tile_dma_w4(int id, const ProblemArgs& p, const WeightArgs& w,
     case 31: return launch_dma_w4<256, 2, 2, 4, 3>(p, w, e, group_m, stream);  // 256x256, 3 stages
     case 32: return launch_dma_w4<128, 2, 2, 2, 4>(p, w, e, group_m, stream);  // 128x256, 4 waves
     case 33: return launch_dma_w4<256, 2, 1, 8, 3>(p, w, e, group_m, stream);  // 256x256, 256x32 waves
+    case 34: return launch_dma_w4<128, 1, 2, 4, 4>(p, w, e, group_m, stream);  // 128x128, 8 waves (64x32)
+    case 35: return launch_dma_w4<64, 1, 1, 4, 4>(p, w, e, group_m, stream);   // 64x128, 4 waves (64x32)
     default: return hipErrorInvalidValue;
   }
 }

@@ -89,6 +89,16 @@ def device():
     return torch.device("cuda:0")
 
 
+@pytest.fixture
+def no_head_tiles():
+    """Plan without single-head tiles, so a test of the decode-block or split-K
+    launches keeps the call on the path it is about."""
+    from mqk import _native
+    _native.set_option("head_tiles", 0)
+    yield
+    _native.set_option("head_tiles", 1)
+
+
 # Short names of the library's kernels, by (demangled or mangled) kernel name.
 _KERNEL_NAMES = (("decode_multi_kernel", "decode_multi"), ("decode_long_kernel", "decode"), ("decode_kernel", "decode"),
                  ("tile_dma_w4_kernel", "tile_w4"), ("tile_dma_split_kernel", "tile_split"), ("tile_dma_kernel", "tile"), ("tile_kernel", "tile_reg"),
@@ -99,6 +109,8 @@ _KERNEL_NAMES = (("decode_multi_kernel", "decode_multi"), ("decode_long_kernel",
 def _short_kernel_name(name: str):
     if re.search(r"tile_dma_kernel(<\d+, 1,|ILi\d+ELi1E)", name):
         return "tile_head"  # single-head tiles (64 x 128 or 128 x 128)
+    if re.search(r"tile_dma_w4_kernel(<\d+, 1,|ILi\d+ELi1E)", name):
+        return "tile_w4_head"  # their int4 twins
     for key, short in _KERNEL_NAMES:
         if key in name:
             return short
@@ -108,7 +120,7 @@ def _short_kernel_name(name: str):
 def launched_kernels(fn, *, warm=True):
     """The library kernels one call of ``fn`` launches, in launch order, as
     short names ("decode" = one 64-row block, "decode_multi" = several blocks,
-    "tile", "tile_head" = single-head tiles, "tile_split" = split-K tile, "tile_w4", "tile_reg", "row_scale", "norm_rope",
+    "tile", "tile_head" = single-head tiles, "tile_split" = split-K tile, "tile_w4", "tile_w4_head", "tile_reg", "row_scale", "norm_rope",
     "f32" = the fp32 front), recorded with torch.profiler (the reference counts its
     kernels the same way, tests/test_fused_qkv_rope.py:287-311).  Other
     kernels (torch's own fills and copies) are left out."""

@@ -92,8 +92,12 @@ def test_decode_blocks_w4a16(device):
     pos = torch.randint(0, 4096, (T,), generator=torch.Generator().manual_seed(7), dtype=torch.int32)
     dp = [tuple(t.to(device) for t in pr) for pr in projs]
     xd, args = x.to(device), (gq.to(device), gk.to(device), cos.to(device), sin.to(device))
-    out = mqk.fused_qkv_rope_w4a16(xd, *dp, *args, pos.to(device))
-    torch.cuda.synchronize()
+    mqk.set_option("head_tiles", 0)  # (one round of int4 single-head tiles would take this call)
+    try:
+        out = mqk.fused_qkv_rope_w4a16(xd, *dp, *args, pos.to(device))
+        torch.cuda.synchronize()
+    finally:
+        mqk.set_option("head_tiles", 1)
     for t0 in range(0, T, 64):
         alone = mqk.fused_qkv_rope_w4a16(xd[:, t0:t0 + 64].contiguous(), *dp, *args, pos[t0:t0 + 64].to(device))
         torch.cuda.synchronize()

@@ -195,7 +195,7 @@ def test_decode_repeatable(device):
             assert torch.equal(x, y)
 
 
-@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21])
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23])
 def test_tile_variants(variant, device):
     """Every prefill tile variant, on a shape with a row tail (M = 600) and a
     head count (24) that all of them can tile."""

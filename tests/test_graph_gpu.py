@@ -170,18 +170,24 @@ def _replay_checks(graph, outs, want, rerun):
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("T,plan", [(32, ["decode"]), (200, ["decode_multi"]),
-                                    (4128, ["tile_w4", "decode"])])
-def test_graph_replay_w4a16(T, plan, device):
+@pytest.mark.parametrize("T,head_tiles,plan", [(32, 1, ["decode"]), (200, 1, ["tile_w4_head"]),
+                                               (200, 0, ["decode_multi"]), (4128, 1, ["tile_w4", "decode"])])
+def test_graph_replay_w4a16(T, head_tiles, plan, device):
     """The W4A16 front under capture, one case per launch plan: the decode kernel
-    (T = 32), one four-block decode launch (T = 200), and the tile launch plus
-    the decode-kernel tail launch (T = 4128 = 16 row tiles of 256 + 32 rows,
-    whose 17th row tile would cost a second round over the CUs).  The plan is
-    checked from the kernels the eager call launches."""
+    (T = 32), one round of int4 single-head tiles (T = 200, the default plan),
+    one four-block decode launch (T = 200 without single-head tiles), and the tile
+    launch plus the decode-kernel tail launch (T = 4128 = 16 row tiles of 256 +
+    32 rows, whose 17th row tile would cost a second round over the CUs).  The
+    plan is checked from the kernels the eager call launches."""
+    import mqk
     from conftest import launched_kernels
     run = _w4a16_case(T, device)
-    assert launched_kernels(run) == plan
-    _graph_replay(run, device)
+    mqk.set_option("head_tiles", head_tiles)
+    try:
+        assert launched_kernels(run) == plan
+        _graph_replay(run, device)
+    finally:
+        mqk.set_option("head_tiles", 1)
 
 
 def _w4a16_case(T, device):
@@ -212,6 +218,7 @@ def _graph_replay(run, device):
     _replay_checks(graph, out, eager, run)
 
 
+@pytest.mark.usefixtures("no_head_tiles")
 def test_graph_survives_workspace_growth(device):
     """A graph captured with a small workspace replays correctly after a later
     eager call on the same stream needed a larger one.

@@ -116,16 +116,6 @@ def test_decode_needs_workspace(lib):
     assert "workspace" in lib.mqk_last_error_detail().decode()
 
 
-@pytest.fixture
-def no_head_tiles():
-    """Plan without single-head tiles, so the split-K and decode-block models
-    below are the ones that decide."""
-    from mqk import _native
-    _native.set_option("head_tiles", 0)
-    yield
-    _native.set_option("head_tiles", 1)
-
-
 def test_head_tile_plan(lib):
     """With single-head tiles (the default) a bf16 call whose 64 x 128 or
     128 x 128 tiles fit one round over the CUs takes that launch and needs no

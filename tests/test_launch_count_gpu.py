@@ -120,15 +120,16 @@ def test_w4a16_front_is_one_launch(device):
 
 
 @pytest.mark.parametrize("hidden,hq,hkv,T,plan", [
-    (1024, 16, 8, 512, ["decode_multi"]), (1024, 16, 8, 1024, ["tile_w4"]),
+    (1024, 16, 8, 512, ["tile_w4_head"]), (1024, 16, 8, 1024, ["tile_w4_head"]),
     (2048, 32, 4, 1024, ["decode_multi"]),
-    (5120, 40, 8, 256, ["decode"] * 4), (5120, 40, 8, 768, ["tile_w4"])])
+    (5120, 40, 8, 256, ["decode"] * 4), (5120, 40, 8, 512, ["tile_w4_head"]), (5120, 40, 8, 768, ["tile_w4"])])
 def test_w4a16_plan_other_shapes(hidden, hq, hkv, T, plan, device):
     """The int4 planner at the other Qwen3 attention shapes takes the kernel family
-    measured fastest on MI355X: e.g. hidden 1024 at T = 1024 on the tile kernel
-    (42.8 us against 55.7 for decode blocks); hidden 5120, whose decode launches
-    hold one 64-row block each, as four decode launches at T = 256 (83 us
-    against 170) and the tile kernel at T = 768 (174 us against 241)."""
+    measured fastest on MI355X: e.g. hidden 1024 at T = 512 and 1024 as one round
+    of int4 single-head tiles (22.7 / 26.0 us against 34.4 / 41.7); hidden 5120,
+    whose decode launches hold one 64-row block each, as four decode launches at
+    T = 256 (83 us against 170), single-head tiles at T = 512 (98.7 us against
+    158.4) and the tile kernel at T = 768 (174 us against 241)."""
     import mqk
     g = torch.Generator(device=device).manual_seed(18 + T)
     D = 128

@@ -19,8 +19,8 @@ from conftest import HEAD_DIM, Case
 pytestmark = pytest.mark.gpu
 
 D = HEAD_DIM
-BF16_DMA_VARIANTS = [10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21]
-INT4_DMA_VARIANTS = [30, 31, 32, 33]
+BF16_DMA_VARIANTS = [10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21, 22, 23]
+INT4_DMA_VARIANTS = [30, 31, 32, 33, 34, 35]
 
 
 def _with_variant(variant, fn):

@@ -72,6 +72,7 @@ def test_w4a16_gemm(M, K, N, device):
 
 
 @pytest.mark.parametrize("M", [1, 16, 200])
+@pytest.mark.usefixtures("no_head_tiles")
 def test_w4a16_gemm_decode_path_matches_tile(M, device):
     """Small M runs on the split-K decode kernel (the reference's decode GEMV
     regime, w4a16_gemm.py:110-189): it must agree with the tile kernel (forced
@@ -193,8 +194,8 @@ def test_fused_w4a16(B, S, positions_mode, scale_dtype, device):
 
 
 @pytest.mark.parametrize("S,hidden,Hq,Hkv,plan", [
-    (256, 5120, 40, 8, ["decode"] * 4), (768, 5120, 40, 8, ["tile_w4"]), (1024, 1024, 16, 8, ["tile_w4"]),
-    (512, 1024, 16, 8, ["decode_multi"])])
+    (256, 5120, 40, 8, ["decode"] * 4), (512, 5120, 40, 8, ["tile_w4_head"]), (768, 5120, 40, 8, ["tile_w4"]),
+    (1024, 1024, 16, 8, ["tile_w4_head"]), (512, 1024, 16, 8, ["tile_w4_head"]), (640, 2048, 32, 4, ["tile_w4_head"])])
 def test_fused_w4a16_default_plan_other_shapes(S, hidden, Hq, Hkv, plan, device):
     """The int4 planner's choices at the other Qwen3 attention shapes, with
     decode-style positions, against the oracle."""
@@ -442,7 +443,7 @@ def test_qk_norm_rope_matches_fused(device):
     assert (ko.float() - kf.float()).abs().max().item() <= 4e-2
 
 
-@pytest.mark.parametrize("variant", [1, 2, 3, 4, 30, 31, 32, 33])
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 30, 31, 32, 33, 34, 35])
 @pytest.mark.parametrize("scale_dtype", [torch.bfloat16, torch.float16])
 def test_fused_w4a16_tile_variants(variant, scale_dtype, device):
     """Every int4 tile variant on a ragged-length shape (T = 600: row tail), 24 heads,
