@@ -148,8 +148,10 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
   constexpr int kPasses = BM / kRowStep;
   static_assert(BM % kRowStep == 0, "the epilogue's row passes must cover the tile");
   // gamma / cos / sin depend only on the token: with few rows per thread they are
-  // loaded once for all NH heads of the tile (16 VGPRs per row)
-  constexpr bool kPreload = kPasses <= 4;
+  // loaded once for all NH heads of the tile (16 VGPRs per row).  Four rows' worth
+  // beside the 128 accumulators of an 8-wave 256-row tile (256 VGPRs per lane at
+  // two waves per SIMD) spilled; 4-wave tiles (one wave per SIMD) have room.
+  constexpr bool kPreload = kPasses <= 2 || (kPasses <= 4 && THREADS <= 256);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
