@@ -44,7 +44,7 @@ enum mqk_status {
   MQK_OK = 0,
   MQK_ERR_NULL_POINTER = -1,     /* a required pointer is NULL */
   MQK_ERR_BAD_SHAPE = -2,        /* a size is negative, zero where it must not be, or inconsistent */
-  MQK_ERR_UNSUPPORTED = -3,      /* a valid shape this library does not implement (e.g. head_dim != 128) */
+  MQK_ERR_UNSUPPORTED = -3,      /* a valid shape this library does not implement (e.g. head_dim 256) */
   MQK_ERR_MISALIGNED = -4,       /* a pointer is not 16-byte aligned */
   MQK_ERR_WORKSPACE = -5,        /* workspace NULL or smaller than mqk_*_workspace_size() */
   MQK_ERR_HIP = -6,              /* a HIP runtime call failed (launch, attribute query) */
@@ -85,7 +85,10 @@ const char* mqk_last_error_detail(void);
  *                                 workspace must not be used by two calls that
  *                                 may overlap (same or different streams).
  *
- * Supported: D == 128, hidden % 64 == 0, Hq >= 1, Hkv >= 1, T >= 0 (T == 0 is
+ * Supported: D == 128, or D == 64 with Hq and Hkv even (the kernels run
+ * 128-column blocks of two heads; the reference's default Qwen3Config has
+ * head_dim 64, mini_qwen/config.py:13), hidden % 64 == 0, Hq >= 1, Hkv >= 1,
+ * T >= 0 (T == 0 is
  * a no-op), x/w/q/k/v 16-byte aligned.  Numerics: bf16 inputs, fp32
  * accumulation on MFMA, the norm and RoPE are applied to the fp32 accumulator
  * (the projection is not rounded to bf16 before the norm), one bf16 rounding
@@ -125,7 +128,9 @@ int mqk_fused_qkv_rope_f16(const mqk_f16* x, const mqk_f16* w_q, const mqk_f16* 
                            int D, int64_t cos_rows, float eps, mqk_f16* q, mqk_f16* k, mqk_f16* v, void* stream);
 
 /* Workspace bytes needed by mqk_fused_qkv_rope_bf16 / _w4a16 for these sizes
- * (0 when the chosen kernels need none). */
+ * (0 when the chosen kernels need none).  Hq and Hkv are counted in 128-column
+ * blocks: the head counts for D == 128, Hq / 2 and Hkv / 2 for D == 64.  The
+ * same holds for mqk_fused_qkv_rope_ex_workspace_size. */
 size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden);
 
 /*

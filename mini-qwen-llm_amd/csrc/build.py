@@ -2,6 +2,8 @@
 
     python mini-qwen-llm_amd/csrc/build.py            # build
     python mini-qwen-llm_amd/csrc/build.py --verbose  # echo the hipcc lines
+    python mini-qwen-llm_amd/csrc/build.py --incremental  # recompile only sources
+                                                          # newer than their object
 
 Every translation unit is compiled in parallel, then linked into
 ``mini-qwen-llm_amd/mqk/libmqk.so`` (the location the ``mqk`` package loads).
@@ -26,9 +28,10 @@ OUT = PKG / "libmqk.so"
 BUILD_DIR = CSRC.parent / "_build"
 SOURCES = ["qkv_tile.hip", "qkv_tile_dma.hip", "qkv_decode.hip", "norm_rope.hip", "input_norm.hip", "qkv_f32.hip",
            "mqk_api.hip"]
-# Sources whose kernels must not use scratch memory (register spills): the
-# compiler's resource-usage remarks are checked and the build fails otherwise.
-NO_SCRATCH = {"qkv_decode.hip", "qkv_f32.hip"}
+# No kernel may use scratch memory (register spills, or an array the compiler
+# could not keep in registers): the compiler's resource-usage remarks of every
+# source are checked and the build fails otherwise.
+NO_SCRATCH = set(SOURCES)
 ARCH = "gfx950"
 
 COMMON_FLAGS = [
@@ -67,8 +70,19 @@ def _scratch_kernels(remarks: str) -> list[str]:
     return bad
 
 
-def _compile(src: str, verbose: bool) -> Path:
+def _up_to_date(src: str, obj: Path) -> bool:
+    """The object is newer than its source and every header of csrc/."""
+    if not obj.exists():
+        return False
+    t = obj.stat().st_mtime
+    deps = [CSRC / src, *CSRC.glob("*.h"), CSRC.parent.parent / "include" / "mqk.h", Path(__file__)]
+    return all(d.stat().st_mtime < t for d in deps if d.exists())
+
+
+def _compile(src: str, verbose: bool, incremental: bool = False) -> Path:
     obj = BUILD_DIR / (Path(src).stem + ".o")
+    if incremental and _up_to_date(src, obj):
+        return obj
     check = src in NO_SCRATCH
     cmd = [_hipcc(), *COMMON_FLAGS, *(["-Rpass-analysis=kernel-resource-usage"] if check else []),
            "-c", str(CSRC / src), "-o", str(obj)]
@@ -88,10 +102,10 @@ def _compile(src: str, verbose: bool) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
+def build(verbose: bool = False, incremental: bool = False) -> Path:
     BUILD_DIR.mkdir(exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
+        objs = list(ex.map(lambda s: _compile(s, verbose, incremental), SOURCES))
     tmp = OUT.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     if verbose:
@@ -106,8 +120,9 @@ def build(verbose: bool = False) -> Path:
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--incremental", action="store_true", help="skip sources whose object is up to date")
     args = ap.parse_args(argv)
-    out = build(args.verbose)
+    out = build(args.verbose, args.incremental)
     print(f"built {out}")
     return 0
 

@@ -160,12 +160,15 @@ struct Plan {
 //   256 x 256 (hidden 1024 / 2048 / 5120 with 32 / 40 / 56 heads, T = 128 .. 1536,
 //     2 to 8 splits; rms error 1.5 us): 12.6 us, 1.6 us per stage of
 //     ceil(stages / splits), 0.195 us per MB, 0.35 us per unit.
-int plan_tile_split(int64_t M, int64_t K, int n_tiles, const Topology& topo, const TileVariant*& v, double& us) {
+// (The 256 x 256 split kernel has no input-norm form: with the norm's registers it
+// would spill.)
+int plan_tile_split(int64_t M, int64_t K, int n_tiles, const Topology& topo, bool in_norm, const TileVariant*& v,
+                    double& us) {
   v = nullptr;
   us = 1e30;
   const int64_t req = g_tile_ksplit.load();
   if (req == 0 || g_prefill_tile.load() != 0) return 0;
-  const int id = n_tiles % 3 == 0 ? 16 : (n_tiles % 2 == 0 ? 18 : 0);
+  const int id = n_tiles % 3 == 0 ? 16 : (n_tiles % 2 == 0 && !in_norm ? 18 : 0);
   if (id == 0) return 0;
   for (int i = 0; i < tile_variant_count(); ++i)
     if (tile_variant(i)->id == id) v = tile_variant(i);
@@ -241,7 +244,7 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
   // per-tile launch and the decode blocks
   const TileVariant* sv = nullptr;
   double split_us = 1e30;
-  const int ksplit = (!int4 && aligned && allow_split && M > 64) ? plan_tile_split(M, K, n_tiles, topo, sv, split_us) : 0;
+  const int ksplit = (!int4 && aligned && allow_split && M > 64) ? plan_tile_split(M, K, n_tiles, topo, in_norm, sv, split_us) : 0;
   // One round of single-head tiles: 64 x 128 while ceil(M/64) x heads fit the CUs,
   // else 128 x 128 with 8 waves while ceil(M/128) x heads do.  Neither needs a
   // partial exchange.  Fitted on MI355X over hidden 2048 / 4096 / 5120 (40 / 48 / 56
@@ -434,13 +437,28 @@ size_t mqk_fused_qkv_rope_ex_workspace_size(int64_t T, int Hq, int Hkv, int64_t 
   return n;
 }
 
+// head_dim: 128, or 64 with even head counts (the kernels then run 128-column
+// blocks of two heads each: Hq * D / 128 and Hkv * D / 128 of them).
+static int check_head_dim(int D, int Hq, int Hkv) {
+  if (D % 2 != 0) return fail(MQK_ERR_BAD_SHAPE, "head_dim must be even (RoPE rotate_half), got %d", D);
+  if (D != kHeadDim && D != 64) return fail(MQK_ERR_UNSUPPORTED, "head_dim %d not supported (128 or 64)", D);
+  if (D == 64 && (Hq % 2 != 0 || Hkv % 2 != 0))
+    return fail(MQK_ERR_UNSUPPORTED, "head_dim 64 needs even head counts (got Hq=%d, Hkv=%d)", Hq, Hkv);
+  return MQK_OK;
+}
+
+// Head counts -> 128-column block counts (identity for head_dim 128).
+static void to_blocks(int D, int& Hq, int& Hkv) {
+  Hq = Hq * D / kHeadDim;
+  Hkv = Hkv * D / kHeadDim;
+}
+
 static int validate_fused_common(const mqk_bf16* x, int64_t T, int64_t S, int64_t hidden, int Hq,
                                  int Hkv, int D, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
                                  bool kv_optional = false) {
   if (T < 0 || hidden <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0)
     return fail(MQK_ERR_BAD_SHAPE, "need T >= 0, hidden > 0, Hq > 0, Hkv > 0, D > 0");
-  if (D % 2 != 0) return fail(MQK_ERR_BAD_SHAPE, "head_dim must be even (RoPE rotate_half), got %d", D);
-  if (D != kHeadDim) return fail(MQK_ERR_UNSUPPORTED, "head_dim %d not supported (only 128)", D);
+  if (int st = check_head_dim(D, Hq, Hkv); st != MQK_OK) return st;
   if (hidden % kBK != 0)
     return fail(MQK_ERR_UNSUPPORTED, "hidden %lld must be a multiple of 64", (long long)hidden);
   if (Hq + 2 * Hkv > kMaxTiles) return fail(MQK_ERR_UNSUPPORTED, "Hq + 2*Hkv must be <= %d", kMaxTiles);
@@ -520,6 +538,7 @@ static int fused_bf16_impl(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf1
     return fail(MQK_ERR_MISALIGNED, "weights must be 16-byte aligned");
   st = check_rope_args(q_gamma, k_gamma, cos, sin, S, cos_rows, positions, eps, varlen);
   if (st != MQK_OK) return st;
+  to_blocks(D, Hq, Hkv);
 
   ProblemArgs p{x, T, hidden, Hq + 2 * Hkv};
   WeightArgs w{};
@@ -530,6 +549,7 @@ static int fused_bf16_impl(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf1
   w.n_cols[1] = w.n_cols[2] = int64_t(Hkv) * kHeadDim;
   EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
                                      q, k, v, Hq, Hkv);
+  e.head_dim = D;
   if ((st = apply_ext(ext, positions, S, T, p, e)) != MQK_OK) return st;
   return run_fused(0, p, w, e, ext ? ext->in_eps : 0.f, workspace, ws_bytes, static_cast<hipStream_t>(stream));
 }
@@ -550,8 +570,7 @@ static int fused_f32_impl(bool half, const void* x, const void* w_q, const void*
                           int64_t cos_rows, float eps, void* q, void* k, void* v, void* stream) {
   if (T < 0 || hidden <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0)
     return fail(MQK_ERR_BAD_SHAPE, "need T >= 0, hidden > 0, Hq > 0, Hkv > 0, D > 0");
-  if (D % 2 != 0) return fail(MQK_ERR_BAD_SHAPE, "head_dim must be even (RoPE rotate_half), got %d", D);
-  if (D != kHeadDim) return fail(MQK_ERR_UNSUPPORTED, "head_dim %d not supported (only 128)", D);
+  if (int st = check_head_dim(D, Hq, Hkv); st != MQK_OK) return st;
   if (hidden % kF32BK != 0)
     return fail(MQK_ERR_UNSUPPORTED, "hidden %lld must be a multiple of %d", (long long)hidden, kF32BK);
   if (Hq + 2 * Hkv > kMaxTiles) return fail(MQK_ERR_UNSUPPORTED, "Hq + 2*Hkv must be <= %d", kMaxTiles);
@@ -564,7 +583,9 @@ static int fused_f32_impl(bool half, const void* x, const void* w_q, const void*
     return fail(MQK_ERR_MISALIGNED, "x/q/k/v and the weights must be 16-byte aligned");
   int st = check_rope_args(q_gamma, k_gamma, cos, sin, S, cos_rows, positions, eps);
   if (st != MQK_OK) return st;
+  to_blocks(D, Hq, Hkv);
   F32Args a{};
+  a.head_dim = D;
   a.x = x;
   a.w[0] = w_q;
   a.w[1] = w_k;
@@ -609,8 +630,9 @@ int mqk_fused_qkv_rope_f16(const mqk_f16* x, const mqk_f16* w_q, const mqk_f16* 
 
 // ---- allocation-free variant of mqk_fused_qkv_rope_bf16 ---------------------------------
 // The decode kernel's scratch (its arrival counters, then its fp32 split partials)
-// lives in this file-scope device array instead of a caller workspace: 4.25 KiB
-// of counters plus 8 MiB of partials, enough for one 64-row block of any head count
+// lives in this file-scope device array instead of a caller workspace: 68.25 KiB
+// of counters (the decode arrival counters, a statistics line and the split-K
+// tile words) plus 8 MiB of partials, enough for one 64-row block of any head count
 // up to one split per CU (e.g. 48 heads x 5 splits at hidden 4096: 7.5 MiB).
 // Each GPU holds its own copy for the life of the process.  Host code never
 // passes `scratch` itself to a kernel (in host code the name is a stand-in, not a
@@ -719,16 +741,17 @@ int mqk_qk_norm_rope_bf16(const mqk_bf16* q_raw, const mqk_bf16* k_raw, const mq
                           int64_t cos_rows, float eps, mqk_bf16* q_out, mqk_bf16* k_out,
                           void* stream) {
   if (T < 0 || Hq < 0 || Hkv < 0 || D <= 0) return fail(MQK_ERR_BAD_SHAPE, "negative size");
-  if (D % 2 != 0) return fail(MQK_ERR_BAD_SHAPE, "head_dim must be even (RoPE rotate_half), got %d", D);
-  if (D != kHeadDim) return fail(MQK_ERR_UNSUPPORTED, "head_dim %d not supported (only 128)", D);
+  if (int st = check_head_dim(D, Hq, Hkv); st != MQK_OK) return st;
   if (T == 0 || Hq + Hkv == 0) return ok();
+  to_blocks(D, Hq, Hkv);
   if ((Hq > 0 && (!q_raw || !q_out)) || (Hkv > 0 && (!k_raw || !k_out)))
     return fail(MQK_ERR_NULL_POINTER, "q/k input or output is NULL");
   int st = check_rope_args(Hq ? q_gamma : k_gamma, Hkv ? k_gamma : q_gamma, cos, sin, S, cos_rows,
                            positions, eps);
   if (st != MQK_OK) return st;
-  const EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
-                                           q_out, k_out, nullptr, Hq, Hkv);
+  EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
+                                     q_out, k_out, nullptr, Hq, Hkv);
+  e.head_dim = D;
   return hip_status(launch_norm_rope(q_raw, k_raw, e, T, static_cast<hipStream_t>(stream)),
                     "norm_rope kernel launch");
 }
@@ -836,6 +859,7 @@ static int fused_w4a16_impl(const mqk_bf16* x, const int32_t* qw_q, const void* 
   int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v, ext && ext->kv);
   if (st != MQK_OK) return st;
   if (T == 0) return ok();
+  to_blocks(D, Hq, Hkv);
   const int64_t nq = int64_t(Hq) * kHeadDim, nkv = int64_t(Hkv) * kHeadDim;
   if ((st = validate_int4(qw_q, sc_q, qz_q, hidden, nq, group, scale_type, "q_proj")) != MQK_OK) return st;
   if ((st = validate_int4(qw_k, sc_k, qz_k, hidden, nkv, group, scale_type, "k_proj")) != MQK_OK) return st;
@@ -859,6 +883,7 @@ static int fused_w4a16_impl(const mqk_bf16* x, const int32_t* qw_q, const void* 
   w.scale_fp16 = scale_type == MQK_SCALE_FP16;
   EpilogueArgs e = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps,
                                      q, k, v, Hq, Hkv);
+  e.head_dim = D;
   if ((st = apply_ext(ext, positions, S, T, p, e)) != MQK_OK) return st;
   return run_fused(1, p, w, e, ext ? ext->in_eps : 0.f, workspace, ws_bytes, static_cast<hipStream_t>(stream));
 }

@@ -15,7 +15,11 @@
 
 namespace mqk {
 
-constexpr int kHeadDim = 128;   // head_dim handled by the kernels (all Qwen3 models)
+// The kernels tile the projection in 128-column blocks.  With head_dim 128 (every
+// Qwen3 checkpoint) a block is one head; with head_dim 64 (the reference's
+// default Qwen3Config) it is two heads, and the epilogues normalise and rotate
+// each 64-column half on its own (pair_runs, head_sum, head_rms).
+constexpr int kHeadDim = 128;   // columns of one block (one head of 128, or two of 64)
 constexpr int kHalfDim = 64;
 constexpr int kBK = 64;         // K extent of one staged tile (8 chunks of 16 bytes per row)
 
@@ -327,6 +331,34 @@ __device__ __forceinline__ float sum8_lanes(float v) {
   return v;
 }
 
+// The two runs of 8 columns that thread c (0..7) of a block row takes in the
+// norm / RoPE epilogues, chosen so that column d of the first run and column
+// d + D/2 of the second are a RoPE pair of one head, and the 8 (D = 128) or 4
+// (D = 64) threads sharing a head are an aligned lane group:
+//   D = 128: columns [8c, 8c+8) and [64+8c, +8); dims the same.
+//   D = 64:  head h = c / 4 of the block, j = c % 4: columns 64h + [8j, +8) and
+//            64h + 32 + [8j, +8); dims [8j, +8) and [32+8j, +8) of head h.
+struct PairRuns {
+  int col_lo, col_hi;  // column of the runs' first element within the 128-column block
+  int dim_lo, dim_hi;  // head dim of the same (indexes gamma and the cos / sin rows)
+};
+__device__ __forceinline__ PairRuns pair_runs(int c, int head_dim) {
+  if (head_dim == 64) {
+    const int h = c >> 2, j = c & 3;
+    return PairRuns{64 * h + 8 * j, 64 * h + 32 + 8 * j, 8 * j, 32 + 8 * j};
+  }
+  return PairRuns{8 * c, kHalfDim + 8 * c, 8 * c, kHalfDim + 8 * c};
+}
+
+// Sum over the lanes that hold one head's runs (pair_runs): the aligned group of
+// 8 lanes for head_dim 128 (bit for bit sum8_lanes), of 4 lanes for head_dim 64.
+__device__ __forceinline__ float head_sum(float v, int head_dim) {
+  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+  if (head_dim != 64) v += dpp_move<0x141>(v);  // row_half_mirror: the other quad
+  return v;
+}
+
 // Epilogue arithmetic with every rounding step written out (no contraction left
 // to the compiler), so that each tile shape's instantiation gives identical bits
 // for the same accumulators however the compiler schedules it.
@@ -340,10 +372,10 @@ __device__ __forceinline__ float run_sumsq(const float (&lo)[8], const float (&h
   return ss;
 }
 
-// 1 / rms of a head from the sum of squares of its 128 dims.
-__device__ __forceinline__ float head_rms(float ss, float eps) {
+// 1 / rms of a head from the sum of squares of its head_dim (128 or 64) dims.
+__device__ __forceinline__ float head_rms(float ss, float eps, int head_dim = kHeadDim) {
 #pragma clang fp contract(off)
-  return rsqrtf(__builtin_fmaf(ss, 1.0f / float(kHeadDim), eps));
+  return rsqrtf(__builtin_fmaf(ss, head_dim == 64 ? 1.0f / 64.0f : 1.0f / float(kHeadDim), eps));
 }
 
 __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }

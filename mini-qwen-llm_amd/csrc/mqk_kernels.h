@@ -6,6 +6,8 @@
 
 namespace mqk {
 
+constexpr int kHeadDimDefault = 128;
+
 // Weight source of the projection.  A 128-column tile h (one head) belongs to
 // projection 0 (Q) for h < Hq, 1 (K) for h < Hq + Hkv, else 2 (V); for a plain
 // GEMM (w4a16_gemm) every tile belongs to projection 0 and Hq is the tile count.
@@ -59,6 +61,10 @@ struct EpilogueArgs {
   // split over two launches); positions, slots and varlen offsets are indexed by
   // the call's token index, outputs and x by the launch's rows.
   int64_t t0;
+  // Head dim, 128 or 64.  Hq / Hkv above (and the problem's n_tiles) count
+  // 128-column blocks, Hq * head_dim / 128 of them: two heads of 64 per block.
+  // gamma has head_dim entries and the cos / sin rows are head_dim apart.
+  int head_dim = kHeadDimDefault;
 };
 
 struct ProblemArgs {
@@ -184,6 +190,8 @@ struct F32Args {
   const int32_t* seq_pos0 = nullptr;
   int64_t n_seqs = 0;
   int64_t t0 = 0;
+  // head dim, 128 or 64 (Hq / Hkv then count 128-column blocks of two heads)
+  int head_dim = kHeadDimDefault;
 };
 constexpr int kF32BK = 32;       // k extent of one staged tile of the fp32 / fp16 front
 // rows: token rows per workgroup, 32 or 16; half: fp16 elements (else fp32)

@@ -1,8 +1,9 @@
 // Standalone QK-Norm + RoPE on already-projected q/k (bf16 in, bf16 out): the
 // functional twin of the reference's _qk_norm_rope_kernel
-// (mini_qwen/kernels/fused_qkv_rope.py:46-127).  One wave per (token, head);
-// lane l owns the RoPE pair (d, d+64) = (l, l+64), so the rotation is
-// lane-local and the sum of squares is one 64-lane butterfly.  Used by the
+// (mini_qwen/kernels/fused_qkv_rope.py:46-127).  One wave per (token, 128-column
+// block): with head_dim 128 lane l owns the RoPE pair (l, l+64), with head_dim 64
+// lanes 32h + j own the pair (j, j+32) of the block's head h, so the rotation is
+// lane-local and the sum of squares is one 64- or 32-lane butterfly.  Used by the
 // unfused paths (already-projected activations); the fused kernels carry their
 // own register epilogue.
 #include "mqk_device.h"
@@ -17,7 +18,7 @@ __global__ void __launch_bounds__(kNrWaves * 64)
 norm_rope_kernel(const uint16_t* __restrict__ q_raw, const uint16_t* __restrict__ k_raw,
                  EpilogueArgs e, int64_t T) {
   const int lane = threadIdx.x & 63;
-  const int heads = e.Hq + e.Hkv;
+  const int heads = e.Hq + e.Hkv;  // 128-column blocks
   const int64_t item = int64_t(blockIdx.x) * kNrWaves + (threadIdx.x >> 6);
   if (item >= T * heads) return;
   const int64_t t = item / heads;
@@ -28,23 +29,29 @@ norm_rope_kernel(const uint16_t* __restrict__ q_raw, const uint16_t* __restrict_
   const uint16_t* src = (is_q ? q_raw : k_raw) + (t * H + hh) * kHeadDim;
   uint16_t* dst = (is_q ? e.q : e.k) + (t * H + hh) * kHeadDim;
   const uint16_t* gamma = is_q ? e.q_gamma : e.k_gamma;
+  // head_dim 128: lane l owns the pair (l, l+64) of the block's head; head_dim 64:
+  // lanes 32h .. 32h+31 own the pairs (j, j+32) of head h of the block (j = l % 32)
+  const int hd = e.head_dim, hd2 = hd / 2;
+  const int d = hd == 64 ? (lane & 31) : lane;
+  const int col = hd == 64 ? (lane >> 5) * 64 + d : d;
 
-  const float x1 = bf16_to_f32(src[lane]);
-  const float x2 = bf16_to_f32(src[lane + kHalfDim]);
+  const float x1 = bf16_to_f32(src[col]);
+  const float x2 = bf16_to_f32(src[col + hd2]);
   float ss = x1 * x1 + x2 * x2;
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
-  const float rms = rsqrtf(ss * (1.0f / float(kHeadDim)) + e.eps);
-  const float x1n = x1 * rms * bf16_to_f32(gamma[lane]);
-  const float x2n = x2 * rms * bf16_to_f32(gamma[lane + kHalfDim]);
-  const int64_t prow = rope_row(e, t) * kHeadDim;
-  const float c1 = bf16_to_f32(e.cos[prow + lane]);
-  const float c2 = bf16_to_f32(e.cos[prow + lane + kHalfDim]);
-  const float s1 = bf16_to_f32(e.sin[prow + lane]);
-  const float s2 = bf16_to_f32(e.sin[prow + lane + kHalfDim]);
+  for (int m = 32; m >= 1; m >>= 1)
+    if (m < hd2 || hd != 64) ss += __shfl_xor(ss, m);
+  const float rms = rsqrtf(ss * (hd == 64 ? 1.0f / 64.0f : 1.0f / float(kHeadDim)) + e.eps);
+  const float x1n = x1 * rms * bf16_to_f32(gamma[d]);
+  const float x2n = x2 * rms * bf16_to_f32(gamma[d + hd2]);
+  const int64_t prow = rope_row(e, t) * hd;
+  const float c1 = bf16_to_f32(e.cos[prow + d]);
+  const float c2 = bf16_to_f32(e.cos[prow + d + hd2]);
+  const float s1 = bf16_to_f32(e.sin[prow + d]);
+  const float s2 = bf16_to_f32(e.sin[prow + d + hd2]);
   // in-place safe: every lane has read its inputs before the butterfly completes
-  dst[lane] = f32_to_bf16(x1n * c1 - x2n * s1);
-  dst[lane + kHalfDim] = f32_to_bf16(x2n * c2 + x1n * s2);
+  dst[col] = f32_to_bf16(x1n * c1 - x2n * s1);
+  dst[col + hd2] = f32_to_bf16(x2n * c2 + x1n * s2);
 }
 
 }  // namespace

@@ -363,6 +363,8 @@ __device__ __forceinline__ void finish_block(const ProblemArgs& p, const WeightA
   // was read when the block started, so no dependent load stalls the finisher.
   const int r = tid >> 3;
   const int c = tid & 7;
+  const int hd = e.head_dim;
+  const PairRuns pr = pair_runs(c, hd);  // (head_dim 64: two heads per block, see pair_runs)
   const int rr = blk * kDecRows + r;  // this thread's row of the launch
   const bool qk = e.qkv && d.proj != 2;
   f32x4_t sum[4];
@@ -432,12 +434,12 @@ __device__ __forceinline__ void finish_block(const ProblemArgs& p, const WeightA
   u32x4_t g_lo{}, g_hi{}, c_lo{}, c_hi{}, s_lo{}, s_hi{};
   if (qk && rr < M) {
     const uint16_t* gamma = d.gamma;
-    g_lo = load8_bf16(gamma + 8 * c);
-    g_hi = load8_bf16(gamma + kHalfDim + 8 * c);
-    c_lo = load8_bf16(e.cos + prow + 8 * c);
-    c_hi = load8_bf16(e.cos + prow + kHalfDim + 8 * c);
-    s_lo = load8_bf16(e.sin + prow + 8 * c);
-    s_hi = load8_bf16(e.sin + prow + kHalfDim + 8 * c);
+    g_lo = load8_bf16(gamma + pr.dim_lo);
+    g_hi = load8_bf16(gamma + pr.dim_hi);
+    c_lo = load8_bf16(e.cos + prow + pr.dim_lo);
+    c_hi = load8_bf16(e.cos + prow + pr.dim_hi);
+    s_lo = load8_bf16(e.sin + prow + pr.dim_lo);
+    s_hi = load8_bf16(e.sin + prow + pr.dim_hi);
   }
 
   // ---- head tile to LDS (fp32 [64][kPitch]); the x slice is no longer read ----------
@@ -454,10 +456,10 @@ __device__ __forceinline__ void finish_block(const ProblemArgs& p, const WeightA
   float lo[8], hi[8];
   {
     const float* src = tile + r * kPitch;
-    const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(src + 8 * c);
-    const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(src + 8 * c + 4);
-    const f32x4_t b0 = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + 8 * c);
-    const f32x4_t b1 = *reinterpret_cast<const f32x4_t*>(src + kHalfDim + 8 * c + 4);
+    const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(src + pr.col_lo);
+    const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(src + pr.col_lo + 4);
+    const f32x4_t b0 = *reinterpret_cast<const f32x4_t*>(src + pr.col_hi);
+    const f32x4_t b1 = *reinterpret_cast<const f32x4_t*>(src + pr.col_hi + 4);
     lo[0] = a0.x; lo[1] = a0.y; lo[2] = a0.z; lo[3] = a0.w;
     lo[4] = a1.x; lo[5] = a1.y; lo[6] = a1.z; lo[7] = a1.w;
     hi[0] = b0.x; hi[1] = b0.y; hi[2] = b0.z; hi[3] = b0.w;
@@ -472,8 +474,8 @@ __device__ __forceinline__ void finish_block(const ProblemArgs& p, const WeightA
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(hi[i], hi[i], __builtin_fmaf(lo[i], lo[i], ss));
-    ss = sum8_lanes(ss);
-    const float rms = rsqrtf(__builtin_fmaf(ss, 1.0f / float(kHeadDim), e.eps));
+    ss = head_sum(ss, hd);
+    const float rms = head_rms(ss, e.eps, hd);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float x1n = lo[i] * rms * bf16_lane(g_lo, i);
@@ -499,18 +501,18 @@ __device__ __forceinline__ void finish_block(const ProblemArgs& p, const WeightA
       uint16_t* base = d.out;
       if (base) {
         uint16_t* dst = base + (int64_t(rr) * H + d.hh) * kHeadDim;
-        *reinterpret_cast<u32x4_t*>(dst + 8 * c) = o1;
-        *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c) = o2;
+        *reinterpret_cast<u32x4_t*>(dst + pr.col_lo) = o1;
+        *reinterpret_cast<u32x4_t*>(dst + pr.col_hi) = o2;
       }
       if (cslot >= 0) {
         uint16_t* crow = paged_row(e, cslot, d.proj, d.hh);
-        *reinterpret_cast<u32x4_t*>(crow + 8 * c) = o1;
-        *reinterpret_cast<u32x4_t*>(crow + kHalfDim + 8 * c) = o2;
+        *reinterpret_cast<u32x4_t*>(crow + pr.col_lo) = o1;
+        *reinterpret_cast<u32x4_t*>(crow + pr.col_hi) = o2;
       }
     } else {  // plain GEMM output [M, N] (whole 128-column tiles: N % 128 == 0)
       uint16_t* dst = e.out + int64_t(rr) * e.N + int64_t(d.head) * kHeadDim;
-      *reinterpret_cast<u32x4_t*>(dst + 8 * c) = o1;
-      *reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c) = o2;
+      *reinterpret_cast<u32x4_t*>(dst + pr.col_lo) = o1;
+      *reinterpret_cast<u32x4_t*>(dst + pr.col_hi) = o2;
     }
   }
   if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -640,7 +642,7 @@ __device__ __forceinline__ uint32_t arrive(uint32_t* counter, const DecWork& d) 
 __device__ __forceinline__ void block_rows(const EpilogueArgs& e, const DecWork& d, int M, int b, int64_t& prow,
                                            int64_t& cslot) {
   const int rr = b * kDecRows + (threadIdx.x >> 3);
-  prow = (e.qkv && d.proj != 2 && rr < M) ? rope_row(e, rr) * kHeadDim : 0;
+  prow = (e.qkv && d.proj != 2 && rr < M) ? rope_row(e, rr) * e.head_dim : 0;
   cslot = (e.qkv && d.proj != 0 && rr < M) ? paged_slot(e, rr) : -1;
 }
 

@@ -224,35 +224,37 @@ __global__ void __launch_bounds__(kThreads) f32_qkv_kernel(F32Args a, int xcds) 
   const int r = tid >> 3, c = tid & 7;
   if (r >= ROWS) return;
   const int64_t t = row0 + r;
+  const int hd = a.head_dim;
+  const PairRuns pr = pair_runs(c, hd);  // (head_dim 64: two heads per block)
   float lo[8], hi[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    lo[i] = ep[r * kEpiPitch + 8 * c + i];
-    hi[i] = ep[r * kEpiPitch + kHalfDim + 8 * c + i];
+    lo[i] = ep[r * kEpiPitch + pr.col_lo + i];
+    hi[i] = ep[r * kEpiPitch + pr.col_hi + i];
   }
   if (proj < 2) {
-    // (every lane of the row's 8-lane group takes part in the sum; rows past M hold zeros)
-    const float ss = sum8_lanes(run_sumsq(lo, hi));
-    const float rms = head_rms(ss, a.eps);
+    // (every lane of the row's lane group takes part in the sum; rows past M hold zeros)
+    const float ss = head_sum(run_sumsq(lo, hi), hd);
+    const float rms = head_rms(ss, a.eps, hd);
     if (t < a.M) {
       const void* g = proj == 0 ? a.q_gamma : a.k_gamma;
-      const int64_t prow = rope_row(a, t) * kHeadDim;
+      const int64_t prow = rope_row(a, t) * hd;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
 #pragma clang fp contract(off)
-        const int d = 8 * c + i;
+        const int d = pr.dim_lo + i, d2 = pr.dim_hi + i;
         const float x1n = lo[i] * rms * elem<T>(g, d);
-        const float x2n = hi[i] * rms * elem<T>(g, d + kHalfDim);
+        const float x2n = hi[i] * rms * elem<T>(g, d2);
         lo[i] = __builtin_fmaf(x1n, elem<T>(a.cos, prow + d), -(x2n * elem<T>(a.sin, prow + d)));
-        hi[i] = __builtin_fmaf(x2n, elem<T>(a.cos, prow + d + kHalfDim), x1n * elem<T>(a.sin, prow + d + kHalfDim));
+        hi[i] = __builtin_fmaf(x2n, elem<T>(a.cos, prow + d2), x1n * elem<T>(a.sin, prow + d2));
       }
     }
   }
   if (t < a.M) {
     const int H = proj == 0 ? a.Hq : a.Hkv;
-    T* dst = static_cast<T*>(pick3(proj, a.q, a.k, a.v)) + (t * H + hh) * kHeadDim + 8 * c;
-    store8<T>(dst, lo, 0);
-    store8<T>(dst + kHalfDim, hi, 0);
+    T* dst = static_cast<T*>(pick3(proj, a.q, a.k, a.v)) + (t * H + hh) * kHeadDim;
+    store8<T>(dst + pr.col_lo, lo, 0);
+    store8<T>(dst + pr.col_hi, hi, 0);
   }
 }
 

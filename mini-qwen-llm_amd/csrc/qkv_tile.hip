@@ -73,7 +73,7 @@ __device__ __forceinline__ void store_block(const f32x16_t (&acc)[4], int64_t ro
   }
 
   const int H = proj == 0 ? e.Hq : e.Hkv;
-  uint16_t* __restrict__ dst = proj == 0 ? e.q : (proj == 1 ? e.k : e.v);
+  uint16_t* __restrict__ dst = pick3(proj, e.q, e.k, e.v);
 
   if (proj == 2) {  // V: plain projection (fused_qkv_rope.py:169, :194)
 #pragma unroll
@@ -95,49 +95,63 @@ __device__ __forceinline__ void store_block(const f32x16_t (&acc)[4], int64_t ro
   }
 
   // Q/K: RMSNorm over the head (fused_qkv_rope.py:98-100) then rotate-half RoPE
-  // (:102-118).  Lane holds d = c32, c32+32, c32+64, c32+96 -> the RoPE pairs
-  // (d, d+64) are nb (0,2) and (1,3), all in registers.
-  const uint16_t* __restrict__ gamma = proj == 0 ? e.q_gamma : e.k_gamma;
+  // (:102-118).  Lane holds columns c32 + 32 nb (nb = 0..3) of the block.  Head dim
+  // 128: one head, RoPE pairs (d, d+64) are nb (0,2) and (1,3).  Head dim 64: two
+  // heads, columns 0-63 (nb 0, 1) and 64-127 (nb 2, 3), pairs (d, d+32) are nb
+  // (0,1) and (2,3).  All in registers.
+  const uint16_t* __restrict__ gamma = pick3(proj, e.q_gamma, e.k_gamma, e.k_gamma);
+  const int hd = e.head_dim;
+  const bool two = hd == 64;
   float g[4];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) g[nb] = bf16_to_f32(gamma[nb * 32 + c32]);
-  const float inv_d = 1.0f / float(kHeadDim);
+  for (int nb = 0; nb < 4; ++nb) g[nb] = bf16_to_f32(gamma[(two ? (nb & 1) : nb) * 32 + c32]);
+  const float inv_d = two ? 1.0f / 64.0f : 1.0f / float(kHeadDim);
 
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    float ss = acc[0][i] * acc[0][i] + acc[1][i] * acc[1][i] + acc[2][i] * acc[2][i] +
-               acc[3][i] * acc[3][i];
-    // Sum over the 32 lanes that share this row (same lane>>5).
-    ss += __shfl_xor(ss, 16);
-    ss += __shfl_xor(ss, 8);
-    ss += __shfl_xor(ss, 4);
-    ss += __shfl_xor(ss, 2);
-    ss += __shfl_xor(ss, 1);
+    // sums of squares over the 32 lanes that share this row (same lane>>5)
+    float ss, ss2 = 0.f;
+    if (!two) {
+      ss = acc[0][i] * acc[0][i] + acc[1][i] * acc[1][i] + acc[2][i] * acc[2][i] + acc[3][i] * acc[3][i];
+    } else {
+      ss = acc[0][i] * acc[0][i] + acc[1][i] * acc[1][i];
+      ss2 = acc[2][i] * acc[2][i] + acc[3][i] * acc[3][i];
+    }
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) {
+      ss += __shfl_xor(ss, m);
+      if (two) ss2 += __shfl_xor(ss2, m);
+    }
     const float rms = rsqrtf(ss * inv_d + e.eps);
+    const float rms2 = two ? rsqrtf(ss2 * inv_d + e.eps) : rms;
     const int64_t t = row_base + 8 * (i >> 2) + 4 * half + (i & 3);
     if (t < p.M) {
-      const int64_t prow = rope_row(e, t) * kHeadDim;
+      const int64_t prow = rope_row(e, t) * hd;
       const int64_t cs = proj == 1 ? paged_slot(e, t) : -1;
       uint16_t* o = dst ? dst + (t * H + hh) * kHeadDim : nullptr;  // k may be null (cache only)
       uint16_t* oc = cs >= 0 ? paged_row(e, cs, proj, hh) : nullptr;
 #pragma unroll
       for (int pr = 0; pr < 2; ++pr) {
-        const int d = pr * 32 + c32;
-        const float x1n = acc[pr][i] * rms * g[pr];
-        const float x2n = acc[pr + 2][i] * rms * g[pr + 2];
+        // (lo, hi) accumulator blocks of the pair, its first dim, and its head's rms
+        const int lo = two ? 2 * pr : pr, hi = two ? 2 * pr + 1 : pr + 2;
+        const int d = two ? c32 : pr * 32 + c32;
+        const int hd2 = hd / 2;
+        const float r = pr == 1 ? rms2 : rms;
+        const float x1n = acc[lo][i] * r * g[lo];
+        const float x2n = acc[hi][i] * r * g[hi];
         const float c1 = bf16_to_f32(e.cos[prow + d]);
-        const float c2 = bf16_to_f32(e.cos[prow + d + kHalfDim]);
+        const float c2 = bf16_to_f32(e.cos[prow + d + hd2]);
         const float s1 = bf16_to_f32(e.sin[prow + d]);
-        const float s2 = bf16_to_f32(e.sin[prow + d + kHalfDim]);
+        const float s2 = bf16_to_f32(e.sin[prow + d + hd2]);
         const uint16_t b1 = f32_to_bf16(x1n * c1 - x2n * s1);
         const uint16_t b2 = f32_to_bf16(x2n * c2 + x1n * s2);
         if (o) {
-          o[d] = b1;
-          o[d + kHalfDim] = b2;
+          o[lo * 32 + c32] = b1;
+          o[hi * 32 + c32] = b2;
         }
         if (oc) {
-          oc[d] = b1;
-          oc[d + kHalfDim] = b2;
+          oc[lo * 32 + c32] = b1;
+          oc[hi * 32 + c32] = b2;
         }
       }
     }
@@ -353,10 +367,16 @@ tile_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
 
   // ---- epilogue -------------------------------------------------------------
   const int head = ht * HPT + wh;
+  if constexpr (KZ == 2) {
+    // (the block is selected by value: indexing acc by the wave's kz would put the
+    // accumulators in scratch memory)
+    f32x16_t blk[4];
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
-    if (KZ == 2 && mb != kz) continue;
-    store_block(acc[mb], m0 + wm * 64 + mb * 32, head, p, e, lane);
+    for (int nb = 0; nb < 4; ++nb) blk[nb] = kz == 0 ? acc[0][nb] : acc[1][nb];
+    store_block(blk, m0 + wm * 64 + kz * 32, head, p, e, lane);
+  } else {
+    store_block(acc[0], m0 + wm * 64, head, p, e, lane);
+    store_block(acc[1], m0 + wm * 64 + 32, head, p, e, lane);
   }
 }
 

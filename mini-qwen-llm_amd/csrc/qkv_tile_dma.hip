@@ -160,19 +160,21 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
   const int c32 = lane & 31;
   // ---- epilogue, one head at a time --------------------------------------------------
   const int c8 = tid & 7;
+  const int hd = e.head_dim;
+  const PairRuns pr = pair_runs(c8, hd);
   u32x4_t gq[2] = {}, gk[2] = {}, cs[kPreload ? kPasses : 1][2] = {}, sn[kPreload ? kPasses : 1][2] = {};
   auto load_rows = [&](int q, u32x4_t (&c2)[2], u32x4_t (&s2)[2]) {
-    const int64_t base = int64_t(prow[q]) * kHeadDim;
-    c2[0] = *reinterpret_cast<const u32x4_t*>(e.cos + base + 8 * c8);
-    c2[1] = *reinterpret_cast<const u32x4_t*>(e.cos + base + kHalfDim + 8 * c8);
-    s2[0] = *reinterpret_cast<const u32x4_t*>(e.sin + base + 8 * c8);
-    s2[1] = *reinterpret_cast<const u32x4_t*>(e.sin + base + kHalfDim + 8 * c8);
+    const int64_t base = int64_t(prow[q]) * hd;
+    c2[0] = *reinterpret_cast<const u32x4_t*>(e.cos + base + pr.dim_lo);
+    c2[1] = *reinterpret_cast<const u32x4_t*>(e.cos + base + pr.dim_hi);
+    s2[0] = *reinterpret_cast<const u32x4_t*>(e.sin + base + pr.dim_lo);
+    s2[1] = *reinterpret_cast<const u32x4_t*>(e.sin + base + pr.dim_hi);
   };
   if (e.qkv) {
-    gq[0] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + 8 * c8);
-    gq[1] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + kHalfDim + 8 * c8);
-    gk[0] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + 8 * c8);
-    gk[1] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + kHalfDim + 8 * c8);
+    gq[0] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + pr.dim_lo);
+    gq[1] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + pr.dim_hi);
+    gk[0] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + pr.dim_lo);
+    gk[1] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + pr.dim_hi);
     if constexpr (kPreload) {
 #pragma unroll
       for (int q = 0; q < kPasses; ++q) load_rows(q, cs[q], sn[q]);
@@ -223,15 +225,15 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
       float lo[8], hi[8];
 #pragma unroll
       for (int v = 0; v < 2; ++v) {
-        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(rowp + 8 * c8 + 4 * v);
-        const f32x4_t b = *reinterpret_cast<const f32x4_t*>(rowp + kHalfDim + 8 * c8 + 4 * v);
+        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(rowp + pr.col_lo + 4 * v);
+        const f32x4_t b = *reinterpret_cast<const f32x4_t*>(rowp + pr.col_hi + 4 * v);
         lo[4 * v] = a.x; lo[4 * v + 1] = a.y; lo[4 * v + 2] = a.z; lo[4 * v + 3] = a.w;
         hi[4 * v] = b.x; hi[4 * v + 1] = b.y; hi[4 * v + 2] = b.z; hi[4 * v + 3] = b.w;
       }
       if (e.qkv && proj != 2) {
         // RMSNorm over the head (fused_qkv_rope.py:98-100), then rotate-half RoPE (:102-118)
-        const float ss = sum8_lanes(run_sumsq(lo, hi));
-        const float rms = head_rms(ss, e.eps);
+        const float ss = head_sum(run_sumsq(lo, hi), hd);
+        const float rms = head_rms(ss, e.eps, hd);
         u32x4_t c2[2], s2[2];
         if constexpr (kPreload) {
           c2[0] = cs[q][0]; c2[1] = cs[q][1]; s2[0] = sn[q][0]; s2[1] = sn[q][1];
@@ -260,20 +262,19 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
           // kernel, so they need not stay in this XCD's L2; measured ~2 % faster)
           if (base) {
             uint16_t* dst = base + (t * H + hh) * kHeadDim;
-            __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(dst + 8 * c8));
-            __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8));
+            __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(dst + pr.col_lo));
+            __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(dst + pr.col_hi));
           }
           if (proj != 0 && cslot[q] >= 0) {
             uint16_t* crow = paged_row(e, cslot[q], proj, hh);
-            __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(crow + 8 * c8));
-            __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(crow + kHalfDim + 8 * c8));
+            __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(crow + pr.col_lo));
+            __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(crow + pr.col_hi));
           }
         } else {
           const int64_t col0 = int64_t(head) * kHeadDim;  // plain GEMM output [M, N]
           uint16_t* dst = e.out + t * e.N + col0;
-          if (col0 + 8 * c8 + 8 <= e.N) __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(dst + 8 * c8));
-          if (col0 + kHalfDim + 8 * c8 + 8 <= e.N)
-            __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8));
+          if (col0 + pr.col_lo + 8 <= e.N) __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(dst + pr.col_lo));
+          if (col0 + pr.col_hi + 8 <= e.N) __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(dst + pr.col_hi));
         }
       }
     }
@@ -295,6 +296,8 @@ __device__ __forceinline__ void finish_unit_rows(const float* tile, int pitch, i
     const int it = it0 + tid;
     if (kItems % THREADS != 0 && it >= kItems) break;  // (whole groups of 8 lanes leave together)
     const int j = it / 256, rr = (it >> 3) & 31, c8 = it & 7;
+    const int hd = e.head_dim;
+    const PairRuns pr = pair_runs(c8, hd);
     const int64_t t = t0 + rr;
     const int head = ht * NH + j;
     int proj, hh;
@@ -303,24 +306,24 @@ __device__ __forceinline__ void finish_unit_rows(const float* tile, int pitch, i
     float lo[8], hi[8];
 #pragma unroll
     for (int v = 0; v < 2; ++v) {
-      const f32x4_t a = *reinterpret_cast<const f32x4_t*>(rowp + 8 * c8 + 4 * v);
-      const f32x4_t b = *reinterpret_cast<const f32x4_t*>(rowp + kHalfDim + 8 * c8 + 4 * v);
+      const f32x4_t a = *reinterpret_cast<const f32x4_t*>(rowp + pr.col_lo + 4 * v);
+      const f32x4_t b = *reinterpret_cast<const f32x4_t*>(rowp + pr.col_hi + 4 * v);
       lo[4 * v] = a.x; lo[4 * v + 1] = a.y; lo[4 * v + 2] = a.z; lo[4 * v + 3] = a.w;
       hi[4 * v] = b.x; hi[4 * v + 1] = b.y; hi[4 * v + 2] = b.z; hi[4 * v + 3] = b.w;
     }
     const bool valid = t < p.M;
     if (e.qkv && proj != 2) {
-      const float ss = sum8_lanes(run_sumsq(lo, hi));
-      const float rms = head_rms(ss, e.eps);
-      const int64_t base = (valid ? rope_row(e, t) : 0) * kHeadDim;
+      const float ss = head_sum(run_sumsq(lo, hi), hd);
+      const float rms = head_rms(ss, e.eps, hd);
+      const int64_t base = (valid ? rope_row(e, t) : 0) * hd;
       u32x4_t c2[2], s2[2];
-      c2[0] = *reinterpret_cast<const u32x4_t*>(e.cos + base + 8 * c8);
-      c2[1] = *reinterpret_cast<const u32x4_t*>(e.cos + base + kHalfDim + 8 * c8);
-      s2[0] = *reinterpret_cast<const u32x4_t*>(e.sin + base + 8 * c8);
-      s2[1] = *reinterpret_cast<const u32x4_t*>(e.sin + base + kHalfDim + 8 * c8);
+      c2[0] = *reinterpret_cast<const u32x4_t*>(e.cos + base + pr.dim_lo);
+      c2[1] = *reinterpret_cast<const u32x4_t*>(e.cos + base + pr.dim_hi);
+      s2[0] = *reinterpret_cast<const u32x4_t*>(e.sin + base + pr.dim_lo);
+      s2[1] = *reinterpret_cast<const u32x4_t*>(e.sin + base + pr.dim_hi);
       const uint16_t* gam = proj == 0 ? e.q_gamma : e.k_gamma;
-      const u32x4_t g0 = *reinterpret_cast<const u32x4_t*>(gam + 8 * c8);
-      const u32x4_t g1 = *reinterpret_cast<const u32x4_t*>(gam + kHalfDim + 8 * c8);
+      const u32x4_t g0 = *reinterpret_cast<const u32x4_t*>(gam + pr.dim_lo);
+      const u32x4_t g1 = *reinterpret_cast<const u32x4_t*>(gam + pr.dim_hi);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int wd = i >> 1, sh = (i & 1) * 16;
@@ -339,21 +342,20 @@ __device__ __forceinline__ void finish_unit_rows(const float* tile, int pitch, i
       uint16_t* obase = proj == 0 ? e.q : (proj == 1 ? e.k : e.v);  // k / v may be null (cache only)
       if (obase) {
         uint16_t* dst = obase + (t * H + hh) * kHeadDim;
-        __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(dst + 8 * c8));
-        __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8));
+        __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(dst + pr.col_lo));
+        __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(dst + pr.col_hi));
       }
       const int64_t slot = proj != 0 ? paged_slot(e, t) : -1;
       if (slot >= 0) {
         uint16_t* crow = paged_row(e, slot, proj, hh);
-        __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(crow + 8 * c8));
-        __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(crow + kHalfDim + 8 * c8));
+        __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(crow + pr.col_lo));
+        __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(crow + pr.col_hi));
       }
     } else {
       const int64_t col0 = int64_t(head) * kHeadDim;  // plain GEMM output [M, N]
       uint16_t* dst = e.out + t * e.N + col0;
-      if (col0 + 8 * c8 + 8 <= e.N) __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(dst + 8 * c8));
-      if (col0 + kHalfDim + 8 * c8 + 8 <= e.N)
-        __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(dst + kHalfDim + 8 * c8));
+      if (col0 + pr.col_lo + 8 <= e.N) __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(dst + pr.col_lo));
+      if (col0 + pr.col_hi + 8 <= e.N) __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(dst + pr.col_hi));
     }
   }
 }
@@ -524,7 +526,7 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
 
 // The split-K launch of the pipelined kernel (a separate kernel, so that the
 // one-workgroup-per-tile kernel above keeps its own register allocation).
-template <int BM, int NH, int WM, int WN, int NS, int SBK>
+template <int BM, int NH, int WM, int WN, int NS, int SBK, bool INORM>
 __global__ void __launch_bounds__(WM* WN * 64)
 tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp) {
   using S = DmaShape<BM, NH, WM, WN, NS, SBK>;
@@ -565,23 +567,6 @@ tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp)
   }
   const int64_t m0 = int64_t(mt) * BM;
 
-  // Epilogue geometry: thread -> rows (tid / 8) + q * kRowStep and the column pairs
-  // [8c, 8c+8) / [64+8c, +8) of every head.  The RoPE table row of each of its
-  // rows (a positions[] load in positions mode) is read now, under the main loop.
-  constexpr int kRowStep = S::kThreads / 8;
-  constexpr int kPasses = BM / kRowStep;
-  // (vector types: indexed in registers even where the compiler merges the
-  // per-row code paths, where a plain array would go to scratch memory)
-  typedef int32_t RowV __attribute__((ext_vector_type(kPasses)));
-  typedef int64_t SlotV __attribute__((ext_vector_type(kPasses)));
-  RowV prow;
-  SlotV cslot;  // paged-KV-cache slot of the row (-1: none)
-#pragma unroll
-  for (int q = 0; q < kPasses; ++q) {
-    const int64_t t = m0 + (tid >> 3) + q * kRowStep;
-    prow[q] = (e.qkv && t < p.M) ? int32_t(rope_row(e, t)) : 0;
-    cslot[q] = (e.qkv && t < p.M) ? paged_slot(e, t) : -1;
-  }
   const int64_t K = p.K;
 
   // ---- this lane's sources: load instruction i of a stage fills staged rows
@@ -609,7 +594,7 @@ tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp)
   }
   // input RMSNorm: scale of the x row and k offset of the chunk each of this
   // lane's x loads brings in (load i < kALoads, row0 + lane / chunks, slot lane % chunks)
-  const bool in_norm = p.in_gamma != nullptr;
+  constexpr bool in_norm = INORM;  // (p.in_gamma != nullptr: a template switch keeps its registers out of the plain kernel)
   float a_scale[S::kALoads];
   int a_koff[S::kALoads];
 #pragma unroll
@@ -830,7 +815,7 @@ tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp)
     constexpr int kItems = kUC * kUThreads;      // f32x4 chunks of a unit
     static_assert(kItems % S::kThreads == 0, "unit chunks per thread");
     constexpr int kPer = kItems / S::kThreads;
-    constexpr int kBatch = 2;                    // splits whose loads are in flight together (4 spill)
+    constexpr int kBatch = 1;                    // splits whose loads are in flight together (2 spill)
     constexpr int kTPitch = BN + 4;              // fp32 pitch of the unit tile
     f32x4_t* own_buf = reinterpret_cast<f32x4_t*>(smem);                  // [kUC][kUThreads]
     float* utile = reinterpret_cast<float*>(smem + size_t(kItems) * 16);  // [32][kTPitch]
@@ -948,8 +933,16 @@ hipError_t launch_dma_split(const ProblemArgs& p, const WeightArgs& w, const Epi
   sp.max_spins = max_spins;
   sp.counters = static_cast<uint32_t*>(workspace);
   sp.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kDecodeCounterBytes);
-  hipLaunchKernelGGL((tile_dma_split_kernel<BM, NH, WM, WN, NS, SBK>), dim3(X * ksplit * tpx), dim3(S::kThreads),
-                     dyn, stream, p, w, e, sp);
+  if (p.in_gamma) {
+    // (no input-norm form of the 256-row tiles: its registers would spill)
+    if constexpr (BM > 128) return hipErrorInvalidValue;
+    else
+      hipLaunchKernelGGL((tile_dma_split_kernel<BM, NH, WM, WN, NS, SBK, true>), dim3(X * ksplit * tpx),
+                         dim3(S::kThreads), dyn, stream, p, w, e, sp);
+  } else {
+    hipLaunchKernelGGL((tile_dma_split_kernel<BM, NH, WM, WN, NS, SBK, false>), dim3(X * ksplit * tpx),
+                       dim3(S::kThreads), dyn, stream, p, w, e, sp);
+  }
   return hipGetLastError();
 }
 

@@ -306,5 +306,11 @@ def retired_workspaces() -> int:
     return len(_retired)
 
 
+def blocks(heads: int, head_dim: int) -> int:
+    """Heads -> the kernels' 128-column blocks (two heads per block at head_dim 64):
+    the head counts the workspace-size queries take."""
+    return heads * head_dim // 128
+
+
 def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()

@@ -39,9 +39,9 @@ class Case:
     """Seeded inputs of one fused_qkv_rope call (host copies; .to(dev) moves them)."""
 
     def __init__(self, B, S, hidden, Hq, Hkv, seed, *, rows=None, theta=1e6, gamma_ones=False,
-                 positions=None, w_std=0.02, x_std=1.0):
+                 positions=None, w_std=0.02, x_std=1.0, head_dim=HEAD_DIM):
         g = torch.Generator().manual_seed(seed)
-        D = HEAD_DIM
+        D = self.D = head_dim
         self.B, self.S, self.hidden, self.Hq, self.Hkv = B, S, hidden, Hq, Hkv
         self.x = (torch.randn(B, S, hidden, generator=g) * x_std).bfloat16()
         self.w_q = (torch.randn(Hq * D, hidden, generator=g) * w_std).bfloat16()

@@ -76,7 +76,8 @@ def test_rope_tables_layout():
 
 # ── QK-Norm (fused_qkv_rope.py:98-100) ───────────────────────────────────────
 
-def test_norm_constant_vector():
+@pytest.mark.parametrize("D", [128, 64])  # head_dim: Qwen3 checkpoints / the reference's default config
+def test_norm_constant_vector(D):
     """x = c * ones  ->  sign(c) * gamma / sqrt(1 + eps / c^2)."""
     g = np.random.default_rng(1).uniform(0.5, 1.5, D)
     for c in (3.0, -0.25, 1e-2):
@@ -85,7 +86,8 @@ def test_norm_constant_vector():
         np.testing.assert_allclose(out[0, 0], exp, rtol=1e-12)
 
 
-def test_norm_one_hot_and_zero():
+@pytest.mark.parametrize("D", [128, 64])  # head_dim: Qwen3 checkpoints / the reference's default config
+def test_norm_one_hot_and_zero(D):
     g = np.linspace(0.5, 1.5, D)
     x = np.zeros((1, 1, D))
     x[0, 0, 17] = 5.0
@@ -96,7 +98,8 @@ def test_norm_one_hot_and_zero():
     assert np.all(orc.qk_norm(np.zeros((2, 3, D)), g) == 0.0)
 
 
-def test_norm_scale_invariant_and_gamma_per_dim():
+@pytest.mark.parametrize("D", [128, 64])  # head_dim: Qwen3 checkpoints / the reference's default config
+def test_norm_scale_invariant_and_gamma_per_dim(D):
     rng = np.random.default_rng(2)
     x = rng.standard_normal((4, 3, D))
     g = rng.uniform(0.5, 1.5, D)
@@ -108,17 +111,18 @@ def test_norm_scale_invariant_and_gamma_per_dim():
 
 # ── RoPE (fused_qkv_rope.py:102-118) ─────────────────────────────────────────
 
-def _tables64(n, theta=1e6):
+def _tables64(n, theta=1e6, D=D):
     return orc.rope_tables(D, n, theta, np.float64)
 
 
-def test_rope_matches_complex_rotation():
+@pytest.mark.parametrize("D", [128, 64])  # head_dim: Qwen3 checkpoints / the reference's default config
+def test_rope_matches_complex_rotation(D):
     """Independent formulation: (x1 + i x2) * e^{i angle} = out1 + i out2, which
     fixes the sign convention and the half pairing of rotate_half."""
     rng = np.random.default_rng(3)
     T, H = 37, 3
     x = rng.standard_normal((T, H, D))
-    cos, sin = _tables64(4096)
+    cos, sin = _tables64(4096, D=D)
     rows = rng.integers(0, 4096, T)
     out = orc.rope(x, cos[rows], sin[rows])
     z = (x[..., : D // 2] + 1j * x[..., D // 2:]) * np.exp(1j * np.arctan2(sin[rows, : D // 2], cos[rows, : D // 2]))[:, None, :]
@@ -126,10 +130,11 @@ def test_rope_matches_complex_rotation():
     np.testing.assert_allclose(out[..., D // 2:], z.imag, atol=1e-12)
 
 
-def test_rope_identity_norm_and_inverse():
+@pytest.mark.parametrize("D", [128, 64])  # head_dim: Qwen3 checkpoints / the reference's default config
+def test_rope_identity_norm_and_inverse(D):
     rng = np.random.default_rng(4)
     x = rng.standard_normal((16, 2, D))
-    cos, sin = _tables64(512)
+    cos, sin = _tables64(512, D=D)
     np.testing.assert_array_equal(orc.rope(x, cos[[0] * 16], sin[[0] * 16]), x)
     rows = rng.integers(0, 512, 16)
     y = orc.rope(x, cos[rows], sin[rows])
@@ -139,7 +144,8 @@ def test_rope_identity_norm_and_inverse():
     np.testing.assert_allclose(back, x, atol=1e-12)
 
 
-def test_rope_uses_both_table_halves():
+@pytest.mark.parametrize("D", [128, 64])  # head_dim: Qwen3 checkpoints / the reference's default config
+def test_rope_uses_both_table_halves(D):
     """The kernel reads cos/sin halves separately (:112-115): tables whose halves
     differ must give different results for the two output halves."""
     x = np.ones((1, 1, D))
@@ -165,19 +171,21 @@ def test_projection_brute_force():
     np.testing.assert_allclose(orc.projection(x, w), ref, rtol=1e-12)
 
 
-def test_fused_shapes_and_v_passthrough():
+@pytest.mark.parametrize("D", [128, 64])  # head_dim: Qwen3 checkpoints / the reference's default config
+def test_fused_shapes_and_v_passthrough(D):
     rng = np.random.default_rng(6)
     B, S, H, Hq, Hkv = 2, 5, 256, 4, 2
     x = rng.standard_normal((B, S, H))
     wq, wk, wv = (rng.standard_normal((h * D, H)) * 0.05 for h in (Hq, Hkv, Hkv))
     g = np.ones(D)
-    cos, sin = _tables64(S)
+    cos, sin = _tables64(S, D=D)
     q, k, v = orc.fused_qkv_rope(x, wq, wk, wv, g, g, cos, sin)
     assert q.shape == (B, S, Hq, D) and k.shape == (B, S, Hkv, D) and v.shape == (B, S, Hkv, D)
     np.testing.assert_allclose(v.reshape(B * S, -1), x.reshape(B * S, H) @ wv.T, rtol=1e-12)
 
 
-def test_fused_equals_unfused_composition():
+@pytest.mark.parametrize("D", [128, 64])  # head_dim: Qwen3 checkpoints / the reference's default config
+def test_fused_equals_unfused_composition(D):
     """The fused oracle agrees with the reference's unfused composition
     (test_fused_qkv_rope.py:244-259) evaluated in float64."""
     rng = np.random.default_rng(7)
@@ -185,7 +193,7 @@ def test_fused_equals_unfused_composition():
     x = rng.standard_normal((B, S, H))
     wq, wk, wv = (rng.standard_normal((h * D, H)) * 0.05 for h in (Hq, Hkv, Hkv))
     gq, gk = rng.uniform(0.8, 1.2, D), rng.uniform(0.8, 1.2, D)
-    cos, sin = _tables64(S)
+    cos, sin = _tables64(S, D=D)
     a = orc.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin)
     b = orc.unfused_composition(x, wq, wk, wv, gq, gk, cos, sin, dtype=np.float64)
     for u, w_ in zip(a, b):
@@ -202,7 +210,7 @@ def test_torch_cpu_baseline_equals_fused_oracle():
     x = rng.standard_normal((B, S, H))
     wq, wk, wv = (rng.standard_normal((h * D, H)) * 0.05 for h in (Hq, Hkv, Hkv))
     gq, gk = rng.uniform(0.8, 1.2, D), rng.uniform(0.8, 1.2, D)
-    cos, sin = _tables64(S)
+    cos, sin = _tables64(S, D=D)
     a = orc.fused_qkv_rope(x, wq, wk, wv, gq, gk, cos, sin)
     t = lambda v: torch.from_numpy(np.ascontiguousarray(v))
     b = unfused_composition_torch(t(x), t(wq), t(wk), t(wv), t(gq), t(gk), t(cos), t(sin))
