@@ -50,6 +50,7 @@ std::atomic<int64_t> g_decode_cost_model{1};  // 0: decode blocks whenever eligi
 std::atomic<int64_t> g_decode_passes{16};  // most 64-row blocks one decode launch covers (1..16)
 std::atomic<int64_t> g_head_tiles{1};  // one round of single-head tiles where the planner models them fastest
 std::atomic<int64_t> g_tile_ksplit{1};  // split-K tile launches: 0 off, 1 by cost model, >= 2 that split count
+std::atomic<int64_t> g_gemv_max_m{kGemvMaxM};  // W4A16 GEMMs with M up to this run the column-parallel kernel
 
 constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace (per head)
 
@@ -768,6 +769,24 @@ static int validate_int4(const int32_t* qw, const void* sc, const int32_t* qz, i
   return MQK_OK;
 }
 
+}  // extern "C"
+
+// The column-parallel kernel for small M (any N % 8 == 0, any operand alignment
+// but x's): no workspace.
+static int w4a16_gemv(const mqk_bf16* x, const int32_t* qweight, const void* scales, const int32_t* qzeros,
+                      int64_t M, int64_t K, int64_t N, int group, int scale_type, mqk_bf16* out, void* stream) {
+  WeightArgs w{};
+  w.qw[0] = qweight;
+  w.sc[0] = scales;
+  w.qz[0] = qzeros;
+  w.n_cols[0] = N;
+  w.group = group;
+  w.scale_fp16 = scale_type == MQK_SCALE_FP16;
+  return hip_status(launch_w4_gemv(x, w, M, K, out, static_cast<hipStream_t>(stream)), "w4a16 GEMV launch");
+}
+
+extern "C" {
+
 int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales,
                    const int32_t* qzeros, int64_t M, int64_t K, int64_t N, int group,
                    int scale_type, mqk_bf16* out, void* stream) {
@@ -778,6 +797,7 @@ int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales
   if (M == 0) return ok();
   if (!x || !out) return fail(MQK_ERR_NULL_POINTER, "x/out must be non-NULL");
   if (!aligned16(x)) return fail(MQK_ERR_MISALIGNED, "x must be 16-byte aligned");
+  if (M <= g_gemv_max_m.load()) return w4a16_gemv(x, qweight, scales, qzeros, M, K, N, group, scale_type, out, stream);
   const int tiles = int((N + kHeadDim - 1) / kHeadDim);
   ProblemArgs p{x, M, K, tiles};
   const Topology topo = device_topology();
@@ -807,6 +827,7 @@ int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales
 }
 
 size_t mqk_w4a16_gemm_workspace_size(int64_t M, int64_t K, int64_t N) {
+  if (M <= g_gemv_max_m.load()) return 0;  // the column-parallel kernel needs none
   if (M <= 0 || K <= 0 || K % kBK != 0 || N <= 0 || N % kHeadDim != 0 || N / kHeadDim > kMaxTiles) return 0;
   const int tiles = int(N / kHeadDim);
   const Plan pl = plan_fused(1, M, K, tiles, true, device_topology());
@@ -823,6 +844,7 @@ int mqk_w4a16_gemm_ex(const mqk_bf16* x, const int32_t* qweight, const void* sca
   if (M == 0) return ok();
   if (!x || !out) return fail(MQK_ERR_NULL_POINTER, "x/out must be non-NULL");
   if (!aligned16(x)) return fail(MQK_ERR_MISALIGNED, "x must be 16-byte aligned");
+  if (M <= g_gemv_max_m.load()) return w4a16_gemv(x, qweight, scales, qzeros, M, K, N, group, scale_type, out, stream);
   // the planned kernels (split-K decode kernel for small M) need whole 128-column
   // tiles and 16-byte aligned operands; anything else takes the tile kernels
   if (N % kHeadDim != 0 || N / kHeadDim > kMaxTiles || !aligned16(qweight) || !aligned16(scales) ||
@@ -978,6 +1000,9 @@ int mqk_set_option(const char* name, int64_t value) {
   } else if (!strcmp(name, "group_m")) {
     if (value < 1 || value > 1024) return fail(MQK_ERR_BAD_OPTION, "group_m must be in [1, 1024]");
     g_group_m = value;
+  } else if (!strcmp(name, "gemv_max_m")) {
+    if (value < 0 || value > kGemvMaxM) return fail(MQK_ERR_BAD_OPTION, "gemv_max_m must be in [0, %d]", kGemvMaxM);
+    g_gemv_max_m = value;
   } else {
     return fail(MQK_ERR_BAD_OPTION, "unknown option '%s'", name);
   }
@@ -996,6 +1021,7 @@ int64_t mqk_get_option(const char* name) {
   if (!strcmp(name, "decode_cost_model")) return g_decode_cost_model.load();
   if (!strcmp(name, "tile_ksplit")) return g_tile_ksplit.load();
   if (!strcmp(name, "head_tiles")) return g_head_tiles.load();
+  if (!strcmp(name, "gemv_max_m")) return g_gemv_max_m.load();
   if (!strcmp(name, "decode_force_recompute")) return g_decode_force_recompute;
   if (!strcmp(name, "decode_max_spins")) return g_decode_max_spins;
   if (!strcmp(name, "device_cus")) return device_topology().cus;    // read-only: the current device's

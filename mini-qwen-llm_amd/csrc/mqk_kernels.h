@@ -165,6 +165,13 @@ extern int g_decode_force_recompute;
 // set it low to exercise the hand-off.
 extern int g_decode_max_spins;
 
+// W4A16 GEMM for small M (1 <= M <= kGemvMaxM): out[M, N] = x[M, K] @ dequant(W)
+// with w.qw[0] / sc[0] / qz[0] / n_cols[0] = N / group / scale_fp16; fp32
+// dequantisation and accumulation, one bf16 rounding; no workspace (w4_gemv.hip).
+constexpr int kGemvMaxM = 16;
+hipError_t launch_w4_gemv(const uint16_t* x, const WeightArgs& w, int64_t M, int64_t K, uint16_t* out,
+                          hipStream_t stream);
+
 // Standalone QK-norm + RoPE.
 hipError_t launch_norm_rope(const uint16_t* q_raw, const uint16_t* k_raw, const EpilogueArgs& e,
                             int64_t T, hipStream_t stream);

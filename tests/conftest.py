@@ -103,7 +103,7 @@ def no_head_tiles():
 _KERNEL_NAMES = (("decode_multi_kernel", "decode_multi"), ("decode_long_kernel", "decode"), ("decode_kernel", "decode"),
                  ("tile_dma_w4_kernel", "tile_w4"), ("tile_dma_split_kernel", "tile_split"), ("tile_dma_kernel", "tile"), ("tile_kernel", "tile_reg"),
                  ("row_scale_kernel", "row_scale"), ("norm_rope_kernel", "norm_rope"),
-                 ("f32_qkv_kernel", "f32"))
+                 ("f32_qkv_kernel", "f32"), ("w4_gemv", "gemv"))
 
 
 def _short_kernel_name(name: str):
@@ -121,7 +121,7 @@ def launched_kernels(fn, *, warm=True):
     """The library kernels one call of ``fn`` launches, in launch order, as
     short names ("decode" = one 64-row block, "decode_multi" = several blocks,
     "tile", "tile_head" = single-head tiles, "tile_split" = split-K tile, "tile_w4", "tile_w4_head", "tile_reg", "row_scale", "norm_rope",
-    "f32" = the fp32 front), recorded with torch.profiler (the reference counts its
+    "f32" = the fp32 front, "gemv" = the small-M W4A16 GEMM), recorded with torch.profiler (the reference counts its
     kernels the same way, tests/test_fused_qkv_rope.py:287-311).  Other
     kernels (torch's own fills and copies) are left out."""
     from torch.profiler import ProfilerActivity, profile
