@@ -2,7 +2,7 @@
 """Benchmark of the fused QKV + QK-Norm + RoPE op on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
-    python bench.py --only {c1f32,c2f32,d14b,c2,c3,c4,c5,mid,mid256,mid128,gemm,copy} --steps K   # one workload, for profiler runs
+    python bench.py --only {c1f32,c2f32,d14b,c2,c3,c4,c5,mid,mid256,mid128,gemm,copy,stream} --steps K   # one workload, for profiler runs
 
 Headline (``value``): BASELINE config 2, Qwen3-8B prefill B=4 x S=512 (2048
 tokens, hidden 4096, 32 Q heads, 8 KV heads, head_dim 128, bf16), tokens/s of
@@ -290,7 +290,28 @@ def copy_kernel(nbytes, steps, dev):
     torch.cuda.synchronize()
 
 
-WORKLOADS = ("c1f32", "c2f32", "d14b", "c2", "c3", "c4", "c5", "mid", "mid256", "mid128", "gemm", "copy")
+def stream_read(steps, warmup, dev, copies=8, nbytes=6144 * 4096 * 2, blocks=None):
+    """The HBM read ceiling of a decode step's weight stream: mqk_read_probe (a
+    plain read with 16-byte non-temporal loads over every CU, nothing else) over
+    one of `copies` buffers of C3's weight size (50.3 MB each, 400 MB in all, past
+    the 256 MB MALL).  Returns (ms per read, GB/s)."""
+    import torch
+    import mqk
+    from mqk import _native
+    lib = mqk.library()
+    nb = blocks or mqk.get_option("device_cus")
+    bufs = [torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).normal_() for _ in range(copies)]
+    out = torch.empty(nb, dtype=torch.int32, device=dev)
+    stream = _native.stream_handle(dev)
+
+    def read(i):
+        _native.check(lib.mqk_read_probe(bufs[i % copies].data_ptr(), nbytes, nb, out.data_ptr(), stream),
+                      "mqk_read_probe")
+    ms, _ = time_steps(read, steps, warmup)
+    return ms, nbytes / (ms * 1e-3) / 1e9
+
+
+WORKLOADS = ("c1f32", "c2f32", "d14b", "c2", "c3", "c4", "c5", "mid", "mid256", "mid128", "gemm", "copy", "stream")
 
 
 def run_only(name, steps, warmup, dev):
@@ -316,6 +337,8 @@ def run_only(name, steps, warmup, dev):
         ms, _ = bench_decode(256, hidden, Hq, Hkv, 2, steps, warmup, dev)
     elif name == "mid128":  # a 128-token call: one decode launch covering two 64-row blocks
         ms, _ = bench_decode(128, hidden, Hq, Hkv, 2, steps, warmup, dev)
+    elif name == "stream":  # the HBM read ceiling of the decode weight stream (a plain 50 MB read)
+        ms = {f"{b}_workgroups": stream_read(steps, warmup, dev, blocks=b)[0] for b in (256, 512, 1024)}
     elif name == "gemm":  # the W4A16 GEMM decode shapes, M = 1 / 4 / 8 / 16
         ms = {m: v[0] * 1e-3 for m, v in bench_w4a16_gemm_decode(steps, warmup, dev).items()}
     else:

@@ -368,6 +368,15 @@ int64_t mqk_get_option(const char* name);
 /* Human-readable list of tile variants, "id:BMxBN/waves;...". */
 const char* mqk_tile_variants(void);
 
+/*
+ * Measurement probe, no counterpart in the reference: reads `bytes` bytes at the
+ * device pointer src (16-byte aligned, bytes % 16 == 0) once, with 16-byte
+ * non-temporal loads over `blocks` workgroups of 512 threads, and writes one
+ * 32-bit word per workgroup to out[blocks].  bench.py times it as the HBM read
+ * ceiling of the decode step's weight stream.  Launches on `stream`.
+ */
+int mqk_read_probe(const void* src, size_t bytes, int blocks, uint32_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,7 +27,7 @@ PKG = CSRC.parent / "mqk"
 OUT = PKG / "libmqk.so"
 BUILD_DIR = CSRC.parent / "_build"
 SOURCES = ["qkv_tile.hip", "qkv_tile_dma.hip", "qkv_decode.hip", "norm_rope.hip", "input_norm.hip", "qkv_f32.hip",
-           "w4_gemv.hip", "mqk_api.hip"]
+           "w4_gemv.hip", "read_probe.hip", "mqk_api.hip"]
 # No kernel may use scratch memory (register spills, or an array the compiler
 # could not keep in registers): the compiler's resource-usage remarks of every
 # source are checked and the build fails otherwise.

@@ -1029,6 +1029,10 @@ int64_t mqk_get_option(const char* name) {
   return -1;
 }
 
+int mqk_read_probe(const void* src, size_t bytes, int blocks, uint32_t* out, void* stream) {
+  return hip_status(launch_read_probe(src, bytes, blocks, out, static_cast<hipStream_t>(stream)), "read probe launch");
+}
+
 const char* mqk_tile_variants(void) {
   static const char* const text = [] {
     static char buf[512];

@@ -172,6 +172,10 @@ constexpr int kGemvMaxM = 16;
 hipError_t launch_w4_gemv(const uint16_t* x, const WeightArgs& w, int64_t M, int64_t K, uint16_t* out,
                           hipStream_t stream);
 
+// HBM read-rate probe (bench.py): reads `bytes` (16-byte aligned) once over
+// `blocks` workgroups of 512 threads and writes one word per workgroup to out.
+hipError_t launch_read_probe(const void* src, size_t bytes, int blocks, uint32_t* out, hipStream_t stream);
+
 // Standalone QK-norm + RoPE.
 hipError_t launch_norm_rope(const uint16_t* q_raw, const uint16_t* k_raw, const EpilogueArgs& e,
                             int64_t T, hipStream_t stream);

@@ -142,6 +142,7 @@ SIGNATURES = {
     "mqk_set_option": (_I, [ctypes.c_char_p, _I64]),
     "mqk_get_option": (_I64, [ctypes.c_char_p]),
     "mqk_tile_variants": (ctypes.c_char_p, []),
+    "mqk_read_probe": (_I, [_P, _SZ, _I, _P, _P]),
 }
 
 
