@@ -816,10 +816,11 @@ int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales
   e.Hkv = 0;
   e.out = out;
   e.N = N;
-  // Whole 128-column tiles can use any int4 variant; a partial last tile needs the
-  // register-staged kernel (variant 1), which bounds-checks columns.
+  // The pipelined int4 variants read qweight and scales with 16-byte loads (a last
+  // tile past N re-reads whole in-range chunks, N % 8 == 0) and qzeros with 4-byte
+  // loads; operands without that alignment take the register-staged kernel.
   const TileVariant* v = nullptr;
-  if (N % kHeadDim == 0 && aligned16(qweight) && aligned16(scales) && aligned16(qzeros))
+  if (aligned16(qweight) && aligned16(scales) && (reinterpret_cast<uintptr_t>(qzeros) & 3u) == 0)
     v = choose_tile_variant(int(g_prefill_tile.load()), M, tiles, 1, topo.cus);
   if (!v) v = choose_tile_variant(1, M, tiles, 1, topo.cus);
   return hip_status(launch_tile(*v, 1, p, w, e, int(g_group_m.load()), static_cast<hipStream_t>(stream)),

@@ -218,6 +218,20 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
       : "memory");
 }
 
+// L2 -> LDS, 4 bytes per lane: this lane's word at gptr goes to LDS byte
+// lds_base + 4 * lane (lds_base wave-uniform).
+__device__ __forceinline__ void dma4(const void* gptr, uint32_t lds_base) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dword %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(gptr)
+      : "memory");
+}
+
 // dma16 of the 16 bytes at gptr + OFF bytes (OFF an immediate of the instruction,
 // 0 <= OFF < 4096), so a run of loads at fixed distances shares one address.  The
 // instruction offset moves the LDS destination as well (M0 + offset + 16 * lane),

@@ -971,13 +971,13 @@ struct W4Shape {
   static constexpr int kStageBytes = (kABytes + kBBytes + kSBytes + kZBytes + 1023) / 1024 * 1024;
   static constexpr int kNA = BM / 8;                  // 1 KB loads: 8 x rows each
   static constexpr int kNW = kBN / 32;                // 1 KB loads: two 512-byte (k-group, head) runs
-  static constexpr int kLoads = kNA + kNW + 2;        // + one for the scales, one for the zeros
+  static constexpr int kLoads = kNA + kNW + 2;        // + one for the scales, one for the zeros (4-byte loads)
   static constexpr int kMaxPerWave = (kLoads + kWaves - 1) / kWaves;
   static constexpr int kRingBytes = NS * kStageBytes;
   static constexpr int kEpiBytes = BM * kEpiPitch * 4;
   static constexpr int kLdsBytes = kRingBytes > kEpiBytes ? kRingBytes : kEpiBytes;
   static_assert(kTM % 32 == 0 && kTN % 32 == 0, "wave tile");
-  static_assert(kBN / 8 <= 64 && kBN / 32 <= 64, "scale / zero load fits one instruction");
+  static_assert(kBN / 8 <= 64, "the scale and the zero loads fit one instruction each");
   static_assert(NS >= 2 && NS <= 8 && kMaxPerWave * (NS - 2) <= 63, "stages");
   static_assert(kLdsBytes <= 160 * 1024, "LDS");
 };
@@ -1057,7 +1057,11 @@ tile_dma_w4_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
       int proj, hh;
       split_head(ht * NH + j, e.Hq, e.Hkv, proj, hh);
       const int64_t n = w.n_cols[proj];
-      base[i] = reinterpret_cast<const char*>(w.qw[proj] + kg * n + int64_t(hh) * kHeadDim + (lane & 31) * 4);
+      // (a plain GEMM's last tile may pass N: its columns past N, whole 16-byte
+      // chunks as N % 8 == 0, re-read the last chunk and are never stored)
+      int64_t c4 = int64_t(hh) * kHeadDim + (lane & 31) * 4;
+      c4 = c4 + 4 <= n ? c4 : n - 4;
+      base[i] = reinterpret_cast<const char*>(w.qw[proj] + kg * n + c4);
       stride[i] = 8 * n * 4;
       dst[i] = uint32_t(S::kABytes + (g - S::kNA) * 1024);
       kind[i] = 1;
@@ -1068,20 +1072,25 @@ tile_dma_w4_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
         int proj, hh;
         split_head(ht * NH + j, e.Hq, e.Hkv, proj, hh);
         const int64_t n = w.n_cols[proj];
-        base[i] = reinterpret_cast<const char*>(static_cast<const uint16_t*>(w.sc[proj]) + int64_t(hh) * kHeadDim +
-                                                (lane % 16) * 8);
+        int64_t c8 = int64_t(hh) * kHeadDim + (lane % 16) * 8;
+        c8 = c8 + 8 <= n ? c8 : n - 8;
+        base[i] = reinterpret_cast<const char*>(static_cast<const uint16_t*>(w.sc[proj]) + c8);
         stride[i] = n * 2;
         active[i] = true;
       }
       dst[i] = uint32_t(S::kABytes + S::kBBytes);
       kind[i] = 2;
     } else if (g == S::kNA + S::kNW + 1) {
-      const int j = lane / 4;  // 4 lanes x 32 zeros per head
+      // zeros: one packed word (8 columns) per lane, 16 lanes per head (4-byte
+      // loads, so a last tile past N never shifts a valid column's word)
+      const int j = lane / 16;
       if (j < NH) {
         int proj, hh;
         split_head(ht * NH + j, e.Hq, e.Hkv, proj, hh);
         const int64_t n = w.n_cols[proj];
-        base[i] = reinterpret_cast<const char*>(w.qz[proj] + int64_t(hh) * (kHeadDim / 8) + (lane % 4) * 4);
+        int64_t wd = int64_t(hh) * (kHeadDim / 8) + (lane % 16);
+        wd = wd < n / 8 ? wd : n / 8 - 1;
+        base[i] = reinterpret_cast<const char*>(w.qz[proj] + wd);
         stride[i] = (n / 8) * 4;
         active[i] = true;
       }
@@ -1114,7 +1123,10 @@ tile_dma_w4_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
     for (int i = 0; i < S::kMaxPerWave; ++i) {
       if (i < nslots) {
         const int64_t stp = kind[i] >= 2 ? gstep : int64_t(kt);
-        if (active[i]) dma16(base[i] + stp * stride[i], sbase + dst[i]);
+        if (active[i]) {
+          if (kind[i] == 3) dma4(base[i] + stp * stride[i], sbase + dst[i]);
+          else dma16(base[i] + stp * stride[i], sbase + dst[i]);
+        }
       }
     }
   };

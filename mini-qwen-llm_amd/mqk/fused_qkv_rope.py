@@ -58,6 +58,11 @@ def _require(t: torch.Tensor, name: str, device: torch.device, dtype=torch.bfloa
         raise ValueError(f"{name} is on {t.device}, expected {device}")
     if dtype is not None and t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.data_ptr() & 15:
+        # a view at an odd offset: the pipelined and decode kernels read every operand
+        # with 16-byte loads, so take a (16-byte aligned) copy rather than the slower
+        # kernels the C ABI keeps for unaligned pointers
+        return t.clone(memory_format=torch.contiguous_format)
     return t if t.is_contiguous() else t.contiguous()
 
 

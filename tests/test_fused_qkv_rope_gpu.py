@@ -442,3 +442,29 @@ def test_shim_accepts_strided_and_int64_inputs(device):
     torch.cuda.synchronize()
     for a, b in zip(out, ref):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("B,S", [(16, 1), (1, 300)])
+def test_unaligned_views_take_the_fast_path(B, S, device):
+    """x and w_k passed as views at an odd element offset: the shim copies them to
+    aligned storage, so the call runs the same kernels (the decode kernel, a tile
+    plan) as with aligned operands and returns the same bits."""
+    import mqk
+    from conftest import launched_kernels
+    pos = torch.randint(0, 4096, (B * S,), generator=torch.Generator().manual_seed(B), dtype=torch.int32)
+    case = Case(B, S, 1024, 16, 8, seed=150 + B, rows=4096, positions=pos)
+    args = list(case.args(device))
+
+    def odd(t):  # same values, storage offset of one element (2 bytes)
+        buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=device)
+        v = buf[1:].view(t.shape)
+        v.copy_(t)
+        return v
+    shifted = list(args)
+    shifted[0], shifted[2] = odd(args[0]), odd(args[2])
+    assert shifted[0].data_ptr() % 16 and shifted[2].data_ptr() % 16
+    ref_kernels = launched_kernels(lambda: mqk.fused_qkv_rope(*args))
+    assert launched_kernels(lambda: mqk.fused_qkv_rope(*shifted)) == ref_kernels
+    assert "tile_reg" not in ref_kernels
+    for a, b in zip(mqk.fused_qkv_rope(*args), mqk.fused_qkv_rope(*shifted)):
+        assert torch.equal(a, b)

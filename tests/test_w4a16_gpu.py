@@ -525,3 +525,20 @@ def test_fused_w4a16_tile_variants(variant, scale_dtype, device):
     finally:
         mqk.set_option("prefill_tile", old)
     _check_w4((q, k, v), x, projs, gq, gk, cos, sin, Hq, Hkv, pos.numpy(), f"w4a16 tile {variant}")
+
+
+@pytest.mark.parametrize("M,K,N", [(300, 1024, 1000), (200, 512, 264), (1024, 2048, 4088)])
+def test_w4a16_gemm_partial_last_tile_pipelined(M, K, N, device):
+    """N not a multiple of 128: the pipelined int4 tile kernel runs the partial last
+    tile (its columns past N re-read in-range chunks and are never stored, the zeros
+    come with 4-byte loads), not the register-staged fallback."""
+    import mqk
+    from conftest import launched_kernels
+    qw, sc, qz = _quant(K, N, seed=M + K)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).bfloat16()
+    d = [t.to(device) for t in (x, qw, sc, qz)]
+    run = lambda: mqk.w4a16_gemm(*d, 128)
+    assert launched_kernels(run) in (["tile_w4"], ["tile_w4_head"])
+    out = run()
+    torch.cuda.synchronize()
+    _check_gemm(out, x, qw, sc, qz, 128, f"partial tile M={M} K={K} N={N}")
