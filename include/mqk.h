@@ -377,6 +377,15 @@ const char* mqk_tile_variants(void);
  */
 int mqk_read_probe(const void* src, size_t bytes, int blocks, uint32_t* out, void* stream);
 
+/*
+ * Measurement probe, no counterpart in the reference: one lane runs a dependent
+ * chain of `spins` fp32 FMAs and writes to the device array out[3] the shader
+ * clock cycles (s_memtime) and 100 MHz ticks (s_memrealtime) that passed over
+ * it, and the chain's result; out[0] / out[1] * 100 is the shader clock in MHz
+ * while it ran.  bench.py reads it right after a timed region.
+ */
+int mqk_clock_probe(uint64_t* out, int spins, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

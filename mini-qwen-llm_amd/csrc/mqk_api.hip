@@ -1034,6 +1034,10 @@ int mqk_read_probe(const void* src, size_t bytes, int blocks, uint32_t* out, voi
   return hip_status(launch_read_probe(src, bytes, blocks, out, static_cast<hipStream_t>(stream)), "read probe launch");
 }
 
+int mqk_clock_probe(uint64_t* out, int spins, void* stream) {
+  return hip_status(launch_clock_probe(out, spins, static_cast<hipStream_t>(stream)), "clock probe launch");
+}
+
 const char* mqk_tile_variants(void) {
   static const char* const text = [] {
     static char buf[512];

@@ -175,6 +175,9 @@ hipError_t launch_w4_gemv(const uint16_t* x, const WeightArgs& w, int64_t M, int
 // HBM read-rate probe (bench.py): reads `bytes` (16-byte aligned) once over
 // `blocks` workgroups of 512 threads and writes one word per workgroup to out.
 hipError_t launch_read_probe(const void* src, size_t bytes, int blocks, uint32_t* out, hipStream_t stream);
+// Shader clock probe (bench.py): out[0..2] = shader clocks and 100 MHz ticks over a
+// dependent chain of `spins` FMAs, and the chain's result.
+hipError_t launch_clock_probe(uint64_t* out, int spins, hipStream_t stream);
 
 // Standalone QK-norm + RoPE.
 hipError_t launch_norm_rope(const uint16_t* q_raw, const uint16_t* k_raw, const EpilogueArgs& e,

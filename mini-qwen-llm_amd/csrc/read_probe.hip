@@ -1,4 +1,6 @@
-// HBM read-rate probe (measurement only; not on the op's path): reads `bytes`
+// Measurement probes (not on the op's path).
+//
+// HBM read-rate probe: reads `bytes`
 // once with 16-byte loads spread over every CU and writes one word per
 // workgroup, so that bench.py can time a plain stream of a decode step's weight
 // bytes next to the decode kernel that streams them.
@@ -43,7 +45,30 @@ __global__ void __launch_bounds__(kProbeThreads) read_probe_kernel(const u32x4_t
   }
 }
 
+// Shader clock probe: one lane runs a dependent FMA chain of `spins` steps and
+// reads the shader clock counter (s_memtime) and the constant 100 MHz counter
+// (s_memrealtime) around it, so the host gets the clock the GPU ran at right then:
+// out[0] = shader clocks, out[1] = 100 MHz ticks, out[2] = the chain's result.
+__global__ void clock_probe_kernel(uint64_t* __restrict__ out, int spins) {
+  if (threadIdx.x != 0) return;
+  const uint64_t t0 = __builtin_amdgcn_s_memtime();
+  const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+  float v = float(spins);
+  for (int i = 0; i < spins; ++i) v = __builtin_fmaf(v, 0.999f, 1.0f);
+  const uint64_t t1 = __builtin_amdgcn_s_memtime();
+  const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
+  out[0] = t1 - t0;
+  out[1] = r1 - r0;
+  out[2] = uint64_t(__float_as_uint(v));
+}
+
 }  // namespace
+
+hipError_t launch_clock_probe(uint64_t* out, int spins, hipStream_t stream) {
+  if (!out || spins < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(clock_probe_kernel, dim3(1), dim3(64), 0, stream, out, spins);
+  return hipGetLastError();
+}
 
 hipError_t launch_read_probe(const void* src, size_t bytes, int blocks, uint32_t* out, hipStream_t stream) {
   if (!src || !out || bytes % 16 != 0 || blocks < 1 || (reinterpret_cast<uintptr_t>(src) & 15u) != 0)

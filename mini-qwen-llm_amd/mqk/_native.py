@@ -143,6 +143,7 @@ SIGNATURES = {
     "mqk_get_option": (_I64, [ctypes.c_char_p]),
     "mqk_tile_variants": (ctypes.c_char_p, []),
     "mqk_read_probe": (_I, [_P, _SZ, _I, _P, _P]),
+    "mqk_clock_probe": (_I, [_P, _I, _P]),
 }
 
 
