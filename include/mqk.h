@@ -104,11 +104,14 @@ int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
 /*
  * fp32 twin of mqk_fused_qkv_rope_bf16: x, weights, q_gamma / k_gamma and the
  * cos / sin tables are fp32, and q / k / v are written in fp32
- * (mini_qwen/kernels/fused_qkv_rope.py:130-195 run on fp32 tensors: an fp32
- * GEMM, then the norm and RoPE of :84-127 loading and storing fp32).  Products
- * and sums in fp32 on the matrix cores; norm and RoPE in fp32.  Same position
- * rules and validation as the bf16 entry point; hidden must be a multiple of
- * 32.  Needs no workspace.  Launches on `stream` without synchronising.
+ * (fused_qkv_rope() called with fp32 tensors, mini_qwen/kernels/fused_qkv_rope.py:130-195).
+ * Products and sums in fp32 on the matrix cores; norm and RoPE in fp32; one
+ * rounding per output, to fp32.  Deliberate difference: the reference's Triton
+ * kernel rounds Q and K to bf16 before storing them into its fp32 outputs
+ * (:117-120); this entry point keeps fp32 precision (it computes the fp32
+ * composition of the unfused path).  Same position rules and validation as the
+ * bf16 entry point; hidden must be a multiple of 32.  Needs no workspace.
+ * Launches on `stream` without synchronising.
  */
 int mqk_fused_qkv_rope_f32(const float* x, const float* w_q, const float* w_k, const float* w_v,
                            const float* q_gamma, const float* k_gamma, const float* cos, const float* sin,
@@ -120,7 +123,10 @@ int mqk_fused_qkv_rope_f32(const float* x, const float* w_q, const float* w_k, c
  * model loaded with dtype=float16, mini_qwen/model/loader.py:12-52): every
  * float input fp16, q / k / v written in fp16.  The fp32 front's kernel with
  * fp16 tiles on the fp16 matrix cores (exact products, fp32 sums); norm and
- * RoPE in fp32; one fp16 rounding per output.  Same validation; no workspace.
+ * RoPE in fp32; one fp16 rounding per output.  Deliberate differences: the
+ * reference rounds the fp16 GEMM output before the norm (:167-169) and Q / K to
+ * bf16 before the fp16 store (:117-120); neither rounding happens here.  Same
+ * validation; no workspace.
  */
 int mqk_fused_qkv_rope_f16(const mqk_f16* x, const mqk_f16* w_q, const mqk_f16* w_k, const mqk_f16* w_v,
                            const mqk_f16* q_gamma, const mqk_f16* k_gamma, const mqk_f16* cos, const mqk_f16* sin,

@@ -1,9 +1,12 @@
 // The fused front for fp32 (and fp16) callers: x, weights, norm weights and
-// RoPE tables in that type, q / k / v out in it.  The reference op accepts fp32
-// tensors too:
-// its GEMM is then an fp32 matmul and its Triton kernel loads, normalises,
-// rotates and stores in fp32 (mini_qwen/kernels/fused_qkv_rope.py:84-127,
-// :167-173; the fp32 layer of the reference's CPU-runnable configuration).
+// RoPE tables in that type, q / k / v out in it.  The reference op accepts such
+// tensors too (mini_qwen/kernels/fused_qkv_rope.py:130-195; the fp32 layer of the
+// reference's CPU-runnable configuration), but its Triton kernel rounds every Q /
+// K output to bf16 before storing it into the fp32 / fp16 buffer (:117-120), and
+// with fp16 tensors its GEMM output is rounded to fp16 before the norm.  This
+// kernel keeps the fp32 projection, norm and RoPE and rounds once, to the output
+// type: it computes the op's fp32 composition (the unfused reference path,
+// attention.py:102-109) to fp32 / fp16 precision, not the fused reference's bits.
 //
 // One workgroup of four waves computes 32 (or 16) token rows x one head (128
 // columns): each wave owns 32 columns and runs the fp32 matrix core (products

@@ -238,7 +238,11 @@ def version() -> int:
 # share a workspace.
 #
 # A HIP graph captured on a stream keeps the workspace address it was captured
-# with and writes partials and counters there on every replay.  A buffer is
+# with and writes partials and counters there on every replay -- whichever stream
+# it is replayed on.  A replay on another stream therefore shares the capture
+# stream's workspace: it must not overlap calls issued on the capture stream (or
+# other replays of graphs captured there); order them with events, or capture on
+# a stream that issues nothing else.  A buffer is
 # therefore never released once a launch has used it: when a call needs more,
 # the stream gets a new, larger buffer (at least twice the old size, so this
 # happens a few times per stream at most) and the old one is retired, kept
@@ -306,6 +310,30 @@ def decode_recomputes(device=None, stream=None) -> int:
 def retired_workspaces() -> int:
     """Number of superseded workspaces kept alive for graphs captured earlier."""
     return len(_retired)
+
+
+def workspace_bytes() -> dict:
+    """Device bytes the workspaces hold: ``{"current": ..., "retired": ...}`` (the
+    buffers streams use now, and the superseded ones kept for captured graphs)."""
+    with _ws_lock:
+        return {"current": sum(b.numel() for b in _workspaces.values()),
+                "retired": sum(b.numel() for b in _retired)}
+
+
+def release_workspaces(retired_only: bool = True) -> int:
+    """Drop the superseded workspaces (``retired_only``), or every workspace, and
+    return the bytes released to torch's allocator.  Only for callers that know
+    no HIP graph captured earlier still replays the op: a graph keeps the
+    workspace address it was captured with, and a replay after its buffer was
+    released writes freed memory.  A stream whose workspace was released gets a
+    new zero-filled one at its next call (so not during capture)."""
+    with _ws_lock:
+        n = sum(b.numel() for b in _retired)
+        _retired.clear()
+        if not retired_only:
+            n += sum(b.numel() for b in _workspaces.values())
+            _workspaces.clear()
+    return n
 
 
 def blocks(heads: int, head_dim: int) -> int:

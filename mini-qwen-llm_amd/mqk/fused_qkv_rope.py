@@ -30,10 +30,13 @@ Differences from the reference, all deliberate:
 
 fp32 inputs (the dtype of the reference's CPU-runnable fp32 layer) take a
 separate kernel: an fp32 projection on the matrix cores (fp32 products and
-sums), norm and RoPE in fp32, fp32 outputs, as the reference computes for fp32
-tensors (an fp32 GEMM, then its kernel loads and stores fp32).  fp16 inputs (a
-model loaded in fp16) take the same kernel on the fp16 matrix cores (exact
-products, fp32 sums), with fp16 outputs.
+sums), norm and RoPE in fp32, fp32 outputs.  fp16 inputs (a model loaded in
+fp16) take the same kernel on the fp16 matrix cores (exact products, fp32
+sums), with fp16 outputs.  Differences from the reference on these dtypes: its
+Triton kernel rounds Q and K to bf16 before storing them into the fp32 / fp16
+outputs (fused_qkv_rope.py:117-120), and on fp16 its GEMM output is rounded to
+fp16 before the norm; here neither happens, so the outputs carry fp32 / fp16
+precision (the unfused composition's values), not the fused reference's bits.
 """
 from __future__ import annotations
 

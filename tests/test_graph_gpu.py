@@ -312,3 +312,60 @@ def test_graph_replay_paged_input_norm_decode(device):
         with torch.cuda.graph(graph, stream=stream):
             out = run()
     _replay_checks(graph, tuple(out) + (kc, vc), tuple(eager) + eager_caches, run)
+
+
+def test_graph_replay_on_another_stream(device):
+    """A graph captured on stream A replays on stream B into A's workspace; with
+    B ordered after A's eager work by an event (and A's next work after the
+    replay), the replays equal the eager call bit for bit.  This is the supported
+    pattern; overlapping them would race on the shared workspace."""
+    import mqk
+    case = Case(32, 1, 1024, 16, 8, seed=4250, rows=4096,
+                positions=torch.randint(0, 4096, (32,), generator=torch.Generator().manual_seed(3),
+                                        dtype=torch.int32))
+    args = case.args(device)
+    sa, sb = torch.cuda.Stream(device), torch.cuda.Stream(device)
+    with torch.cuda.stream(sa):
+        eager = mqk.fused_qkv_rope(*args)
+        sa.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=sa):
+            out = mqk.fused_qkv_rope(*args)
+    for rep in range(3):
+        with torch.cuda.stream(sa):
+            again = mqk.fused_qkv_rope(*args)  # eager work on A's workspace
+        done_a = torch.cuda.Event()
+        done_a.record(sa)
+        for t in out:
+            t.fill_(0)
+        sb.wait_stream(torch.cuda.current_stream(device))
+        sb.wait_event(done_a)
+        with torch.cuda.stream(sb):
+            graph.replay()
+        sa.wait_stream(sb)
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(out, eager)), f"replay {rep}"
+        assert all(torch.equal(a, b) for a, b in zip(again, eager))
+
+
+def test_workspace_bytes_and_release(device):
+    """workspace_bytes() reports what the workspaces hold; release_workspaces()
+    frees the retired ones (or all), and the next call allocates a fresh, zeroed
+    workspace and gives the same bits."""
+    import mqk
+    case = Case(48, 1, 1024, 16, 8, seed=4251, rows=4096,
+                positions=torch.randint(0, 4096, (48,), generator=torch.Generator().manual_seed(4),
+                                        dtype=torch.int32))
+    args = case.args(device)
+    ref = mqk.fused_qkv_rope(*args)
+    torch.cuda.synchronize()
+    held = mqk.workspace_bytes()
+    assert held["current"] > 0
+    assert mqk.release_workspaces() == held["retired"]
+    assert mqk.workspace_bytes()["retired"] == 0
+    released = mqk.release_workspaces(retired_only=False)
+    assert released == held["current"] and mqk.workspace_bytes() == {"current": 0, "retired": 0}
+    out = mqk.fused_qkv_rope(*args)
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(out, ref))
+    assert mqk.workspace_bytes()["current"] > 0
