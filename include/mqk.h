@@ -176,7 +176,9 @@ int mqk_qk_norm_rope_bf16(const mqk_bf16* q_raw, const mqk_bf16* k_raw, const mq
  *   qweight [K/8, N] int32   nibble i of qweight[j, n] is W[8j+i, n] (w4a16_gemm.py:11)
  *   scales  [K/group, N]     bf16 or fp16 (scale_type)
  *   qzeros  [K/group, N/8]   int32, packed along N, nibble i of qzeros[g, j] is z[g, 8j+i]
- *   dequant: (q - z) * s computed exactly in fp32, rounded once to bf16 for the MFMA.
+ *   dequant: (q - z) * s computed exactly in fp32; M <= 16 multiplies the exact
+ *   fp32 weight with fp32 sums (column-parallel kernels, no workspace), larger M
+ *   rounds it once to bf16 for the bf16 MFMA tiles.
  * Supported: K % 64 == 0, group % 64 == 0, K % group == 0, N % 8 == 0.
  */
 int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales,
@@ -187,11 +189,12 @@ int mqk_w4a16_gemm(const mqk_bf16* x, const int32_t* qweight, const void* scales
 size_t mqk_w4a16_gemm_workspace_size(int64_t M, int64_t K, int64_t N);
 
 /*
- * mqk_w4a16_gemm with the kernel choice of the fused op: small and mid M (the
- * decode regime of w4a16_gemm.py:110-189, the reference's M = 1 GEMV, and its
- * published decode shapes M in {1, 4, 8, 16}, K = 1024, N = 4096) run on the
- * split-K decode kernel, which streams the packed weights over every CU once for
- * up to sixteen 64-row blocks; larger M on the tile kernels.  The workspace is
+ * mqk_w4a16_gemm with the kernel choice of the fused op: M <= 16 (the decode
+ * regime of w4a16_gemm.py:110-189, the reference's M = 1 GEMV, and its published
+ * decode shapes M in {1, 4, 8, 16}, K = 1024, N = 4096) runs the column-parallel
+ * kernels of mqk_w4a16_gemm (no workspace); mid M runs on the split-K decode
+ * kernel, which streams the packed weights over every CU once for up to sixteen
+ * 64-row blocks; larger M on the tile kernels.  The workspace is
  * as for mqk_fused_qkv_rope_bf16 (zero-filled once at allocation, not shared by
  * calls that may overlap).  N not a multiple of 128 or operands not 16-byte
  * aligned: the tile kernels of mqk_w4a16_gemm, no workspace needed.
