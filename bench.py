@@ -92,7 +92,7 @@ def time_steps(fn, steps, warmup):
     return e0.elapsed_time(e1) / steps, wall
 
 
-def gpu_clock_mhz(dev, spins=200000):
+def gpu_clock_mhz(dev, spins=20000):
     """The shader clock (MHz) right now: mqk_clock_probe's clock cycles over its
     100 MHz ticks, on the current stream (so it runs right after queued work)."""
     import torch
