@@ -490,7 +490,8 @@ def main(argv=None) -> int:
         a4 = flops(8192, h4, n4) / (ms4 * 1e-3) / 1e12
         sec["config4_30b_a3b_s8192"] = {"tokens_per_s": round(8192 / (ms4 * 1e-3), 1),
                                         "ms_per_step": round(ms4, 6), "bound": "mfma", "achieved_TFLOPs": round(a4, 2),
-                                        "frac": round(a4 / PEAK_BF16_TFLOPS, 4)}
+                                        "frac": round(a4 / PEAK_BF16_TFLOPS, 4),
+                                        "traffic": load_traffic("qkv_tile_pair_c4_traffic")}
         log(f"[bench] config 4: {ms4 * 1e3:.1f} us/step, {a4:.0f} TFLOP/s")
         # mid token counts: Qwen3-8B prefill of B=1 x S=512 (the reference's smallest
         # published (B, S) point, docs/02_fused_qkv_rope.md:69-81, there at 0.6B shapes

@@ -51,6 +51,8 @@ std::atomic<int64_t> g_decode_passes{16};  // most 64-row blocks one decode laun
 std::atomic<int64_t> g_head_tiles{1};  // one round of single-head tiles where the planner models them fastest
 std::atomic<int64_t> g_tile_ksplit{1};  // split-K tile launches: 0 off, 1 by cost model, >= 2 that split count
 std::atomic<int64_t> g_gemv_max_m{kGemvMaxM};  // W4A16 GEMMs with M up to this run the column-parallel kernel
+std::atomic<int64_t> g_pair_tiles{1};  // pair-tile variants (24, 25) as tile chooser candidates
+std::atomic<int64_t> g_pair_max_spins{1 << 14};  // a pair side's polls for its partner before it hands its half over
 
 constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace (per head)
 
@@ -198,7 +200,8 @@ int plan_tile_split(int64_t M, int64_t K, int n_tiles, const Topology& topo, boo
 }
 
 Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const Topology& topo,
-                bool allow_blocks = true, bool in_norm = false, bool allow_split = true) {
+                bool allow_blocks = true, bool in_norm = false, bool allow_split = true, bool allow_pair = false) {
+  allow_pair = allow_pair && !int4 && aligned && g_pair_tiles.load() != 0;
   Plan pl;
   const int64_t cus = topo.cus;
   if (use_decode(M) && aligned) {
@@ -287,13 +290,12 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
     pl.v = hv;
     return pl;
   }
-  pl.v = choose_tile_variant(int(g_prefill_tile.load()), M, n_tiles, int4, topo.cus);
+  pl.v = choose_tile_variant(int(g_prefill_tile.load()), M, n_tiles, int4, topo.cus, allow_pair);
   if (!pl.v || !g_tail_split.load() || !aligned || M <= 64) return pl;
   const int64_t r = M % pl.v->bm;
   if (r == 0 || r > 64 || !use_decode(r)) return pl;
-  const int64_t ct = n_tiles / pl.v->hpt;
-  const int64_t rounds_all = ((M + pl.v->bm - 1) / pl.v->bm * ct + cus - 1) / cus;
-  const int64_t rounds_main = ((M - r) / pl.v->bm * ct + cus - 1) / cus;
+  const int64_t rounds_all = (tile_count(*pl.v, M, n_tiles) + cus - 1) / cus;
+  const int64_t rounds_main = (tile_count(*pl.v, M - r, n_tiles) + cus - 1) / cus;
   if (rounds_main >= rounds_all) return pl;
   const int splits = decode_splits_for(r, K, n_tiles, int(g_decode_splits.load()), topo.cus, topo.xcds);
   if (splits > 0) {
@@ -312,7 +314,11 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
   const Topology topo = device_topology();
   p.cus = topo.cus;
   p.xcds = topo.xcds;
-  Plan pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, true, p.in_gamma != nullptr);
+  // pair tiles: q/k/v outputs with head_dim 128 (their epilogue splits a head in
+  // 32-dim runs) and paged-cache slots below 2^31 (held in 32 bits)
+  const bool pair_ok = e.qkv && e.head_dim == kHeadDim &&
+                       (!e.k_cache || double(e.num_blocks) * double(e.block_size) < 2147483647.0);
+  Plan pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, true, p.in_gamma != nullptr, true, pair_ok);
   if (!pl.v && pl.splits == 0)
     return fail(MQK_ERR_BAD_OPTION, "prefill_tile variant %lld cannot run this problem (%d heads%s)",
                 (long long)g_prefill_tile.load(), p.n_tiles, int4 ? ", int4 weights" : "");
@@ -320,6 +326,9 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
   // so the scales never start before them, whichever kernel runs this call)
   auto region = [&](const Plan& q) {
     if (q.ksplit > 0) return kDecodeCounterBytes + tile_split_part_bytes(q.v->id, p.M, p.n_tiles, q.ksplit);
+    if (q.v && is_pair_variant(q.v->id))
+      return std::max(pair_tile_workspace_bytes(q.v->id, p.M - q.tail, p.n_tiles),
+                      q.splits > 0 ? decode_workspace_bytes(p.n_tiles, q.splits, q.passes) : size_t(0));
     return q.splits > 0 ? decode_workspace_bytes(p.n_tiles, q.splits, q.passes) : decode_counter_bytes();
   };
   size_t base = region(pl);
@@ -329,7 +338,12 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
   const bool split_ok = epilogue_aligned(e) && !(p.in_gamma && pl.v && tile_dma_lds_bytes(pl.v->id) + p.K * 2 > 160 * 1024);
   if (pl.ksplit > 0 && (!fits(base) || !split_ok)) {
     // a workspace sized without the split-K tile launch (or operands it cannot take): plan without it
-    pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, true, p.in_gamma != nullptr, false);
+    pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, true, p.in_gamma != nullptr, false, pair_ok);
+    base = region(pl);
+  }
+  if (pl.v && is_pair_variant(pl.v->id) && !fits(base)) {
+    // a workspace sized without the pair tiles' exchange area: plan without them
+    pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, true, p.in_gamma != nullptr, false, false);
     base = region(pl);
   }
   while (!pl.v && pl.passes > 1 && !fits(base)) {
@@ -347,8 +361,9 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
     base = decode_counter_bytes();
   }
   const size_t scale_off = align_up(base, 256);
-  const size_t need =
-      p.in_gamma ? scale_off + size_t(p.M) * sizeof(float) : ((pl.splits > 0 || pl.ksplit > 0) ? base : 0);
+  const bool pair = pl.v && is_pair_variant(pl.v->id);
+  const size_t need = p.in_gamma ? scale_off + size_t(p.M) * sizeof(float)
+                                 : ((pl.splits > 0 || pl.ksplit > 0 || pair) ? base : 0);
   if (need > 0 && (!workspace || ws_bytes < need))
     return fail(MQK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given%s", need, ws_bytes,
                 workspace ? "" : " (NULL)");
@@ -371,7 +386,12 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
       v = choose_tile_variant(p.n_tiles % 2 == 0 ? 4 : 1, p.M, p.n_tiles, int4, p.cus);
     ProblemArgs pm = p;
     pm.M = p.M - pl.tail;
-    const int st = hip_status(launch_tile(*v, int4, pm, w, e, int(g_group_m.load()), stream), "tile kernel launch");
+    const int st =
+        is_pair_variant(v->id)
+            ? hip_status(launch_pair_tile(v->id, pm, w, e, int(g_group_m.load()), workspace,
+                                          int(g_pair_max_spins.load()), stream),
+                         "pair tile kernel launch")
+            : hip_status(launch_tile(*v, int4, pm, w, e, int(g_group_m.load()), stream), "tile kernel launch");
     if (st != MQK_OK || pl.tail == 0) return st;
   }
   // the decode kernel on the last pl.tail rows (all of them when there is no tile
@@ -423,8 +443,9 @@ size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hid
   const int tiles = Hq + 2 * Hkv;
   size_t n = 0;
   for (int int4 = 0; int4 < 2; ++int4) {  // the same size serves both weight formats
-    const Plan pl = plan_fused(int4, T, hidden, tiles, true, device_topology());
+    const Plan pl = plan_fused(int4, T, hidden, tiles, true, device_topology(), true, false, true, true);
     if (pl.splits > 0) n = std::max(n, decode_workspace_bytes(tiles, pl.splits, pl.passes));
+    if (pl.v && is_pair_variant(pl.v->id)) n = std::max(n, pair_tile_workspace_bytes(pl.v->id, T - pl.tail, tiles));
     if (pl.ksplit > 0) n = std::max(n, kDecodeCounterBytes + tile_split_part_bytes(pl.v->id, T, tiles, pl.ksplit));
   }
   return n;
@@ -1001,6 +1022,15 @@ int mqk_set_option(const char* name, int64_t value) {
   } else if (!strcmp(name, "group_m")) {
     if (value < 1 || value > 1024) return fail(MQK_ERR_BAD_OPTION, "group_m must be in [1, 1024]");
     g_group_m = value;
+  } else if (!strcmp(name, "pair_tiles")) {
+    if (value < 0 || value > 1) return fail(MQK_ERR_BAD_OPTION, "pair_tiles must be 0 or 1");
+    g_pair_tiles = value;
+  } else if (!strcmp(name, "pair_max_spins")) {
+    if (value < 0 || value > (1 << 24)) return fail(MQK_ERR_BAD_OPTION, "pair_max_spins must be in [0, 2^24]");
+    g_pair_max_spins = value;
+  } else if (!strcmp(name, "pair_hold")) {
+    if (value < 0 || value > 4096) return fail(MQK_ERR_BAD_OPTION, "pair_hold must be in [0, 4096]");
+    g_pair_hold = int(value);
   } else if (!strcmp(name, "gemv_max_m")) {
     if (value < 0 || value > kGemvMaxM) return fail(MQK_ERR_BAD_OPTION, "gemv_max_m must be in [0, %d]", kGemvMaxM);
     g_gemv_max_m = value;
@@ -1023,6 +1053,9 @@ int64_t mqk_get_option(const char* name) {
   if (!strcmp(name, "tile_ksplit")) return g_tile_ksplit.load();
   if (!strcmp(name, "head_tiles")) return g_head_tiles.load();
   if (!strcmp(name, "gemv_max_m")) return g_gemv_max_m.load();
+  if (!strcmp(name, "pair_tiles")) return g_pair_tiles.load();
+  if (!strcmp(name, "pair_max_spins")) return g_pair_max_spins.load();
+  if (!strcmp(name, "pair_hold")) return g_pair_hold;
   if (!strcmp(name, "decode_force_recompute")) return g_decode_force_recompute;
   if (!strcmp(name, "decode_max_spins")) return g_decode_max_spins;
   if (!strcmp(name, "device_cus")) return device_topology().cus;    // read-only: the current device's
@@ -1045,8 +1078,9 @@ const char* mqk_tile_variants(void) {
     buf[0] = '\0';
     for (int i = 0; i < tile_variant_count(); ++i) {
       const TileVariant* v = tile_variant(i);
+      // (a pair variant's hpt counts the heads of both workgroups of a pair)
       n += snprintf(buf + n, sizeof(buf) - n, "%s%d:%dx%d/%dw", i ? ";" : "", v->id, v->bm,
-                                    v->hpt * kHeadDim, v->threads / 64);
+                    is_pair_variant(v->id) ? v->hpt * kHeadDim / 2 : v->hpt * kHeadDim, v->threads / 64);
     }
     return buf;
   }();

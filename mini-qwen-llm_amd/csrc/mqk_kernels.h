@@ -96,7 +96,12 @@ struct TileVariant {
 int tile_variant_count();
 const TileVariant* tile_variant(int index);
 // Picks a variant for the problem (id 0 = automatic).
-const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles, int int4, int cus);
+// allow_pair: the pair-tile variants (24, 25) may be chosen (bf16 q/k/v outputs
+// with head_dim 128 and a workspace for their exchange).
+const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles, int int4, int cus,
+                                       bool allow_pair = false);
+// Workgroups of one launch of variant v over M rows and n_tiles heads.
+int64_t tile_count(const TileVariant& v, int64_t M, int n_tiles);
 hipError_t launch_tile(const TileVariant& v, int int4, const ProblemArgs& p, const WeightArgs& w,
                        const EpilogueArgs& e, int group_m, hipStream_t stream);
 // Direct-to-LDS pipelined tile kernel (variant ids >= 10, bf16 weights).
@@ -117,6 +122,21 @@ hipError_t launch_tile_dma(int id, const ProblemArgs& p, const WeightArgs& w, co
 hipError_t launch_tile_dma_split(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                                  int ksplit, int force_recompute, int max_spins, void* workspace, hipStream_t stream);
 size_t tile_split_part_bytes(int id, int64_t M, int n_tiles, int ksplit);
+// Pair tiles (ids 24: 256 x 192, 25: 256 x 320; bf16 weights, head_dim 128): two
+// workgroups cover 2 * hpt + 1 heads of 256 rows (hpt = 1 or 2 whole heads each,
+// and half of the head they share).  The sides exchange the shared head's row sums
+// of squares through the workspace: kDecodeCounterBytes of counters (the pair
+// words reuse the split-K tile lines, zero between launches), then per pair
+// 2 * 256 floats of sums and a 256 x 64 float hand-over area;
+// pair_tile_workspace_bytes(id, M, n_tiles) in all.  max_spins bounds a side's
+// wait for its partner before it hands its half over.
+hipError_t launch_pair_tile(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e, int group_m,
+                            void* workspace, int max_spins, hipStream_t stream);
+size_t pair_tile_workspace_bytes(int id, int64_t M, int n_tiles);
+inline bool is_pair_variant(int id) { return id == 24 || id == 25; }
+// (tests) side 1 of every pair waits this many ~4 us intervals before it publishes,
+// which sends side 0 down the hand-over path once its bounded wait runs out.
+extern int g_pair_hold;
 // int4-weight (W4A16) variant of the pipelined kernel, ids 30-33.
 hipError_t launch_tile_dma_w4(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                               int group_m, hipStream_t stream);

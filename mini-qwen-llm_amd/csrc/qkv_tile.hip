@@ -423,6 +423,8 @@ const TileVariant kVariants[] = {
     {21, 128, 1, 0, 512},
     {22, 256, 1, 0, 512},
     {23, 128, 2, 0, 512},
+    {24, 256, 3, 0, 512},  // pair tiles: hpt = heads per pair of workgroups (256 x 192 each)
+    {25, 256, 5, 0, 512},  // (256 x 320 each)
     {30, 128, 3, 0, 512},
     {31, 256, 2, 0, 512},
     {32, 128, 2, 0, 256},
@@ -451,10 +453,17 @@ static bool supports(const TileVariant& v, int int4) {
   return v.id < 10 || (int4 ? v.id >= 30 : v.id < 30);
 }
 
-const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles, int int4, int cus_) {
+int64_t tile_count(const TileVariant& v, int64_t M, int n_tiles) {
+  return ((M + v.bm - 1) / v.bm) * (n_tiles / v.hpt) * (is_pair_variant(v.id) ? 2 : 1);
+}
+
+const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles, int int4, int cus_, bool allow_pair) {
+  // (a pair launch has one exchange word per pair in the workspace's kSplitMaxTiles lines)
+  auto pair_fits = [&](const TileVariant& v) { return allow_pair && tile_count(v, M, n_tiles) / 2 <= kSplitMaxTiles; };
   if (requested_id > 0) {
     const TileVariant* v = find_variant(requested_id);
-    if (!v || n_tiles % v->hpt != 0 || !supports(*v, int4)) return nullptr;
+    if (!v || n_tiles % v->hpt != 0 || !supports(*v, int4) || (is_pair_variant(v->id) && !pair_fits(*v)))
+      return nullptr;
     return v;
   }
   // Score = relative per-tile speed (measured on MI355X) x fraction of the last
@@ -469,8 +478,13 @@ const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles,
   // pipelined variant tiles and for explicit requests.
   // (23, 128x256 with 8 waves and 3 stages of 64 k, measured ~1.2x the rate of 13:
   // the reference's published Qwen3-0.6B B=4 x S=512 call in 24.6 us against 30.3)
+  // (pair tiles, 24 = 2 x 256 x 192 per 3 heads and 25 = 2 x 256 x 320 per 5 heads,
+  // need the workspace and head_dim 128 (allow_pair).  Measured on MI355X: 24 no
+  // faster than 16 at Qwen3-8B prefill (104.6-104.9 us against 104.5-105.6), so it
+  // ranks just below it; 25 takes BASELINE config 4's 512 tiles in two rounds in
+  // 170.5-171.7 us against 188.5-189.0 for variant 18's 640 tiles)
   static const Cand bf16_cands[] = {{16, 1.00f}, {18, 1.27f}, {17, 1.26f}, {11, 0.94f}, {10, 1.19f},
-                                    {23, 0.90f}, {13, 0.75f}, {12, 0.75f}};
+                                    {23, 0.90f}, {13, 0.75f}, {12, 0.75f}, {25, 1.33f}, {24, 0.99f}};
   // (33 is 31 with waves of 256 x 32, so every int4 weight is dequantised once per
   // workgroup instead of twice: 419 us against 447 us on the W4A16 ragged batch)
   static const Cand int4_cands[] = {{33, 1.07f}, {31, 1.00f}, {30, 0.75f}, {32, 0.54f}};
@@ -481,8 +495,8 @@ const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles,
   float best_score = -1.f;
   for (int i = 0; i < ncand; ++i) {
     const TileVariant* v = find_variant(cands[i].id);
-    if (!v || n_tiles % v->hpt != 0 || !supports(*v, int4)) continue;
-    const int64_t tiles = ((M + v->bm - 1) / v->bm) * (n_tiles / v->hpt);
+    if (!v || n_tiles % v->hpt != 0 || !supports(*v, int4) || (is_pair_variant(v->id) && !pair_fits(*v))) continue;
+    const int64_t tiles = tile_count(*v, M, n_tiles);
     const int64_t rounds = (tiles + cus - 1) / cus;
     const float util = float(tiles) / float(rounds * cus);
     // rows past M in the last row tile are wasted work

@@ -28,6 +28,8 @@
 // take 8-column pairs of a row (columns [8c, 8c+8) and [64+8c, +8)) so the
 // RMSNorm sum of squares is an 8-lane butterfly and every RoPE pair is
 // thread-local; each output row segment is written with 16-byte stores.
+#include <type_traits>
+
 #include "mqk_device.h"
 #include "mqk_kernels.h"
 
@@ -56,12 +58,14 @@ __device__ __forceinline__ void norm_rope_pair(float& lo, float& hi, float rms, 
 // SBK = K extent of one stage (32 or 64): staged rows of 64 or 128 bytes.  A
 // CU's L2 -> LDS rate depends on the bytes per row: 128-byte rows measured
 // ~1.35x the rate of 64-byte rows (fewer, full-line requests in flight).
-template <int BM, int NH, int WM, int WN, int NS, int SBK>
+// XC: extra columns beyond the NH whole heads (64 in a pair tile: half of a head
+// shared with the partner tile).
+template <int BM, int NH, int WM, int WN, int NS, int SBK, int XC = 0>
 struct DmaShape {
   static constexpr int kRowBytes = SBK * 2;
   static constexpr int kChunks = kRowBytes / 16;         // 16-byte chunks per staged row
   static constexpr int kRowsPerLoad = 1024 / kRowBytes;  // rows filled by one 1 KB load instruction
-  static constexpr int kBN = NH * kHeadDim;
+  static constexpr int kBN = NH * kHeadDim + XC;
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = kWaves * 64;
   static constexpr int kTM = BM / WM;
@@ -139,11 +143,11 @@ __device__ __forceinline__ void norm_chunk(unsigned char* chunk_ptr, int64_t k0,
 // launch finishes a tile's rows in 32-row units spread over its workgroups).
 template <int BM, int NH, int WM, int WN, int THREADS, int MB, int NB, class RowV, class SlotV>
 __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], const RowV& prow,
-                                              const SlotV& cslot, int ht, int64_t m0, const ProblemArgs& p,
+                                              const SlotV& cslot, int head0, int64_t m0, const ProblemArgs& p,
                                               const EpilogueArgs& e, unsigned char* smem,
                                               uint32_t units = 0xFFFFFFFFu) {
   constexpr int kTM = BM / WM;
-  constexpr int kTN = NH * kHeadDim / WN;
+  constexpr int kTN = NB * 32;  // (a pair tile's waves also hold the shared half head's columns)
   constexpr int kRowStep = THREADS / 8;
   constexpr int kPasses = BM / kRowStep;
   static_assert(BM % kRowStep == 0, "the epilogue's row passes must cover the tile");
@@ -152,6 +156,9 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
   // beside the 128 accumulators of an 8-wave 256-row tile (256 VGPRs per lane at
   // two waves per SIMD) spilled; 4-wave tiles (one wave per SIMD) have room.
   constexpr bool kPreload = kPasses <= 2 || (kPasses <= 4 && THREADS <= 256);
+  // beside more than 128 accumulators (the 256 x 320 pair tile) the gammas are read
+  // per row pass instead of held through the epilogue
+  constexpr bool kLateGamma = MB * NB * 16 > 128;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -171,10 +178,12 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
     s2[1] = *reinterpret_cast<const u32x4_t*>(e.sin + base + pr.dim_hi);
   };
   if (e.qkv) {
-    gq[0] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + pr.dim_lo);
-    gq[1] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + pr.dim_hi);
-    gk[0] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + pr.dim_lo);
-    gk[1] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + pr.dim_hi);
+    if constexpr (!kLateGamma) {
+      gq[0] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + pr.dim_lo);
+      gq[1] = *reinterpret_cast<const u32x4_t*>(e.q_gamma + pr.dim_hi);
+      gk[0] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + pr.dim_lo);
+      gk[1] = *reinterpret_cast<const u32x4_t*>(e.k_gamma + pr.dim_hi);
+    }
     if constexpr (kPreload) {
 #pragma unroll
       for (int q = 0; q < kPasses; ++q) load_rows(q, cs[q], sn[q]);
@@ -199,7 +208,7 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
       }
     }
     __syncthreads();
-    const int head = ht * NH + j;
+    const int head = head0 + j;
     int proj, hh;
     split_head(head, e.Hq, e.Hkv, proj, hh);
     // this head's gamma pairs in fp32, converted once for all its row passes
@@ -240,7 +249,13 @@ __device__ __forceinline__ void tile_epilogue(const f32x16_t (&acc)[MB][NB], con
         } else {
           load_rows(q, c2, s2);
         }
-        const u32x4_t* g = proj == 0 ? gq : gk;
+        u32x4_t glate[2];
+        if constexpr (kLateGamma) {
+          const uint16_t* gam = pick3<const uint16_t>(proj, e.q_gamma, e.k_gamma, e.k_gamma);
+          glate[0] = *reinterpret_cast<const u32x4_t*>(gam + pr.dim_lo);
+          glate[1] = *reinterpret_cast<const u32x4_t*>(gam + pr.dim_hi);
+        }
+        const u32x4_t* g = kLateGamma ? glate : (proj == 0 ? gq : gk);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int wd = i >> 1, sh = (i & 1) * 16;
@@ -375,33 +390,283 @@ __device__ __forceinline__ int hw_xcc_id() {
   return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11));  // hwreg(HW_REG_XCC_ID, 0, 4)
 }
 
-template <int BM, int NH, int WM, int WN, int NS, int SBK>
-__global__ void __launch_bounds__(WM* WN * 64)
-tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
-  using S = DmaShape<BM, NH, WM, WN, NS, SBK>;
-  constexpr int kRowBytes = S::kRowBytes;
-  constexpr int BN = S::kBN;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[S::kLdsBytes];
-  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+// Exchange area of a pair-tile launch (in the workspace, see launch_pair_tile).
+struct PairX {
+  uint32_t* words;  // pair q's word at words[q * kSplitLineBytes / 4]: bit s = side s has published its
+                    // half's row sums of squares, bit 2 + s = side s has handed its half over; zero
+                    // between launches (the pair's last reader clears it)
+  float* sumsq;     // [pair][side][BM]: each side's half-head sum of squares per row
+  float* handoff;   // [pair][BM][64]: fp32 half-head values of a side that handed its half over
+  int max_spins;    // polls of the pair word before a side hands its half over
+  int hold;         // (tests) side 1 sleeps this many ~4 us intervals before publishing,
+                    // so that side 0's bounded wait runs out and it hands its half over
+};
 
+// Epilogue of a pair tile: the NH whole heads as tile_epilogue, then this side's
+// half of the shared head h_pair + NH.  The half holds head dims 32*side + [0, 32)
+// and 32*side + [64, 96), which are the runs of threads c8 = 4*side + (0..3) of the
+// whole-head epilogue, so every RoPE pair is local to the tile.  Its RMSNorm needs
+// the other half's sum of squares: each side publishes its rows' sums (the first
+// two butterfly levels of head_sum over its four runs; the third level, own + other,
+// gives the bits of the whole-head epilogue) and sets its bit in the pair word, runs
+// its whole heads, then reads the partner's sums.  A side that polls max_spins
+// times without seeing the partner's bit hands its fp32 half over instead (values,
+// then bit 2 + side); the partner, arriving later, sees that bit and finishes both
+// halves.  Published data uses agent-scope (device-coherent) stores and loads, so
+// the two sides may run on any XCDs.  V heads (and plain outputs) need no exchange.
+template <int BM, int NH, int WM, int WN, int THREADS, int MB, int NB, class RowV, class SlotV>
+__device__ __forceinline__ void pair_epilogue(const f32x16_t (&acc)[MB][NB], RowV prow, SlotV cslot,
+                                              int h_pair, int side, int pair, int64_t m0, const ProblemArgs& p,
+                                              const EpilogueArgs& e, unsigned char* smem, const PairX& px) {
+  constexpr int kTM = BM / WM;
+  constexpr int kTN = NB * 32;
+  constexpr int kHalf0 = NH * kHeadDim;  // first tile column of the shared half
+  constexpr int kHStep = THREADS / 4;    // rows of one half pass (4 threads per row)
+  constexpr int kHPasses = BM / kHStep;
+  static_assert(BM % kHStep == 0, "the half passes must cover the tile");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave % WM;
   const int wn = wave / WM;
+  const int c32 = lane & 31;
+  const int lhalf = lane >> 5;
+  const int c4 = tid & 3;
+  float* ep = reinterpret_cast<float*>(smem);
+  __shared__ uint32_t xword;
+  int proj, hh;
+  split_head(h_pair + NH, e.Hq, e.Hkv, proj, hh);
+  const bool qk = e.qkv && proj != 2;
+  const int head0 = h_pair + side * (NH + 1);
+  // RoPE table rows and paged-KV-cache slots of the whole-head epilogue's rows
+  // (tid / 8 + q * THREADS / 8)
+#pragma unroll
+  for (int q = 0; q < BM / (THREADS / 8); ++q) {
+    const int64_t t = m0 + (tid >> 3) + q * (THREADS / 8);
+    prow[q] = (e.qkv && t < p.M) ? int32_t(rope_row(e, t)) : 0;
+    cslot[q] = (e.qkv && t < p.M) ? paged_slot(e, t) : -1;
+  }
+
+  // the half's accumulator columns -> ep[row][0, 64)
+  auto stage_half = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int col = wn * kTN + nb * 32;
+      if (col >= kHalf0) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int row = wm * kTM + mb * 32 + 8 * (i >> 2) + 4 * lhalf + (i & 3);
+            ep[row * kEpiPitch + (col - kHalf0) + c32] = acc[mb][nb][i];
+          }
+      }
+    }
+  };
+  // this thread's runs of row r: half columns [8*c4, +8) and [32 + 8*c4, +8)
+  auto read_row = [&](int r, float (&lo)[8], float (&hi)[8]) __attribute__((always_inline)) {
+    const float* rowp = ep + r * kEpiPitch;
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const f32x4_t a = *reinterpret_cast<const f32x4_t*>(rowp + 8 * c4 + 4 * v);
+      const f32x4_t b = *reinterpret_cast<const f32x4_t*>(rowp + 32 + 8 * c4 + 4 * v);
+      lo[4 * v] = a.x; lo[4 * v + 1] = a.y; lo[4 * v + 2] = a.z; lo[4 * v + 3] = a.w;
+      hi[4 * v] = b.x; hi[4 * v + 1] = b.y; hi[4 * v + 2] = b.z; hi[4 * v + 3] = b.w;
+    }
+  };
+  // sum of squares of the row's half: run_sumsq, then head_sum's first two levels
+  auto half_sumsq = [&](const float (&lo)[8], const float (&hi)[8]) __attribute__((always_inline)) {
+    float v = run_sumsq(lo, hi);
+    v += dpp_move<0xB1>(v);  // quad_perm [1,0,3,2]
+    v += dpp_move<0x4E>(v);  // quad_perm [2,3,0,1]
+    return v;
+  };
+  // norm (qk: with the other half's sums `other`), RoPE and stores of side s's half from ep
+  auto finish_half = [&](int s, const float* other) __attribute__((always_inline)) {
+    const PairRuns pr = pair_runs(4 * s + c4, kHeadDim);
+#pragma unroll
+    for (int q = 0; q < kHPasses; ++q) {
+      const int r = (tid >> 2) + q * kHStep;
+      const int64_t t = m0 + r;
+      const bool valid = t < p.M;
+      float lo[8], hi[8];
+      read_row(r, lo, hi);
+      if (qk) {
+#pragma clang fp contract(off)
+        const float own = half_sumsq(lo, hi);
+        const float ss = own + __hip_atomic_load(other + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float rms = head_rms(ss, e.eps, kHeadDim);
+        const int64_t base = (valid ? rope_row(e, t) : 0) * kHeadDim;
+        u32x4_t c2[2], s2[2];
+        c2[0] = *reinterpret_cast<const u32x4_t*>(e.cos + base + pr.dim_lo);
+        c2[1] = *reinterpret_cast<const u32x4_t*>(e.cos + base + pr.dim_hi);
+        s2[0] = *reinterpret_cast<const u32x4_t*>(e.sin + base + pr.dim_lo);
+        s2[1] = *reinterpret_cast<const u32x4_t*>(e.sin + base + pr.dim_hi);
+        const uint16_t* gam = pick3<const uint16_t>(proj, e.q_gamma, e.k_gamma, e.k_gamma);
+        const u32x4_t g0 = *reinterpret_cast<const u32x4_t*>(gam + pr.dim_lo);
+        const u32x4_t g1 = *reinterpret_cast<const u32x4_t*>(gam + pr.dim_hi);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int wd = i >> 1, sh = (i & 1) * 16;
+          norm_rope_pair(lo[i], hi[i], rms, bf16_to_f32((g0[wd] >> sh) & 0xFFFFu),
+                         bf16_to_f32((g1[wd] >> sh) & 0xFFFFu), c2, s2, wd, sh);
+        }
+      }
+      if (!valid) continue;
+      u32x4_t o1, o2;
+      o1.x = pack_bf16x2(lo[0], lo[1]); o1.y = pack_bf16x2(lo[2], lo[3]);
+      o1.z = pack_bf16x2(lo[4], lo[5]); o1.w = pack_bf16x2(lo[6], lo[7]);
+      o2.x = pack_bf16x2(hi[0], hi[1]); o2.y = pack_bf16x2(hi[2], hi[3]);
+      o2.z = pack_bf16x2(hi[4], hi[5]); o2.w = pack_bf16x2(hi[6], hi[7]);
+      const int H = proj == 0 ? e.Hq : e.Hkv;
+      uint16_t* obase = pick3<uint16_t>(proj, e.q, e.k, e.v);  // k / v may be null (cache only)
+      if (obase) {
+        uint16_t* dst = obase + (t * H + hh) * kHeadDim;
+        __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(dst + pr.dim_lo));
+        __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(dst + pr.dim_hi));
+      }
+      const int64_t slot = proj != 0 ? paged_slot(e, t) : -1;
+      if (slot >= 0) {
+        uint16_t* crow = paged_row(e, slot, proj, hh);
+        __builtin_nontemporal_store(o1, reinterpret_cast<u32x4_t*>(crow + pr.dim_lo));
+        __builtin_nontemporal_store(o2, reinterpret_cast<u32x4_t*>(crow + pr.dim_hi));
+      }
+    }
+  };
+
+  if (!qk) {  // a V head: each side stores its half as it is
+    tile_epilogue<BM, NH, WM, WN, THREADS>(acc, prow, cslot, head0, m0, p, e, smem);
+    stage_half();
+    __syncthreads();
+    finish_half(side, nullptr);
+    return;
+  }
+  uint32_t* word = px.words + size_t(pair) * (kSplitLineBytes / 4);
+  float* const ss_mine = px.sumsq + (size_t(pair) * 2 + side) * BM;
+  float* const ss_other = px.sumsq + (size_t(pair) * 2 + (side ^ 1)) * BM;
+  const uint32_t p_other = 1u << (side ^ 1), h_other = 4u << (side ^ 1);
+  // ---- publish this half's sums of squares --------------------------------------
+  if (side == 1)
+    for (int n = 0; n < px.hold; ++n) __builtin_amdgcn_s_sleep(127);
+  stage_half();
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kHPasses; ++q) {
+    const int r = (tid >> 2) + q * kHStep;
+    float lo[8], hi[8];
+    read_row(r, lo, hi);
+    const float v = half_sumsq(lo, hi);
+    if (c4 == 0) __hip_atomic_store(ss_mine + r, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's sums have been written
+  __syncthreads();                                    // ... and every thread's
+  if (tid == 0) xword = __hip_atomic_fetch_or(word, 1u << side, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const uint32_t seen = xword;
+  // ---- the whole heads (their barriers separate the reads of xword from its next write)
+  tile_epilogue<BM, NH, WM, WN, THREADS>(acc, prow, cslot, head0, m0, p, e, smem);
+  bool other_half = false, clear = false;
+  if (seen & p_other) {
+    // the partner published first: it clears the word, unless it handed its half over
+    other_half = (seen & h_other) != 0;
+    clear = other_half;
+  } else {
+    if (tid == 0) {
+      uint32_t v = 0;
+      for (int n = 0;; ++n) {
+        v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((v & p_other) || n >= px.max_spins) break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+      xword = v;
+    }
+    __syncthreads();
+    if (!(xword & p_other)) {
+      // no partner yet: hand this half over (values, then the bit)
+      stage_half();
+      __syncthreads();
+      float* dst = px.handoff + size_t(pair) * BM * 64;
+#pragma unroll
+      for (int q = 0; q < kHPasses; ++q) {
+        const int r = (tid >> 2) + q * kHStep;
+        float lo[8], hi[8];
+        read_row(r, lo, hi);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __hip_atomic_store(dst + r * 64 + 8 * c4 + i, lo[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(dst + r * 64 + 32 + 8 * c4 + i, hi[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (tid == 0) xword = __hip_atomic_fetch_or(word, 4u << side, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      if (!(xword & p_other)) return;  // the partner will finish this half
+    }
+    clear = true;  // the partner has published and no longer reads the word
+  }
+  // ---- finish this half (and the partner's, if it handed it over) -------------------
+  stage_half();
+  __syncthreads();
+  finish_half(side, ss_other);
+  if (other_half) {
+    __syncthreads();  // ep is reloaded with the partner's values
+    const float* src = px.handoff + size_t(pair) * BM * 64;
+#pragma unroll
+    for (int q = 0; q < kHPasses; ++q) {
+      const int r = (tid >> 2) + q * kHStep;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        ep[r * kEpiPitch + 8 * c4 + i] =
+            __hip_atomic_load(src + r * 64 + 8 * c4 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ep[r * kEpiPitch + 32 + 8 * c4 + i] =
+            __hip_atomic_load(src + r * 64 + 32 + 8 * c4 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __syncthreads();
+    finish_half(side ^ 1, ss_mine);
+  }
+  if (clear && tid == 0) __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The pipelined tile kernel.  XC == 0: one workgroup per BM x (NH*128) tile of
+// whole heads (px unused).  XC == 64: a pair tile: the heads
+// [h0, h0 + 2*NH + 1) of a pair are covered by two workgroups, side 0 holding
+// heads h0 .. h0+NH-1 and half of head h0+NH, side 1 the other half of that head
+// and heads h0+NH+1 .. h0+2NH; pair_epilogue finishes the shared head.
+template <int BM, int NH, int WM, int WN, int NS, int SBK, int XC = 0>
+__global__ void __launch_bounds__(WM* WN * 64)
+tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m, PairX px) {
+  using S = DmaShape<BM, NH, WM, WN, NS, SBK, XC>;
+  constexpr int kRowBytes = S::kRowBytes;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[S::kLdsBytes];
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = XC ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;  // (uniform: fewer VGPRs in pair tiles)
+  const int wm = wave % WM;
+  const int wn = wave / WM;
 
   // ---- tile coordinates: XCD-contiguous ids, grouped along M ------------------
+  // (pair tiles: the two sides of a pair are consecutive tile ids, so they share
+  // an XCD and a round of the grid; the grouping runs over pairs)
   const int n_mt = int((p.M + BM - 1) / BM);
-  const int n_ht = p.n_tiles / NH;
-  const int tile = xcd_tile_id(blockIdx.x, gridDim.x, p.xcds);
+  const int n_ht = XC ? p.n_tiles / (2 * NH + 1) : p.n_tiles / NH;
+  const int tile0 = xcd_tile_id(blockIdx.x, gridDim.x, p.xcds);
+  const int side = XC ? (tile0 & 1) : 0;
+  const int tile = XC ? (tile0 >> 1) : tile0;
   const int per_group = group_m * n_ht;
   const int grp = tile / per_group;
   const int first_m = grp * group_m;
   const int gsz = min(group_m, n_mt - first_m);
   const int rr = tile - grp * per_group;
   const int mt = first_m + rr % gsz;
-  const int ht = rr / gsz;
+  const int ht = rr / gsz;  // (pair tiles: the pair's index along the heads)
   const int64_t m0 = int64_t(mt) * BM;
+  // first head of the tile's whole heads, and (pair tiles) the shared head
+  const int h_pair = ht * (2 * NH + 1);
+  const int head0 = XC ? h_pair + side * (NH + 1) : ht * NH;
 
   // Epilogue geometry: thread -> rows (tid / 8) + q * kRowStep and the column pairs
   // [8c, 8c+8) / [64+8c, +8) of every head.  The RoPE table row of each of its
@@ -411,14 +676,19 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   // (vector types: indexed in registers even where the compiler merges the
   // per-row code paths, where a plain array would go to scratch memory)
   typedef int32_t RowV __attribute__((ext_vector_type(kPasses)));
-  typedef int64_t SlotV __attribute__((ext_vector_type(kPasses)));
+  // (pair tiles: 32-bit slots, so that the epilogue's row state fits beside the
+  // accumulators; their launch requires caches of fewer than 2^31 slots)
+  typedef typename std::conditional<XC != 0, int32_t, int64_t>::type SlotT;
+  typedef SlotT SlotV __attribute__((ext_vector_type(kPasses)));
   RowV prow;
   SlotV cslot;  // paged-KV-cache slot of the row (-1: none)
 #pragma unroll
   for (int q = 0; q < kPasses; ++q) {
     const int64_t t = m0 + (tid >> 3) + q * kRowStep;
-    prow[q] = (e.qkv && t < p.M) ? int32_t(rope_row(e, t)) : 0;
-    cslot[q] = (e.qkv && t < p.M) ? paged_slot(e, t) : -1;
+    // (pair tiles look the rows and slots up in their epilogue: held through the
+    // main loop beside 160 accumulators they would spill)
+    prow[q] = (!XC && e.qkv && t < p.M) ? int32_t(rope_row(e, t)) : 0;
+    cslot[q] = (!XC && e.qkv && t < p.M) ? paged_slot(e, t) : -1;
   }
   const int64_t K = p.K;
 
@@ -437,9 +707,14 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
       src[i] = p.x + grow * K + chunk * 8;
     } else {
       const int brow = row - BM;
-      int proj, hh;
-      split_head(ht * NH + brow / kHeadDim, e.Hq, e.Hkv, proj, hh);
-      int64_t col = int64_t(hh) * kHeadDim + (brow % kHeadDim);
+      int proj, hh, head = head0 + brow / kHeadDim, dim = brow % kHeadDim;
+      if (XC && brow >= NH * kHeadDim) {  // the shared head's half: dims 32*side + [0, 32) and + [64, 96)
+        const int u = brow - NH * kHeadDim;
+        head = h_pair + NH;
+        dim = (u < 32 ? u : u + 32) + 32 * side;
+      }
+      split_head(head, e.Hq, e.Hkv, proj, hh);
+      int64_t col = int64_t(hh) * kHeadDim + dim;
       col = col < w.n_cols[proj] ? col : w.n_cols[proj] - 1;
       src[i] = w.w[proj] + col * K + chunk * 8;
     }
@@ -521,7 +796,10 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
   }
   barrier();  // every wave is done with the ring; the epilogue reuses the LDS
 
-  tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, cslot, ht, m0, p, e, smem);
+  if constexpr (XC != 0)
+    pair_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, cslot, h_pair, side, mt * n_ht + ht, m0, p, e, smem, px);
+  else
+    tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, cslot, head0, m0, p, e, smem);
 }
 
 // The split-K launch of the pipelined kernel (a separate kernel, so that the
@@ -903,7 +1181,7 @@ hipError_t launch_dma(const ProblemArgs& p, const WeightArgs& w, const EpilogueA
   const size_t dyn = p.in_gamma ? size_t(p.K) * 2 : 0;
   if (S::kLdsBytes + dyn > 160 * 1024) return hipErrorInvalidValue;
   hipLaunchKernelGGL((tile_dma_kernel<BM, NH, WM, WN, NS, SBK>), dim3(blocks), dim3(S::kThreads), dyn, stream, p, w, e,
-                     group_m < 1 ? 1 : group_m);
+                     group_m < 1 ? 1 : group_m, PairX{});
   return hipGetLastError();
 }
 
@@ -1190,7 +1468,34 @@ tile_dma_w4_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
     }
   }
   barrier();  // every wave is done with the ring; the epilogue reuses the LDS
-  tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, cslot, ht, m0, p, e, smem);
+  tile_epilogue<BM, NH, WM, WN, S::kThreads>(acc, prow, cslot, ht * NH, m0, p, e, smem);
+}
+
+template <int BM, int NH, int WM, int WN, int NS, int SBK>
+size_t pair_bytes(int64_t M, int n_tiles) {
+  const int64_t pairs = (M + BM - 1) / BM * (n_tiles / (2 * NH + 1));
+  return kDecodeCounterBytes + size_t(pairs) * (2 * BM + BM * 64) * sizeof(float);
+}
+
+template <int BM, int NH, int WM, int WN, int NS, int SBK>
+hipError_t launch_pair(const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e, int group_m,
+                       void* workspace, int max_spins, hipStream_t stream) {
+  using S = DmaShape<BM, NH, WM, WN, NS, SBK, 64>;
+  if (p.n_tiles % (2 * NH + 1) != 0 || !workspace || e.head_dim != kHeadDim) return hipErrorInvalidValue;
+  const int64_t pairs = (p.M + BM - 1) / BM * (p.n_tiles / (2 * NH + 1));
+  if (pairs > kSplitMaxTiles) return hipErrorInvalidValue;
+  const size_t dyn = p.in_gamma ? size_t(p.K) * 2 : 0;
+  if (S::kLdsBytes + dyn > 160 * 1024) return hipErrorInvalidValue;
+  char* ws = static_cast<char*>(workspace);
+  PairX px;
+  px.words = reinterpret_cast<uint32_t*>(ws + kSplitWordsOffset);
+  px.sumsq = reinterpret_cast<float*>(ws + kDecodeCounterBytes);
+  px.handoff = px.sumsq + size_t(pairs) * 2 * BM;
+  px.max_spins = max_spins < 0 ? 0 : max_spins;
+  px.hold = g_pair_hold;
+  hipLaunchKernelGGL((tile_dma_kernel<BM, NH, WM, WN, NS, SBK, 64>), dim3(unsigned(pairs * 2)), dim3(S::kThreads), dyn,
+                     stream, p, w, e, group_m < 1 ? 1 : group_m, px);
+  return hipGetLastError();
 }
 
 template <int BM, int NH, int WM, int WN, int NS>
@@ -1229,8 +1534,29 @@ hipError_t launch_tile_dma(int id, const ProblemArgs& p, const WeightArgs& w, co
   }
 }
 
+int g_pair_hold = 0;
+
+hipError_t launch_pair_tile(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e, int group_m,
+                            void* workspace, int max_spins, hipStream_t stream) {
+  switch (id) {
+    case 24: return launch_pair<256, 1, 4, 2, 2, 64>(p, w, e, group_m, workspace, max_spins, stream);  // 256x192
+    case 25: return launch_pair<256, 2, 4, 2, 2, 64>(p, w, e, group_m, workspace, max_spins, stream);  // 256x320
+    default: return hipErrorInvalidValue;
+  }
+}
+
+size_t pair_tile_workspace_bytes(int id, int64_t M, int n_tiles) {
+  switch (id) {
+    case 24: return pair_bytes<256, 1, 4, 2, 2, 64>(M, n_tiles);
+    case 25: return pair_bytes<256, 2, 4, 2, 2, 64>(M, n_tiles);
+    default: return 0;
+  }
+}
+
 int tile_dma_lds_bytes(int id) {
   switch (id) {
+    case 24: return DmaShape<256, 1, 4, 2, 2, 64, 64>::kLdsBytes;
+    case 25: return DmaShape<256, 2, 4, 2, 2, 64, 64>::kLdsBytes;
     case 10: return DmaShape<256, 2, 4, 2, 4, 32>::kLdsBytes;
     case 11: return DmaShape<128, 3, 2, 4, 4, 32>::kLdsBytes;
     case 12: return DmaShape<256, 1, 4, 1, 4, 32>::kLdsBytes;

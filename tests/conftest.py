@@ -107,6 +107,8 @@ _KERNEL_NAMES = (("decode_multi_kernel", "decode_multi"), ("decode_long_kernel",
 
 
 def _short_kernel_name(name: str):
+    if re.search(r"tile_dma_kernel(<\d+, \d+, \d+, \d+, \d+, \d+, 64>|I(Li\d+E){6}Li64EE)", name):
+        return "tile_pair"  # pair tiles (256 x 192 or 256 x 320, two workgroups per 3 or 5 heads)
     if re.search(r"tile_dma_kernel(<\d+, 1,|ILi\d+ELi1E)", name):
         return "tile_head"  # single-head tiles (64 x 128 or 128 x 128)
     if re.search(r"tile_dma_w4_kernel(<\d+, 1,|ILi\d+ELi1E)", name):
@@ -120,7 +122,7 @@ def _short_kernel_name(name: str):
 def launched_kernels(fn, *, warm=True):
     """The library kernels one call of ``fn`` launches, in launch order, as
     short names ("decode" = one 64-row block, "decode_multi" = several blocks,
-    "tile", "tile_head" = single-head tiles, "tile_split" = split-K tile, "tile_w4", "tile_w4_head", "tile_reg", "row_scale", "norm_rope",
+    "tile", "tile_head" = single-head tiles, "tile_pair" = pair tiles, "tile_split" = split-K tile, "tile_w4", "tile_w4_head", "tile_reg", "row_scale", "norm_rope",
     "f32" = the fp32 front, "gemv" = the small-M W4A16 GEMM), recorded with torch.profiler (the reference counts its
     kernels the same way, tests/test_fused_qkv_rope.py:287-311).  Other
     kernels (torch's own fills and copies) are left out."""

@@ -139,12 +139,25 @@ def test_head_tile_plan(lib):
 
 @pytest.mark.usefixtures("no_head_tiles")
 def test_workspace_size(lib):
-    assert lib.mqk_fused_qkv_rope_workspace_size(2048, 32, 8, 4096) == 0     # tile kernel only
+    from mqk import _native
+    C = 4096 + 256 + 512 * 128  # 1024 arrival counters, the statistics line, a line per split-K tile
+    # BASELINE config 4 (T = 8192, hidden 2048, 40 heads) in pair tiles of 2 x 256 x 320 per 5
+    # heads: the counters (the pair words reuse the split-K tile lines), then per pair
+    # 2 x 256 floats of row sums of squares and a 256 x 64 float hand-over area
+    assert lib.mqk_fused_qkv_rope_workspace_size(8192, 32, 4, 2048) == C + 32 * 8 * (2 * 256 + 256 * 64) * 4
+    # at most 512 pairs (one exchange word each in the counters' 512 tile lines): T = 16384
+    # still runs as pairs, 16640 (520 pairs) as 256 x 256 tiles without a workspace
+    assert lib.mqk_fused_qkv_rope_workspace_size(16384, 32, 4, 2048) == C + 512 * (2 * 256 + 256 * 64) * 4
+    assert lib.mqk_fused_qkv_rope_workspace_size(16640, 32, 4, 2048) == 0
+    _native.set_option("pair_tiles", 0)
+    try:
+        assert lib.mqk_fused_qkv_rope_workspace_size(8192, 32, 4, 2048) == 0   # tile kernel only
+        assert lib.mqk_fused_qkv_rope_workspace_size(2048, 32, 8, 4096) == 0   # tile kernel only
+    finally:
+        _native.set_option("pair_tiles", 1)
     assert lib.mqk_fused_qkv_rope_workspace_size(0, 32, 8, 4096) == 0
     n = lib.mqk_fused_qkv_rope_workspace_size(64, 32, 8, 4096)
-    C = 4096 + 256 + 512 * 128  # 1024 arrival counters, the statistics line, a line per split-K tile
     assert n >= C + 48 * 64 * 128 * 4  # counters + at least one fp32 partial per head
-    from mqk import _native
     _native.set_option("tile_ksplit", 0)  # decode blocks or the one-workgroup-per-tile launch only
     try:
         # 64 < T: one decode launch covers every 64-row block; each block has its own
@@ -194,7 +207,11 @@ def test_split_tile_plan(lib):
     try:
         assert lib.mqk_fused_qkv_rope_workspace_size(512, 32, 8, 4096) == C + 64 * 4 * part
         assert lib.mqk_fused_qkv_rope_workspace_size(1024, 32, 8, 4096) == C + 128 * 2 * part
-        assert lib.mqk_fused_qkv_rope_workspace_size(2048, 32, 8, 4096) == 0  # 256 tiles: one each
+        _native.set_option("pair_tiles", 0)
+        try:
+            assert lib.mqk_fused_qkv_rope_workspace_size(2048, 32, 8, 4096) == 0  # 256 tiles: one each
+        finally:
+            _native.set_option("pair_tiles", 1)
         _native.set_option("tile_ksplit", 0)
         try:
             assert lib.mqk_fused_qkv_rope_workspace_size(512, 32, 8, 4096) == 0

@@ -64,6 +64,13 @@ def test_default_plan_by_token_count(T, plan, device):
     assert launched_kernels(_bf16_call(case, device)) == plan
 
 
+def test_config4_is_one_pair_tile_launch(device):
+    """BASELINE config 4 (hidden 2048, 32 / 4 heads, T = 8192): 512 pair tiles of
+    256 x 320 in two rounds, one launch."""
+    case = Case(1, 8192, 2048, 32, 4, seed=19)
+    assert launched_kernels(_bf16_call(case, device)) == ["tile_pair"]
+
+
 @pytest.mark.parametrize("hidden,hq,hkv,T,plan", [
     (1024, 16, 8, 128, ["tile_head"]), (1024, 16, 8, 1024, ["tile_head"]), (1024, 16, 8, 2048, ["tile"]),
     (2048, 32, 4, 128, ["tile_head"]), (2048, 32, 4, 512, ["tile_head"]), (2048, 32, 4, 1536, ["tile"]),
