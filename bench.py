@@ -8,7 +8,12 @@ Headline (``value``): BASELINE config 2, Qwen3-8B prefill B=4 x S=512 (2048
 tokens, hidden 4096, 32 Q heads, 8 KV heads, head_dim 128, bf16), tokens/s of
 mqk.fused_qkv_rope with every input resident in HBM.  One step = one call of the
 op (one kernel launch) on that batch; K steps are timed with HIP events on the
-stream the op launches on, bracketed by device synchronisation.
+stream the op launches on, bracketed by device synchronisation.  The headline is
+measured after the secondary workloads (its own W warm-up steps still precede its
+K timed steps), so that it runs at the clock the GPU holds under load; the same
+measurement taken first in the process, on a cold clock, is reported as the
+secondary line ``config2_first_in_process`` (``--no-secondary``: only that one,
+as the headline).
 
 ``roofline`` prices the dominant (only) kernel of a step: 2*T*hidden*N FLOP per
 launch / average launch duration, against the bf16 dense MFMA peak (2.5
@@ -421,15 +426,25 @@ def main(argv=None) -> int:
         return 0
 
     # ---- headline: config 2, Qwen3-8B prefill B=4 x S=512 ---------------------
+    # With the secondary workloads on, the headline is measured after them: its own
+    # W warm-up steps then K timed steps run at the clock the GPU holds under load
+    # rather than while it leaves idle (a handful of warm-up steps lasts well under a
+    # millisecond).  The same measurement taken first in the process, on a cold
+    # clock, is kept as the secondary line config2_first_in_process.
     B, S, hidden, Hq, Hkv = 4, 512, 4096, 32, 8
     T = B * S
     N = (Hq + 2 * Hkv) * D
+    fl = flops(T, hidden, N)
     log(f"[bench] config 2 prefill T={T} hidden={hidden} N={N}: {args.warmup} warmup + {args.steps} steps")
     ms, wall = bench_prefill(T, B, S, hidden, Hq, Hkv, 1, args.steps, args.warmup, dev)
     clock_headline = gpu_clock_mhz(dev)
-    fl = flops(T, hidden, N)
     achieved = fl / (ms * 1e-3) / 1e12
-    log(f"[bench] config 2: {ms * 1e3:.1f} us per launch, {achieved:.0f} TFLOP/s")
+    first = {"ms_per_step": round(ms, 6), "tokens_per_s": round(T / (ms * 1e-3), 1),
+             "achieved_TFLOPs": round(fl / (ms * 1e-3) / 1e12, 2),
+             "frac": round(fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+             "warmup": args.warmup, "steps": args.steps, "gpu_clock_mhz_after_timed": clock_headline,
+             "note": "config 2 measured first in the process, before any other GPU work"}
+    log(f"[bench] config 2 (first in the process): {ms * 1e3:.1f} us per launch")
     result = {
         "metric": "fused QKV+QKNorm+RoPE tokens/s and % roofline (Qwen3-8B shapes, bf16, 1 GPU)",
         "value": round(T / (ms * 1e-3), 1),
@@ -452,6 +467,7 @@ def main(argv=None) -> int:
                      "flop_per_launch": fl},
         "wall_s_timed": round(wall, 4),
         "gpu_clock_mhz_after_timed": clock_headline,
+        "measured": "first in the process (no secondary workloads ran)",
     }
 
     if not args.no_secondary:
@@ -465,9 +481,9 @@ def main(argv=None) -> int:
             "tokens_per_s": round(T / (mss * 1e-3), 1), "ms_per_step": round(mss, 6), "bound": "mfma",
             "achieved_TFLOPs": round(acs, 2), "frac": round(acs / PEAK_BF16_TFLOPS, 4),
             "warmup": "3 s of back-to-back steps", "gpu_clock_mhz_after_timed": clk,
-            "headline_gpu_clock_mhz_after_timed": clock_headline}
+            "first_in_process_gpu_clock_mhz_after_timed": clock_headline}
         log(f"[bench] config 2 after a 3 s warm-up: {mss * 1e3:.1f} us per launch, {acs:.0f} TFLOP/s, "
-            f"clock {clk} MHz (headline: {clock_headline} MHz)")
+            f"clock {clk} MHz (first in the process: {clock_headline} MHz)")
         # config 3: decode B=64, weight-read bound
         dms, _ = bench_decode(64, hidden, Hq, Hkv, 2, max(50, args.steps), 300, dev)
         dgbs = decode_bytes(64, hidden, N) / (dms * 1e-3) / 1e9
@@ -543,6 +559,19 @@ def main(argv=None) -> int:
             "achieved_TFLOPs": round(ar, 2), "frac": round(ar / PEAK_BF16_TFLOPS, 4),
             "reference_ms_rtx4090d": 0.198, "reference_source": "docs/02_fused_qkv_rope.md:60-64"}
         log(f"[bench] 0.6B B=4 x S=512: {msr * 1e3:.1f} us/step (reference: 198 us on an RTX 4090 D)")
+        # the headline again, after the workloads above: --warmup then --steps, as before
+        sec["config2_first_in_process"] = first
+        ms, wall = bench_prefill(T, B, S, hidden, Hq, Hkv, 1, args.steps, args.warmup, dev)
+        clock_headline = gpu_clock_mhz(dev)
+        achieved = fl / (ms * 1e-3) / 1e12
+        log(f"[bench] config 2 (headline, after the secondary workloads): {ms * 1e3:.1f} us per launch, "
+            f"{achieved:.0f} TFLOP/s")
+        result.update({"value": round(T / (ms * 1e-3), 1), "ms_per_step": round(ms, 6),
+                       "wall_s_timed": round(wall, 4), "gpu_clock_mhz_after_timed": clock_headline,
+                       "measured": "after the secondary workloads (their GPU work precedes this "
+                                   "measurement's own --warmup steps); config2_first_in_process holds "
+                                   "the same measurement taken first"})
+        result["roofline"].update({"achieved": round(achieved, 2), "frac": round(achieved / PEAK_BF16_TFLOPS, 4)})
         result["secondary"] = sec
 
     if not args.no_cpu:
