@@ -376,6 +376,8 @@ int mqk_fused_qkv_rope_ex_w4a16(const mqk_bf16* x, const int32_t* qw_q, const vo
  *                    hands its half of the shared head over (default 16384; for tests)
  *   "pair_hold"      (tests) side 1 of every pair waits this many ~4 us intervals before
  *                    publishing its sums, so that side 0 takes the hand-over path (default 0)
+ *   "pair_cross_xcd" (tests) 1: the two sides of a pair take adjacent workgroup ids, which
+ *                    the round-robin dispatch places on different XCDs (default 0: one XCD)
  * Returns MQK_OK or MQK_ERR_BAD_OPTION.  mqk_get_option also reads "device_cus" and
  * "device_xcds": the compute units and XCDs of the current device, as the planner and
  * the decode kernel's grid use them (hipDeviceGetAttribute; -1 for unknown names).

@@ -1030,7 +1030,10 @@ int mqk_set_option(const char* name, int64_t value) {
     g_pair_max_spins = value;
   } else if (!strcmp(name, "pair_hold")) {
     if (value < 0 || value > 4096) return fail(MQK_ERR_BAD_OPTION, "pair_hold must be in [0, 4096]");
-    g_pair_hold = int(value);
+    g_pair_hold = (g_pair_hold & ~0xFFFF) | int(value);
+  } else if (!strcmp(name, "pair_cross_xcd")) {
+    if (value != 0 && value != 1) return fail(MQK_ERR_BAD_OPTION, "pair_cross_xcd must be 0 or 1");
+    g_pair_hold = (g_pair_hold & 0xFFFF) | (int(value) << 16);
   } else if (!strcmp(name, "gemv_max_m")) {
     if (value < 0 || value > kGemvMaxM) return fail(MQK_ERR_BAD_OPTION, "gemv_max_m must be in [0, %d]", kGemvMaxM);
     g_gemv_max_m = value;
@@ -1055,7 +1058,8 @@ int64_t mqk_get_option(const char* name) {
   if (!strcmp(name, "gemv_max_m")) return g_gemv_max_m.load();
   if (!strcmp(name, "pair_tiles")) return g_pair_tiles.load();
   if (!strcmp(name, "pair_max_spins")) return g_pair_max_spins.load();
-  if (!strcmp(name, "pair_hold")) return g_pair_hold;
+  if (!strcmp(name, "pair_hold")) return g_pair_hold & 0xFFFF;
+  if (!strcmp(name, "pair_cross_xcd")) return g_pair_hold >> 16;
   if (!strcmp(name, "decode_force_recompute")) return g_decode_force_recompute;
   if (!strcmp(name, "decode_max_spins")) return g_decode_max_spins;
   if (!strcmp(name, "device_cus")) return device_topology().cus;    // read-only: the current device's

@@ -134,8 +134,9 @@ hipError_t launch_pair_tile(int id, const ProblemArgs& p, const WeightArgs& w, c
                             void* workspace, int max_spins, hipStream_t stream);
 size_t pair_tile_workspace_bytes(int id, int64_t M, int n_tiles);
 inline bool is_pair_variant(int id) { return id == 24 || id == 25; }
-// (tests) side 1 of every pair waits this many ~4 us intervals before it publishes,
-// which sends side 0 down the hand-over path once its bounded wait runs out.
+// (tests) bits 0-15: side 1 of every pair waits this many ~4 us intervals before it
+// publishes, which sends side 0 down the hand-over path once its bounded wait runs
+// out; bit 16: the sides take adjacent workgroup ids (different XCDs).
 extern int g_pair_hold;
 // int4-weight (W4A16) variant of the pipelined kernel, ids 30-33.
 hipError_t launch_tile_dma_w4(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,

@@ -400,6 +400,8 @@ struct PairX {
   int max_spins;    // polls of the pair word before a side hands its half over
   int hold;         // (tests) side 1 sleeps this many ~4 us intervals before publishing,
                     // so that side 0's bounded wait runs out and it hands its half over
+  int cross;        // (tests) the sides of a pair take adjacent workgroup ids, which the
+                    // round-robin dispatch places on different XCDs
 };
 
 // Epilogue of a pair tile: the NH whole heads as tile_epilogue, then this side's
@@ -653,7 +655,7 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m, PairX 
   // an XCD and a round of the grid; the grouping runs over pairs)
   const int n_mt = int((p.M + BM - 1) / BM);
   const int n_ht = XC ? p.n_tiles / (2 * NH + 1) : p.n_tiles / NH;
-  const int tile0 = xcd_tile_id(blockIdx.x, gridDim.x, p.xcds);
+  const int tile0 = (XC && px.cross) ? int(blockIdx.x) : xcd_tile_id(blockIdx.x, gridDim.x, p.xcds);
   const int side = XC ? (tile0 & 1) : 0;
   const int tile = XC ? (tile0 >> 1) : tile0;
   const int per_group = group_m * n_ht;
@@ -1492,7 +1494,8 @@ hipError_t launch_pair(const ProblemArgs& p, const WeightArgs& w, const Epilogue
   px.sumsq = reinterpret_cast<float*>(ws + kDecodeCounterBytes);
   px.handoff = px.sumsq + size_t(pairs) * 2 * BM;
   px.max_spins = max_spins < 0 ? 0 : max_spins;
-  px.hold = g_pair_hold;
+  px.hold = g_pair_hold & 0xFFFF;
+  px.cross = g_pair_hold >> 16;
   hipLaunchKernelGGL((tile_dma_kernel<BM, NH, WM, WN, NS, SBK, 64>), dim3(unsigned(pairs * 2)), dim3(S::kThreads), dyn,
                      stream, p, w, e, group_m < 1 ? 1 : group_m, px);
   return hipGetLastError();

@@ -164,6 +164,22 @@ def test_pair_tiles_graph_replay(device):
             mqk.set_option(k, v)
 
 
+@pytest.mark.parametrize("variant,Hq,Hkv,whole", PAIRS)
+def test_pair_tiles_across_xcds(variant, Hq, Hkv, whole, device):
+    """The two sides of every pair on different XCDs (adjacent workgroup ids), in
+    the normal exchange and through the hand-over path: the device-coherent
+    exchange gives the same bits as the whole-head tiles."""
+    import mqk
+    case = Case(1, 512, 1024, Hq, Hkv, seed=4800 + variant)
+    args = case.args(device)
+    ref = _run(lambda: mqk.fused_qkv_rope(*args), prefill_tile=whole)
+    out = _run(lambda: mqk.fused_qkv_rope(*args), prefill_tile=variant, pair_cross_xcd=1)
+    _same(out, ref, f"variant {variant} across XCDs")
+    out = _run(lambda: mqk.fused_qkv_rope(*args), prefill_tile=variant, pair_cross_xcd=1, pair_max_spins=0,
+               pair_hold=25)
+    _same(out, ref, f"variant {variant} across XCDs (hand-over)")
+
+
 def test_pair_tiles_on_many_streams(device):
     """The exchange uses device-coherent accesses, so a pair whose sides land on
     different XCDs (whatever the hardware queue's starting XCD) still agrees."""
