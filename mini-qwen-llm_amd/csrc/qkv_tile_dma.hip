@@ -3,8 +3,9 @@
 //
 // A workgroup computes a BM x (NH*128) tile of  x[M,K] @ W^T  (NH whole heads;
 // the Q/K/V weight matrices are addressed directly).  K is consumed in SBK-wide
-// (32 or 64) stages held in an NS-deep LDS ring that is filled with global_load_lds_dwordx4
-// (L2 -> LDS without VGPRs): while stage k is multiplied, the loads of stages
+// (32 or 64) stages held in an NS-deep LDS ring that is filled with direct loads
+// (buffer_load_dwordx4 ... lds in this kernel, global_load_lds_dwordx4 in the int4
+// and split-K kernels; L2 -> LDS without VGPRs): while stage k is multiplied, the loads of stages
 // k+1 .. k+NS-1 are in flight, which hides the L2 latency that a single
 // register-staged prefetch could not.  One barrier per stage: after it, every
 // wave's loads for stage k have landed (each wave first waits for its own with
@@ -646,7 +647,7 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m, PairX 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = XC ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;  // (uniform: fewer VGPRs in pair tiles)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // (uniform: load bases and LDS offsets in SGPRs)
   const int wm = wave % WM;
   const int wn = wave / WM;
 
@@ -695,18 +696,25 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m, PairX 
   const int64_t K = p.K;
 
   // ---- this lane's sources: load instruction i of a stage fills staged rows
-  // [R*(wave + i*W), +R), R = rows per load; lane -> row +lane/chunks, slot lane%chunks
-  const uint16_t* src[S::kLoadsPerWave];
+  // [R*(wave + i*W), +R), R = rows per load; lane -> row +lane/chunks, slot lane%chunks.
+  // The loads go through buffer resources based at the tile's first x row and, per
+  // projection, at the tile's first weight row of it, so the per-lane offsets stay
+  // small (at most the tile's rows x K x 2 bytes); loads i < kALoads fill x rows,
+  // the others weight rows of one projection each (proj_of[i], wave-uniform).
+  // The tile's first head of each projection (its weight rows start there).
+  uint32_t voff[S::kLoadsPerWave];
+  const uint16_t* lbase[S::kLoadsPerWave];  // the load's base (x: the tile's first row; weights: the head's)
   uint32_t dst_off[S::kLoadsPerWave];
 #pragma unroll
   for (int i = 0; i < S::kLoadsPerWave; ++i) {
     const int row0 = S::kRowsPerLoad * (wave + i * S::kWaves);
     const int row = row0 + lane / S::kChunks;
     const int chunk = stage_slot<SBK>(row, lane % S::kChunks);  // global chunk stored in slot lane % chunks
-    if (row < BM) {
+    if (i < S::kALoads) {
       int64_t grow = m0 + row;
       grow = grow < p.M ? grow : p.M - 1;  // rows past M re-read the last row; never stored
-      src[i] = p.x + grow * K + chunk * 8;
+      lbase[i] = p.x + m0 * K;
+      voff[i] = uint32_t(((grow - m0) * K + chunk * 8) * 2);
     } else {
       const int brow = row - BM;
       int proj, hh, head = head0 + brow / kHeadDim, dim = brow % kHeadDim;
@@ -718,10 +726,17 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m, PairX 
       split_head(head, e.Hq, e.Hkv, proj, hh);
       int64_t col = int64_t(hh) * kHeadDim + dim;
       col = col < w.n_cols[proj] ? col : w.n_cols[proj] - 1;
-      src[i] = w.w[proj] + col * K + chunk * 8;
+      // (one head's rows per load: its base, the head's first row, is wave-uniform)
+      const uint16_t* hb = pick3<const uint16_t>(proj, w.w[0], w.w[1], w.w[2]) + int64_t(hh) * kHeadDim * K;
+      lbase[i] = hb;
+      voff[i] = uint32_t(((col - int64_t(hh) * kHeadDim) * K + chunk * 8) * 2);
     }
     dst_off[i] = uint32_t(row0 * kRowBytes);
   }
+  // the loads' resources, built once (wave-uniform bases)
+  i32x4_t rsrc[S::kLoadsPerWave];
+#pragma unroll
+  for (int i = 0; i < S::kLoadsPerWave; ++i) rsrc[i] = raw_buffer_rsrc(lbase[i]);
   // input RMSNorm: scale of the x row and k offset of the chunk each of this
   // lane's x loads brings in (load i < kALoads, row0 + lane / chunks, slot lane % chunks)
   const bool in_norm = p.in_gamma != nullptr;
@@ -741,10 +756,9 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m, PairX 
   }
   auto issue = [&](int kt) {
     const uint32_t base = lds0 + uint32_t((kt % NS) * S::kStageBytes);
+    const uint32_t koff = uint32_t(kt) * (SBK * 2);
 #pragma unroll
-    for (int i = 0; i < S::kLoadsPerWave; ++i) {
-      dma16(src[i] + int64_t(kt) * SBK, base + dst_off[i]);
-    }
+    for (int i = 0; i < S::kLoadsPerWave; ++i) bdma16(rsrc[i], voff[i], koff, base + dst_off[i]);
   };
 
   // ---- main loop -------------------------------------------------------------------
