@@ -135,7 +135,8 @@ int mqk_fused_qkv_rope_f16(const mqk_f16* x, const mqk_f16* w_q, const mqk_f16* 
 
 /* Workspace bytes needed by mqk_fused_qkv_rope_bf16 / _w4a16 for these sizes
  * (0 when the chosen kernels need none; pair tiles need 66 KiB per pair of
- * workgroups, e.g. 16.9 MB for BASELINE config 4).  Hq and Hkv are counted in 128-column
+ * 256-row workgroups, e.g. 16.9 MB for BASELINE config 4, 33 KiB per pair of
+ * 128-row ones, e.g. 4.3 MB for Qwen3-8B at T = 1024).  Hq and Hkv are counted in 128-column
  * blocks: the head counts for D == 128, Hq / 2 and Hkv / 2 for D == 64.  The
  * same holds for mqk_fused_qkv_rope_ex_workspace_size. */
 size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden);
@@ -368,10 +369,12 @@ int mqk_fused_qkv_rope_ex_w4a16(const mqk_bf16* x, const int32_t* qw_q, const vo
  *                    split-K tile launch; 0: never
  *   "pair_tiles"     1 (default): bf16 calls with head_dim 128 may run as pair tiles (two
  *                    256-row workgroups per 3 heads, 256 x 192 each, variant 24, or per 5
- *                    heads, 256 x 320 each, variant 25, sharing one head whose RMSNorm sums
- *                    they exchange through the workspace) where the tile chooser prefers
- *                    them (e.g. 512 tiles in two rounds instead of 640
- *                    of 256 x 256); 0: never
+ *                    heads, 256 x 320 each, variant 25; 128-row forms 26 and 27; the two
+ *                    share one head whose RMSNorm sums they exchange through the
+ *                    workspace) where the planner prefers them (e.g. BASELINE config 4:
+ *                    512 tiles in two rounds instead of 640 of 256 x 256; Qwen3-8B at
+ *                    T = 768 .. 1024: one round of 128-row pairs instead of split-K
+ *                    tiles); 0: never
  *   "pair_max_spins" polls (~1 us apart) a pair tile makes for its partner's sums before it
  *                    hands its half of the shared head over (default 16384; for tests)
  *   "pair_hold"      (tests) side 1 of every pair waits this many ~4 us intervals before

@@ -271,23 +271,48 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
       else head_us = one64 ? 2.0 + 0.5 * stages : 2.5 + stages * (0.6 + 0.0002 * double(t128));
     }
   }
+  // One round of 128-row pair tiles (26: 2 x 128 x 192 per 3 heads, 27: 2 x 128 x 320
+  // per 5 heads) over more than half of the CUs, which no whole-head shape fills at
+  // these T.  Fitted on MI355X
+  // (hidden 2560 / 4096, 48 heads, T = 576 .. 1024, within ~2 us):
+  //   26: 15 us + (0.465 + 0.001 * workgroups) us per 64-k stage;
+  //   27 (hidden 2048 / 5120, 40 / 80 heads): ~5 us + 1.4 us per stage.
+  const TileVariant* pv = nullptr;
+  double pair_us = 1e30;
+  if (allow_pair && M > 64 && g_prefill_tile.load() == 0) {
+    const int id = n_tiles % 3 == 0 ? 26 : (n_tiles % 5 == 0 ? 27 : 0);
+    for (int i = 0; id != 0 && i < tile_variant_count(); ++i)
+      if (tile_variant(i)->id == id) pv = tile_variant(i);
+    const int64_t wgs = pv ? tile_count(*pv, M, n_tiles) : 0;
+    if (pv && 2 * wgs > cus && wgs <= cus && wgs / 2 <= kSplitMaxTiles && !(in_norm && tile_dma_lds_bytes(id) + K * 2 > 160 * 1024)) {
+      const double stages = double(K / 64);
+      pair_us = id == 26 ? 15.0 + stages * (0.465 + 0.001 * double(wgs)) : 5.0 + 1.4 * stages;
+    } else {
+      pv = nullptr;
+    }
+  }
   const bool blocks_ok = allow_blocks && aligned && M > 64 && g_prefill_tile.load() == 0 &&
                          g_decode_max_t.load() >= 64 && nblk <= g_decode_blocks.load() && blk_splits > 0;
   const bool forced_split = ksplit > 0 && g_tile_ksplit.load() >= 2;
   if (blocks_ok && !forced_split &&
-      (!g_decode_cost_model.load() || (blocks_us <= tile_us && blocks_us <= split_us && blocks_us <= head_us))) {
+      (!g_decode_cost_model.load() ||
+       (blocks_us <= tile_us && blocks_us <= split_us && blocks_us <= head_us && blocks_us <= pair_us))) {
     pl.splits = blk_splits;
     pl.tail = M;
     pl.passes = int(std::min<int64_t>(per_launch, nblk));
     return pl;
   }
-  if (ksplit > 0 && (forced_split || (split_us < tile_us && split_us <= head_us))) {
+  if (ksplit > 0 && (forced_split || (split_us < tile_us && split_us <= head_us && split_us <= pair_us))) {
     pl.v = sv;
     pl.ksplit = ksplit;
     return pl;
   }
-  if (hv && head_us < tile_us) {
+  if (hv && head_us < tile_us && head_us <= pair_us) {
     pl.v = hv;
+    return pl;
+  }
+  if (pv && pair_us < tile_us) {
+    pl.v = pv;
     return pl;
   }
   pl.v = choose_tile_variant(int(g_prefill_tile.load()), M, n_tiles, int4, topo.cus, allow_pair);

@@ -425,6 +425,8 @@ const TileVariant kVariants[] = {
     {23, 128, 2, 0, 512},
     {24, 256, 3, 0, 512},  // pair tiles: hpt = heads per pair of workgroups (256 x 192 each)
     {25, 256, 5, 0, 512},  // (256 x 320 each)
+    {26, 128, 3, 0, 512},  // (128 x 192 each)
+    {27, 128, 5, 0, 512},  // (128 x 320 each)
     {30, 128, 3, 0, 512},
     {31, 256, 2, 0, 512},
     {32, 128, 2, 0, 256},
@@ -482,9 +484,13 @@ const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles,
   // need the workspace and head_dim 128 (allow_pair).  Measured on MI355X: 24 no
   // faster than 16 at Qwen3-8B prefill (104.6-104.9 us against 104.5-105.6), so it
   // ranks just below it; 25 takes BASELINE config 4's 512 tiles in two rounds in
-  // 170.5-171.7 us against 188.5-189.0 for variant 18's 640 tiles)
+  // 170.5-171.7 us against 188.5-189.0 for variant 18's 640 tiles; the 128-row pairs
+  // 26 (3 stages of 64 k) and 27 (2 stages) fill one round where the whole-head
+  // tiles cannot: e.g. hidden 2560 (48 heads) T = 896 41.7 us against 48.5 for 23,
+  // hidden 2048 (40 heads) T = 2048 49.5 against 58.0 for 18)
   static const Cand bf16_cands[] = {{16, 1.00f}, {18, 1.27f}, {17, 1.26f}, {11, 0.94f}, {10, 1.19f},
-                                    {23, 0.90f}, {13, 0.75f}, {12, 0.75f}, {25, 1.33f}, {24, 0.99f}};
+                                    {23, 0.90f}, {13, 0.75f}, {12, 0.75f}, {25, 1.33f}, {24, 0.99f},
+                                    {26, 0.82f}, {27, 0.87f}};
   // (33 is 31 with waves of 256 x 32, so every int4 weight is dequantised once per
   // workgroup instead of twice: 419 us against 447 us on the W4A16 ragged batch)
   static const Cand int4_cands[] = {{33, 1.07f}, {31, 1.00f}, {30, 0.75f}, {32, 0.54f}};
@@ -497,6 +503,7 @@ const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles,
     const TileVariant* v = find_variant(cands[i].id);
     if (!v || n_tiles % v->hpt != 0 || !supports(*v, int4) || (is_pair_variant(v->id) && !pair_fits(*v))) continue;
     const int64_t tiles = tile_count(*v, M, n_tiles);
+    if (v->bm == 128 && is_pair_variant(v->id) && 2 * tiles <= cus) continue;  // (measured from half a round up)
     const int64_t rounds = (tiles + cus - 1) / cus;
     const float util = float(tiles) / float(rounds * cus);
     // rows past M in the last row tile are wasted work

@@ -99,6 +99,17 @@ def no_head_tiles():
     _native.set_option("head_tiles", 1)
 
 
+@pytest.fixture
+def no_pair_tiles():
+    """Plan without pair tiles (their 128-row form takes some mid token counts
+    that the split-K launch runs otherwise), so a test of another launch keeps
+    the call on the path it is about."""
+    from mqk import _native
+    _native.set_option("pair_tiles", 0)
+    yield
+    _native.set_option("pair_tiles", 1)
+
+
 # Short names of the library's kernels, by (demangled or mangled) kernel name.
 _KERNEL_NAMES = (("decode_multi_kernel", "decode_multi"), ("decode_long_kernel", "decode"), ("decode_kernel", "decode"),
                  ("tile_dma_w4_kernel", "tile_w4"), ("tile_dma_split_kernel", "tile_split"), ("tile_dma_kernel", "tile"), ("tile_kernel", "tile_reg"),

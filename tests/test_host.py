@@ -121,7 +121,10 @@ def test_head_tile_plan(lib):
     128 x 128 tiles fit one round over the CUs takes that launch and needs no
     workspace: T = 256 and 512 at Qwen3-8B dims (48 heads: 192 tiles), and
     hidden 2048 at T = 768 (40 heads, 6 x 40 = 240 tiles of 128 x 128).  At
-    T = 1024 (8 x 48 = 384 tiles) the split-K launch keeps the call."""
+    T = 1024 (8 x 48 = 384 single-head tiles, two rounds) one round of 128-row
+    pair tiles takes the call (8 x 16 pairs of 2 x 128 x 192): the counters, then
+    per pair 2 x 128 floats of row sums of squares and a 128 x 64 float hand-over
+    area.  With pair tiles off, the split-K launch keeps it."""
     from mqk import _native
     if _native.get_option("device_cus") != 256:
         pytest.skip("the plan depends on the device's CU count (256 on MI355X)")
@@ -132,9 +135,12 @@ def test_head_tile_plan(lib):
         assert lib.mqk_fused_qkv_rope_workspace_size(256, 32, 8, 4096) == 0
         assert lib.mqk_fused_qkv_rope_workspace_size(512, 32, 8, 4096) == 0
         assert lib.mqk_fused_qkv_rope_workspace_size(768, 32, 4, 2048) == 0
+        assert lib.mqk_fused_qkv_rope_workspace_size(1024, 32, 8, 4096) == C + 128 * (2 * 128 + 128 * 64) * 4
+        _native.set_option("pair_tiles", 0)
         assert lib.mqk_fused_qkv_rope_workspace_size(1024, 32, 8, 4096) == C + 128 * 2 * part
     finally:
         _native.set_option("decode_blocks", 16)
+        _native.set_option("pair_tiles", 1)
 
 
 @pytest.mark.usefixtures("no_head_tiles")
@@ -195,6 +201,7 @@ def test_workspace_size(lib):
 
 
 @pytest.mark.usefixtures("no_head_tiles")
+@pytest.mark.usefixtures("no_pair_tiles")
 def test_split_tile_plan(lib):
     """The planner's split-K tile model at Qwen3-8B dims (bf16 needs the split
     workspace; int4 keeps its decode blocks, so the size is the larger need):
@@ -207,11 +214,7 @@ def test_split_tile_plan(lib):
     try:
         assert lib.mqk_fused_qkv_rope_workspace_size(512, 32, 8, 4096) == C + 64 * 4 * part
         assert lib.mqk_fused_qkv_rope_workspace_size(1024, 32, 8, 4096) == C + 128 * 2 * part
-        _native.set_option("pair_tiles", 0)
-        try:
-            assert lib.mqk_fused_qkv_rope_workspace_size(2048, 32, 8, 4096) == 0  # 256 tiles: one each
-        finally:
-            _native.set_option("pair_tiles", 1)
+        assert lib.mqk_fused_qkv_rope_workspace_size(2048, 32, 8, 4096) == 0  # 256 tiles: one each
         _native.set_option("tile_ksplit", 0)
         try:
             assert lib.mqk_fused_qkv_rope_workspace_size(512, 32, 8, 4096) == 0

@@ -1,7 +1,8 @@
-"""Pair tiles (variants 24 and 25): two workgroups share one head.
+"""Pair tiles (variants 24-27): two workgroups share one head.
 
-A pair of 256-row workgroups covers 2 * hpt + 1 heads (3 for variant 24, 256 x 192
-each; 5 for variant 25, 256 x 320 each).  Each side holds hpt whole heads and half
+A pair of 256-row (24, 25) or 128-row (26, 27) workgroups covers 2 * hpt + 1 heads
+(3 for variants 24 and 26, 256 x 192 / 128 x 192 each; 5 for variants 25 and 27,
+256 x 320 / 128 x 320 each).  Each side holds hpt whole heads and half
 of the head they share: head dims 32*side + [0, 32) and + [64, 96), so every RoPE
 pair (d, d + 64) stays on one side.  The shared head's RMSNorm needs both halves'
 sums of squares, which the sides exchange through the workspace (a side whose
@@ -14,7 +15,8 @@ tile, so the outputs must equal variant 16's / 18's bit for bit -- through both
 exchange paths, with RoPE positions, varlen offsets, the input RMSNorm and the
 paged-cache write, under graph replay and on many streams.  The oracle bar of
 test_fused_qkv_rope_gpu.py (max-abs 2e-2, rel-L2 1e-2) is checked at BASELINE
-config 4's dims, where the planner takes variant 25.
+config 4's dims, where the planner takes variant 25, and at the mid token counts
+where it takes the 128-row pairs.
 """
 from __future__ import annotations
 
@@ -33,7 +35,7 @@ REL_L2 = 1e-2
 # 3 and as 128 x 384; 40 heads as pairs of 5 and as 256 x 256.  The shared heads
 # are Q, K and V heads in both (48: 1, 4, .., 34, 37 (K), 40, 43, 46 (V);
 # 40: 2, 7, .., 27, 32 (K), 37 (V)).
-PAIRS = [(24, 32, 8, 16), (25, 32, 4, 18)]
+PAIRS = [(24, 32, 8, 16), (25, 32, 4, 18), (26, 32, 8, 16), (27, 32, 4, 18)]
 
 
 def _opts(**kv):
@@ -240,3 +242,32 @@ def test_pair_tiles_not_taken_without_workspace_room_or_for_head_dim_64(device):
     finally:
         for k, v in old.items():
             mqk.set_option(k, v)
+
+
+@pytest.mark.parametrize("T,hidden,Hq,Hkv,variant,whole", [(1024, 4096, 32, 8, 26, 16), (768, 2560, 32, 8, 26, 16),
+                                                          (2048, 2048, 32, 4, 27, 18)])
+def test_mid_t_takes_128_row_pairs_and_meets_the_oracle(T, hidden, Hq, Hkv, variant, whole, device):
+    """One round of 128-row pair tiles where no whole-head shape fills the CUs:
+    Qwen3-8B at T = 1024 (8 x 16 pairs of 2 x 128 x 192, where the split-K launch
+    ran before), Qwen3-4B dims at T = 768 (6 x 16 pairs) and Qwen3-30B-A3B
+    attention dims at T = 2048 (16 x 8 pairs of 2 x 128 x 320).  The planner's one
+    launch is the pair kernel; sampled tokens against the oracle at the acceptance
+    bar, every token against the whole-head tiles bit for bit."""
+    import mqk
+    from oracle import qkv_rope_oracle as orc
+    case = Case(1, T, hidden, Hq, Hkv, seed=4900 + T)
+    args = case.args(device)
+    assert launched_kernels(lambda: mqk.fused_qkv_rope(*args)) == ["tile_pair"]
+    got = mqk.fused_qkv_rope(*args)
+    torch.cuda.synchronize()
+    idx = np.sort(np.random.default_rng(T).choice(T, 64, replace=False))
+    ref = case.oracle(token_idx=idx)
+    for name, o, r in zip("qkv", got, ref):
+        o = f32(o).reshape(T, -1, D)[idx].reshape(r.shape)
+        assert np.isfinite(o).all()
+        assert orc.max_abs(o, r) <= MAX_ABS, name
+        assert orc.rel_l2(o, r) <= REL_L2, name
+    forced = _run(lambda: mqk.fused_qkv_rope(*args), prefill_tile=variant)
+    _same(got, forced, f"planner against variant {variant}")
+    whole_out = _run(lambda: mqk.fused_qkv_rope(*args), prefill_tile=whole)
+    _same(got, whole_out, f"T = {T}, hidden {hidden}")
