@@ -369,7 +369,8 @@ int mqk_fused_qkv_rope_ex_w4a16(const mqk_bf16* x, const int32_t* qw_q, const vo
  *                    split-K tile launch; 0: never
  *   "pair_tiles"     1 (default): bf16 calls with head_dim 128 may run as pair tiles (two
  *                    256-row workgroups per 3 heads, 256 x 192 each, variant 24, or per 5
- *                    heads, 256 x 320 each, variant 25; 128-row forms 26 and 27; the two
+ *                    heads, 256 x 320 each, variant 25; 128-row forms 26 and 27, a 192-row
+ *                    form 28; the two
  *                    share one head whose RMSNorm sums they exchange through the
  *                    workspace) where the planner prefers them (e.g. BASELINE config 4:
  *                    512 tiles in two rounds instead of 640 of 256 x 256; Qwen3-8B at

@@ -122,9 +122,9 @@ hipError_t launch_tile_dma(int id, const ProblemArgs& p, const WeightArgs& w, co
 hipError_t launch_tile_dma_split(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e,
                                  int ksplit, int force_recompute, int max_spins, void* workspace, hipStream_t stream);
 size_t tile_split_part_bytes(int id, int64_t M, int n_tiles, int ksplit);
-// Pair tiles (ids 24: 256 x 192, 25: 256 x 320, 26: 128 x 192, 27: 128 x 320; bf16
-// weights, head_dim 128): two workgroups cover 2 * hpt + 1 heads of BM = 256 or 128
-// rows (hpt = 1 or 2 whole heads each, and half of the head they share).  The sides
+// Pair tiles (ids 24: 256 x 192, 25: 256 x 320, 26: 128 x 192, 27: 128 x 320,
+// 28: 192 x 192; bf16 weights, head_dim 128): two workgroups cover 2 * hpt + 1 heads
+// of BM = 256, 128 or 192 rows (hpt = 1 or 2 whole heads each, and half of the head they share).  The sides
 // exchange the shared head's row sums of squares through the workspace:
 // kDecodeCounterBytes of counters (the pair words reuse the split-K tile lines, zero
 // between launches), then per pair 2 * BM floats of sums and a BM x 64 float
@@ -134,7 +134,7 @@ size_t tile_split_part_bytes(int id, int64_t M, int n_tiles, int ksplit);
 hipError_t launch_pair_tile(int id, const ProblemArgs& p, const WeightArgs& w, const EpilogueArgs& e, int group_m,
                             void* workspace, int max_spins, hipStream_t stream);
 size_t pair_tile_workspace_bytes(int id, int64_t M, int n_tiles);
-inline bool is_pair_variant(int id) { return id >= 24 && id <= 27; }
+inline bool is_pair_variant(int id) { return id >= 24 && id <= 28; }
 // (tests) bits 0-15: side 1 of every pair waits this many ~4 us intervals before it
 // publishes, which sends side 0 down the hand-over path once its bounded wait runs
 // out; bit 16: the sides take adjacent workgroup ids (different XCDs).

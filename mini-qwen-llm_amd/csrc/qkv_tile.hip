@@ -427,6 +427,7 @@ const TileVariant kVariants[] = {
     {25, 256, 5, 0, 512},  // (256 x 320 each)
     {26, 128, 3, 0, 512},  // (128 x 192 each)
     {27, 128, 5, 0, 512},  // (128 x 320 each)
+    {28, 192, 3, 0, 384},  // (192 x 192 each)
     {30, 128, 3, 0, 512},
     {31, 256, 2, 0, 512},
     {32, 128, 2, 0, 256},
@@ -487,10 +488,13 @@ const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles,
   // 170.5-171.7 us against 188.5-189.0 for variant 18's 640 tiles; the 128-row pairs
   // 26 (3 stages of 64 k) and 27 (2 stages) fill one round where the whole-head
   // tiles cannot: e.g. hidden 2560 (48 heads) T = 896 41.7 us against 48.5 for 23,
-  // hidden 2048 (40 heads) T = 2048 49.5 against 58.0 for 18)
+  // hidden 2048 (40 heads) T = 2048 49.5 against 58.0 for 18; the 192-row pair 28
+  // (3 stages) where it fills nearly one round: hidden 4096 T = 1536 86 against 100
+  // for 16, and 78-81 against 67-74 with 7 of 8 workgroups per CU, so it is
+  // taken only beyond that)
   static const Cand bf16_cands[] = {{16, 1.00f}, {18, 1.27f}, {17, 1.26f}, {11, 0.94f}, {10, 1.19f},
                                     {23, 0.90f}, {13, 0.75f}, {12, 0.75f}, {25, 1.33f}, {24, 0.99f},
-                                    {26, 0.82f}, {27, 0.87f}};
+                                    {26, 0.82f}, {27, 0.87f}, {28, 0.91f}};
   // (33 is 31 with waves of 256 x 32, so every int4 weight is dequantised once per
   // workgroup instead of twice: 419 us against 447 us on the W4A16 ragged batch)
   static const Cand int4_cands[] = {{33, 1.07f}, {31, 1.00f}, {30, 0.75f}, {32, 0.54f}};
@@ -504,6 +508,7 @@ const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles,
     if (!v || n_tiles % v->hpt != 0 || !supports(*v, int4) || (is_pair_variant(v->id) && !pair_fits(*v))) continue;
     const int64_t tiles = tile_count(*v, M, n_tiles);
     if (v->bm == 128 && is_pair_variant(v->id) && 2 * tiles <= cus) continue;  // (measured from half a round up)
+    if (v->bm == 192 && (8 * tiles <= 7 * cus || tiles > cus)) continue;       // (and 28 in most of one round)
     const int64_t rounds = (tiles + cus - 1) / cus;
     const float util = float(tiles) / float(rounds * cus);
     // rows past M in the last row tile are wasted work

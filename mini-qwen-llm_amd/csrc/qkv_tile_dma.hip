@@ -1560,6 +1560,7 @@ hipError_t launch_pair_tile(int id, const ProblemArgs& p, const WeightArgs& w, c
     case 25: return launch_pair<256, 2, 4, 2, 2, 64>(p, w, e, group_m, workspace, max_spins, stream);  // 256x320
     case 26: return launch_pair<128, 1, 4, 2, 3, 64>(p, w, e, group_m, workspace, max_spins, stream);  // 128x192
     case 27: return launch_pair<128, 2, 4, 2, 2, 64>(p, w, e, group_m, workspace, max_spins, stream);  // 128x320
+    case 28: return launch_pair<192, 1, 3, 2, 3, 64>(p, w, e, group_m, workspace, max_spins, stream);  // 192x192
     default: return hipErrorInvalidValue;
   }
 }
@@ -1570,6 +1571,7 @@ size_t pair_tile_workspace_bytes(int id, int64_t M, int n_tiles) {
     case 25: return pair_bytes<256, 2, 4, 2, 2, 64>(M, n_tiles);
     case 26: return pair_bytes<128, 1, 4, 2, 3, 64>(M, n_tiles);
     case 27: return pair_bytes<128, 2, 4, 2, 2, 64>(M, n_tiles);
+    case 28: return pair_bytes<192, 1, 3, 2, 3, 64>(M, n_tiles);
     default: return 0;
   }
 }
@@ -1580,6 +1582,7 @@ int tile_dma_lds_bytes(int id) {
     case 25: return DmaShape<256, 2, 4, 2, 2, 64, 64>::kLdsBytes;
     case 26: return DmaShape<128, 1, 4, 2, 3, 64, 64>::kLdsBytes;
     case 27: return DmaShape<128, 2, 4, 2, 2, 64, 64>::kLdsBytes;
+    case 28: return DmaShape<192, 1, 3, 2, 3, 64, 64>::kLdsBytes;
     case 10: return DmaShape<256, 2, 4, 2, 4, 32>::kLdsBytes;
     case 11: return DmaShape<128, 3, 2, 4, 4, 32>::kLdsBytes;
     case 12: return DmaShape<256, 1, 4, 1, 4, 32>::kLdsBytes;

@@ -54,12 +54,14 @@ def test_mid_t_decode_block_launches(T, plan, device):
 
 @pytest.mark.parametrize("T,plan", [(128, ["decode_multi"]), (192, ["decode_multi"]), (256, ["tile_head"]),
                                     (512, ["tile_head"]), (640, ["tile_head"]), (768, ["tile_pair"]),
-                                    (1024, ["tile_pair"]), (1152, ["tile"]), (2048, ["tile"])])
+                                    (1024, ["tile_pair"]), (1152, ["tile"]), (1536, ["tile_pair"]),
+                                    (2048, ["tile"])])
 def test_default_plan_by_token_count(T, plan, device):
     """The default planner at hidden 4096 (bf16): decode blocks for a few 64-row
     blocks, one round of single-head tiles from about 200 tokens while those fit
-    the CUs, one round of 128-row pair tiles beyond, one tile per workgroup once
-    the tiles fill the CUs."""
+    the CUs, one round of 128-row pair tiles beyond, whole-head tiles, then nearly
+    a round of 192-row pair tiles, one tile per workgroup once the tiles fill the
+    CUs."""
     case = Case(1, T, HID, HQ, HKV, seed=15 + T)
     assert launched_kernels(_bf16_call(case, device)) == plan
 

@@ -1,8 +1,8 @@
-"""Pair tiles (variants 24-27): two workgroups share one head.
+"""Pair tiles (variants 24-28): two workgroups share one head.
 
-A pair of 256-row (24, 25) or 128-row (26, 27) workgroups covers 2 * hpt + 1 heads
-(3 for variants 24 and 26, 256 x 192 / 128 x 192 each; 5 for variants 25 and 27,
-256 x 320 / 128 x 320 each).  Each side holds hpt whole heads and half
+A pair of 256-row (24, 25), 128-row (26, 27) or 192-row (28) workgroups covers
+2 * hpt + 1 heads (3 for variants 24, 26 and 28, 256 x 192 / 128 x 192 / 192 x 192
+each; 5 for variants 25 and 27, 256 x 320 / 128 x 320 each).  Each side holds hpt whole heads and half
 of the head they share: head dims 32*side + [0, 32) and + [64, 96), so every RoPE
 pair (d, d + 64) stays on one side.  The shared head's RMSNorm needs both halves'
 sums of squares, which the sides exchange through the workspace (a side whose
@@ -35,7 +35,7 @@ REL_L2 = 1e-2
 # 3 and as 128 x 384; 40 heads as pairs of 5 and as 256 x 256.  The shared heads
 # are Q, K and V heads in both (48: 1, 4, .., 34, 37 (K), 40, 43, 46 (V);
 # 40: 2, 7, .., 27, 32 (K), 37 (V)).
-PAIRS = [(24, 32, 8, 16), (25, 32, 4, 18), (26, 32, 8, 16), (27, 32, 4, 18)]
+PAIRS = [(24, 32, 8, 16), (25, 32, 4, 18), (26, 32, 8, 16), (27, 32, 4, 18), (28, 32, 8, 16)]
 
 
 def _opts(**kv):
@@ -245,14 +245,17 @@ def test_pair_tiles_not_taken_without_workspace_room_or_for_head_dim_64(device):
 
 
 @pytest.mark.parametrize("T,hidden,Hq,Hkv,variant,whole", [(1024, 4096, 32, 8, 26, 16), (768, 2560, 32, 8, 26, 16),
-                                                          (2048, 2048, 32, 4, 27, 18)])
-def test_mid_t_takes_128_row_pairs_and_meets_the_oracle(T, hidden, Hq, Hkv, variant, whole, device):
-    """One round of 128-row pair tiles where no whole-head shape fills the CUs:
-    Qwen3-8B at T = 1024 (8 x 16 pairs of 2 x 128 x 192, where the split-K launch
-    ran before), Qwen3-4B dims at T = 768 (6 x 16 pairs) and Qwen3-30B-A3B
-    attention dims at T = 2048 (16 x 8 pairs of 2 x 128 x 320).  The planner's one
-    launch is the pair kernel; sampled tokens against the oracle at the acceptance
-    bar, every token against the whole-head tiles bit for bit."""
+                                                          (2048, 2048, 32, 4, 27, 18), (1536, 4096, 32, 8, 28, 16),
+                                                          (1400, 2560, 32, 8, 28, 16)])
+def test_mid_t_takes_pair_tiles_and_meets_the_oracle(T, hidden, Hq, Hkv, variant, whole, device):
+    """One round of pair tiles where no whole-head shape fills the CUs: Qwen3-8B
+    at T = 1024 (8 x 16 pairs of 2 x 128 x 192, where the split-K launch ran
+    before) and T = 1536 (8 x 16 pairs of 2 x 192 x 192), Qwen3-4B dims at T = 768
+    (6 x 16 pairs of 128-row tiles) and T = 1400 (8 x 16 pairs of 192-row tiles,
+    the last one partial), Qwen3-30B-A3B attention dims at T = 2048 (16 x 8 pairs
+    of 2 x 128 x 320).  The planner's one launch is the pair kernel; sampled tokens
+    against the oracle at the acceptance bar, every token against the whole-head
+    tiles bit for bit."""
     import mqk
     from oracle import qkv_rope_oracle as orc
     case = Case(1, T, hidden, Hq, Hkv, seed=4900 + T)
