@@ -390,7 +390,7 @@ def stream_read(steps, warmup, dev, copies=8, nbytes=6144 * 4096 * 2, blocks=Non
     return ms, nbytes / (ms * 1e-3) / 1e9
 
 
-WORKLOADS = ("c1f32", "c2f32", "d14b", "c2", "c3", "c4", "c5", "mid", "mid256", "mid128", "gemm", "copy", "stream")
+WORKLOADS = ("c1f32", "c2f32", "d14b", "c2", "c3", "c4", "c5", "mid", "mid1024", "mid1536", "mid256", "mid128", "gemm", "copy", "stream")
 
 
 def run_only(name, steps, warmup, dev):
@@ -413,6 +413,9 @@ def run_only(name, steps, warmup, dev):
         ms, _ = bench_w4a16(hidden, Hq, Hkv, 4, steps, warmup, dev)
     elif name == "mid":  # a 512-token call (random positions): one round of 128 x 128 single-head tiles
         ms, _ = bench_decode(512, hidden, Hq, Hkv, 2, steps, warmup, dev)
+    elif name in ("mid1024", "mid1536"):  # one sequence of 1024 / 1536 tokens: one round of pair tiles
+        sl = int(name[3:])
+        ms, _ = bench_prefill(sl, 1, sl, hidden, Hq, Hkv, 5, steps, warmup, dev)
     elif name == "mid256":  # a 256-token call: one round of 64 x 128 single-head tiles
         ms, _ = bench_decode(256, hidden, Hq, Hkv, 2, steps, warmup, dev)
     elif name == "mid128":  # a 128-token call: one decode launch covering two 64-row blocks
@@ -553,6 +556,15 @@ def main(argv=None) -> int:
                                        "ms_per_step": round(msm, 6), "bound": "mfma", "achieved_TFLOPs": round(am, 2),
                                        "frac": round(am / PEAK_BF16_TFLOPS, 4)}
         log(f"[bench] B=1 x S=512: {msm * 1e3:.1f} us/step, {am:.0f} TFLOP/s")
+        # longer single-sequence prefills at Qwen3-8B shapes: one round of pair tiles
+        # (2 x 128 x 192 per 3 heads at S=1024, 2 x 192 x 192 at S=1536)
+        for sl in (1024, 1536):
+            msl, _ = bench_prefill(sl, 1, sl, hidden, Hq, Hkv, 5, max(100, args.steps), 200, dev)
+            al = flops(sl, hidden, N) / (msl * 1e-3) / 1e12
+            sec[f"mid_qwen3_8b_b1_s{sl}"] = {"tokens_per_s": round(sl / (msl * 1e-3), 1),
+                                             "ms_per_step": round(msl, 6), "bound": "mfma",
+                                             "achieved_TFLOPs": round(al, 2), "frac": round(al / PEAK_BF16_TFLOPS, 4)}
+            log(f"[bench] B=1 x S={sl}: {msl * 1e3:.1f} us/step, {al:.0f} TFLOP/s")
         # config 5: W4A16 ragged continuous batch
         ms5, T5 = bench_w4a16(hidden, Hq, Hkv, 4, 100, 100, dev)
         a5 = flops(T5, hidden, N) / (ms5 * 1e-3) / 1e12
