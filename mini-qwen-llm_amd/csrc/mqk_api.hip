@@ -366,8 +366,10 @@ int run_fused(int int4, ProblemArgs p, const WeightArgs& w, const EpilogueArgs& 
     pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, true, p.in_gamma != nullptr, false, pair_ok);
     base = region(pl);
   }
-  if (pl.v && is_pair_variant(pl.v->id) && !fits(base)) {
-    // a workspace sized without the pair tiles' exchange area: plan without them
+  if (pl.v && is_pair_variant(pl.v->id) &&
+      (!fits(base) || (p.in_gamma && tile_dma_lds_bytes(pl.v->id) + p.K * 2 > 160 * 1024))) {
+    // a workspace sized without the pair tiles' exchange area, or an input norm whose
+    // gamma does not fit the LDS beside their ring: plan without them
     pl = plan_fused(int4, p.M, p.K, p.n_tiles, epilogue_aligned(e), topo, true, p.in_gamma != nullptr, false, false);
     base = region(pl);
   }

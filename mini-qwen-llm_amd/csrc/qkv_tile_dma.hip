@@ -1501,7 +1501,7 @@ hipError_t launch_pair(const ProblemArgs& p, const WeightArgs& w, const Epilogue
   const int64_t pairs = (p.M + BM - 1) / BM * (p.n_tiles / (2 * NH + 1));
   if (pairs > kSplitMaxTiles) return hipErrorInvalidValue;
   const size_t dyn = p.in_gamma ? size_t(p.K) * 2 : 0;
-  if (S::kLdsBytes + dyn > 160 * 1024) return hipErrorInvalidValue;
+  if (S::kLdsBytes + 16 + dyn > 160 * 1024) return hipErrorInvalidValue;  // (+ the exchange word)
   char* ws = static_cast<char*>(workspace);
   PairX px;
   px.words = reinterpret_cast<uint32_t*>(ws + kSplitWordsOffset);
@@ -1576,13 +1576,16 @@ size_t pair_tile_workspace_bytes(int id, int64_t M, int n_tiles) {
   }
 }
 
+// (pair tiles: their epilogue's exchange word adds one 16-byte LDS allocation)
+constexpr int kPairWordLds = 16;
+
 int tile_dma_lds_bytes(int id) {
   switch (id) {
-    case 24: return DmaShape<256, 1, 4, 2, 2, 64, 64>::kLdsBytes;
-    case 25: return DmaShape<256, 2, 4, 2, 2, 64, 64>::kLdsBytes;
-    case 26: return DmaShape<128, 1, 4, 2, 3, 64, 64>::kLdsBytes;
-    case 27: return DmaShape<128, 2, 4, 2, 2, 64, 64>::kLdsBytes;
-    case 28: return DmaShape<192, 1, 3, 2, 3, 64, 64>::kLdsBytes;
+    case 24: return DmaShape<256, 1, 4, 2, 2, 64, 64>::kLdsBytes + kPairWordLds;
+    case 25: return DmaShape<256, 2, 4, 2, 2, 64, 64>::kLdsBytes + kPairWordLds;
+    case 26: return DmaShape<128, 1, 4, 2, 3, 64, 64>::kLdsBytes + kPairWordLds;
+    case 27: return DmaShape<128, 2, 4, 2, 2, 64, 64>::kLdsBytes + kPairWordLds;
+    case 28: return DmaShape<192, 1, 3, 2, 3, 64, 64>::kLdsBytes + kPairWordLds;
     case 10: return DmaShape<256, 2, 4, 2, 4, 32>::kLdsBytes;
     case 11: return DmaShape<128, 3, 2, 4, 4, 32>::kLdsBytes;
     case 12: return DmaShape<256, 1, 4, 1, 4, 32>::kLdsBytes;

@@ -162,3 +162,29 @@ def test_input_norm_prefill_then_decode_same_workspace(device):
     for got, want in zip((q, k, v), dec.oracle()):
         g_ = f32(got).reshape(want.shape)
         assert orc.max_abs(g_, want) <= 2e-2 and orc.rel_l2(g_, want) <= 1e-2
+
+
+@pytest.mark.parametrize("T,hidden,plan", [(1536, 8192, ["row_scale", "tile"]), (1536, 4096, ["row_scale", "tile_pair"])])
+def test_input_norm_pair_tiles_need_lds_room(T, hidden, plan, device):
+    """With the input norm, gamma (hidden x 2 bytes) sits in the LDS beside the
+    ring.  At hidden 8192 it does not fit beside the 192-row pair tiles' ring and
+    exchange word (144 KiB + 16 B + 16 KiB), so the planner takes whole-head tiles
+    there; at hidden 4096 the pair tiles run.  Either way the result is the
+    variant-16 launch's, bit for bit."""
+    from conftest import launched_kernels
+    import mqk
+    case = Case(1, T, hidden, 32, 8, seed=5200 + hidden)
+    x, wq, wk, wv, gq, gk, cos, sin, _ = case.args(device)
+    gam = _gamma(hidden, 52).to(device)
+    call = lambda: mqk.fused_qkv_rope_ex(x, wq, wk, wv, gq, gk, cos, sin, input_norm_w=gam)
+    assert launched_kernels(call) == plan
+    out = call()
+    torch.cuda.synchronize()
+    mqk.set_option("prefill_tile", 16)
+    try:
+        ref = call()
+        torch.cuda.synchronize()
+    finally:
+        mqk.set_option("prefill_tile", 0)
+    for name, a, b in zip("qkv", out, ref):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), name
