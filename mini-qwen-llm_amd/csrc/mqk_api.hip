@@ -51,7 +51,7 @@ std::atomic<int64_t> g_decode_passes{16};  // most 64-row blocks one decode laun
 std::atomic<int64_t> g_head_tiles{1};  // one round of single-head tiles where the planner models them fastest
 std::atomic<int64_t> g_tile_ksplit{1};  // split-K tile launches: 0 off, 1 by cost model, >= 2 that split count
 std::atomic<int64_t> g_gemv_max_m{kGemvMaxM};  // W4A16 GEMMs with M up to this run the column-parallel kernel
-std::atomic<int64_t> g_pair_tiles{1};  // pair-tile variants (24, 25) as tile chooser candidates
+std::atomic<int64_t> g_pair_tiles{1};  // pair-tile variants (24-28) as planner candidates
 std::atomic<int64_t> g_pair_max_spins{1 << 14};  // a pair side's polls for its partner before it hands its half over
 
 constexpr int kMaxTiles = 1024;  // arrival counters available in the workspace (per head)

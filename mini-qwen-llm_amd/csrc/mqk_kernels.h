@@ -96,7 +96,7 @@ struct TileVariant {
 int tile_variant_count();
 const TileVariant* tile_variant(int index);
 // Picks a variant for the problem (id 0 = automatic).
-// allow_pair: the pair-tile variants (24, 25) may be chosen (bf16 q/k/v outputs
+// allow_pair: the pair-tile variants (24-28) may be chosen (bf16 q/k/v outputs
 // with head_dim 128 and a workspace for their exchange).
 const TileVariant* choose_tile_variant(int requested_id, int64_t M, int n_tiles, int int4, int cus,
                                        bool allow_pair = false);

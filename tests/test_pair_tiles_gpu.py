@@ -134,15 +134,16 @@ def test_pair_tiles_ex_features(variant, Hq, Hkv, whole, device):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"variant {variant}: {name} differs"
 
 
-def test_pair_tiles_graph_replay(device):
-    """Variant 25 in a HIP graph: the pair words are cleared by the launch itself,
+@pytest.mark.parametrize("variant,Hkv", [(25, 4), (26, 8), (28, 8)])
+def test_pair_tiles_graph_replay(variant, Hkv, device):
+    """Pair tiles in a HIP graph: the pair words are cleared by the launch itself,
     so replays, with eager calls of the same and another plan in between, stay
     bit-exact."""
     import mqk
-    case = Case(1, 1024, 2048, 32, 4, seed=4400)
+    case = Case(1, 1024, 2048, 32, Hkv, seed=4400)
     args = case.args(device)
-    small = Case(1, 64, 2048, 32, 4, seed=4401).args(device)
-    old = _opts(prefill_tile=25)
+    small = Case(1, 64, 2048, 32, Hkv, seed=4401).args(device)
+    old = _opts(prefill_tile=variant)
     try:
         stream = torch.cuda.Stream(device)
         with torch.cuda.stream(stream):
@@ -182,14 +183,15 @@ def test_pair_tiles_across_xcds(variant, Hq, Hkv, whole, device):
     _same(out, ref, f"variant {variant} across XCDs (hand-over)")
 
 
-def test_pair_tiles_on_many_streams(device):
+@pytest.mark.parametrize("variant", [24, 26, 28])
+def test_pair_tiles_on_many_streams(variant, device):
     """The exchange uses device-coherent accesses, so a pair whose sides land on
     different XCDs (whatever the hardware queue's starting XCD) still agrees."""
     import mqk
     case = Case(1, 512, 1024, 32, 8, seed=4500)
     args = case.args(device)
     ref = _run(lambda: mqk.fused_qkv_rope(*args), prefill_tile=16)
-    old = _opts(prefill_tile=24)
+    old = _opts(prefill_tile=variant)
     try:
         streams = [torch.cuda.Stream(device) for _ in range(8)]
         for i, st in enumerate(streams):
