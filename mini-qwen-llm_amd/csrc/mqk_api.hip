@@ -271,22 +271,21 @@ Plan plan_fused(int int4, int64_t M, int64_t K, int n_tiles, bool aligned, const
       else head_us = one64 ? 2.0 + 0.5 * stages : 2.5 + stages * (0.6 + 0.0002 * double(t128));
     }
   }
-  // One round of 128-row pair tiles (26: 2 x 128 x 192 per 3 heads, 27: 2 x 128 x 320
-  // per 5 heads) over more than half of the CUs, which no whole-head shape fills at
-  // these T.  Fitted on MI355X
-  // (hidden 2560 / 4096, 48 heads, T = 576 .. 1024, within ~2 us):
-  //   26: 15 us + (0.465 + 0.001 * workgroups) us per 64-k stage;
-  //   27 (hidden 2048 / 5120, 40 / 80 heads): ~5 us + 1.4 us per stage.
+  // One round of 128-row pair tiles (26: 2 x 128 x 192 per 3 heads) over more than
+  // half of the CUs, which no whole-head shape fills at these T, against the split-K,
+  // single-head and decode-block launches.  Fitted on MI355X (hidden 2560 / 4096,
+  // 48 heads, T = 576 .. 1024, within ~2 us): 15 us + (0.465 + 0.001 * workgroups) us
+  // per 64-k stage.  (The 2-stage 128 x 320 form 27 and the 192-row form 28 win only
+  // against whole-head tiles; the tile chooser ranks them.)
   const TileVariant* pv = nullptr;
   double pair_us = 1e30;
-  if (allow_pair && M > 64 && g_prefill_tile.load() == 0) {
-    const int id = n_tiles % 3 == 0 ? 26 : (n_tiles % 5 == 0 ? 27 : 0);
-    for (int i = 0; id != 0 && i < tile_variant_count(); ++i)
-      if (tile_variant(i)->id == id) pv = tile_variant(i);
+  if (allow_pair && M > 64 && g_prefill_tile.load() == 0 && n_tiles % 3 == 0) {
+    for (int i = 0; i < tile_variant_count(); ++i)
+      if (tile_variant(i)->id == 26) pv = tile_variant(i);
     const int64_t wgs = pv ? tile_count(*pv, M, n_tiles) : 0;
-    if (pv && 2 * wgs > cus && wgs <= cus && wgs / 2 <= kSplitMaxTiles && !(in_norm && tile_dma_lds_bytes(id) + K * 2 > 160 * 1024)) {
-      const double stages = double(K / 64);
-      pair_us = id == 26 ? 15.0 + stages * (0.465 + 0.001 * double(wgs)) : 5.0 + 1.4 * stages;
+    if (pv && 2 * wgs > cus && wgs <= cus && wgs / 2 <= kSplitMaxTiles &&
+        !(in_norm && tile_dma_lds_bytes(26) + K * 2 > 160 * 1024)) {
+      pair_us = 15.0 + double(K / 64) * (0.465 + 0.001 * double(wgs));
     } else {
       pv = nullptr;
     }
