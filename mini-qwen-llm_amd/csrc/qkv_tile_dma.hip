@@ -1441,14 +1441,16 @@ tile_dma_w4_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
     }
   };
 
-  f32x16_t acc[S::kMB][S::kNB];
+  // 16 x 16 accumulator blocks (v_mfma_f32_16x16x32_bf16), as the bf16 tile kernel
+  constexpr int kMB = S::kTM / 16, kNB = S::kTN / 16;
+  f32x4_t acc[kMB][kNB];
 #pragma unroll
-  for (int mb = 0; mb < S::kMB; ++mb)
+  for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
-    for (int nb = 0; nb < S::kNB; ++nb) acc[mb][nb] = f32x16_t{};
+    for (int nb = 0; nb < kNB; ++nb) acc[mb][nb] = f32x4_t{};
 
-  const int c32 = lane & 31;
-  const int khalf = lane >> 5;
+  const int c16 = lane & 15;
+  const int kq = lane >> 4;
   const bool fp16 = w.scale_fp16 != 0;
   const int nkt = int(K / 64);
 #pragma unroll
@@ -1469,34 +1471,32 @@ tile_dma_w4_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m) {
     barrier();
     if (kt + NS - 1 < nkt) issue(kt + NS - 1);
     const unsigned char* st = smem + (kt % NS) * S::kStageBytes;
-    float scl[S::kNB], zro[S::kNB];
+    float scl[kNB], zro[kNB];
 #pragma unroll
-    for (int nb = 0; nb < S::kNB; ++nb) {
-      const int col = wn * S::kTN + nb * 32 + c32;
+    for (int nb = 0; nb < kNB; ++nb) {
+      const int col = wn * S::kTN + nb * 16 + c16;
       const uint32_t sraw = *reinterpret_cast<const uint16_t*>(st + S::kABytes + S::kBBytes + col * 2);
       const uint32_t zw = *reinterpret_cast<const uint32_t*>(st + S::kABytes + S::kBBytes + S::kSBytes + (col / 8) * 4);
       scl[nb] = fp16 ? f16_to_f32(sraw) : bf16_to_f32(sraw);
       zro[nb] = float((zw >> ((col % 8) * 4)) & 0xFu);
     }
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int chunk = 2 * ks + khalf;  // x chunk == weight k-group of this lane
-      u32x4_t af[S::kMB], bf[S::kNB];
+    for (int ks = 0; ks < 2; ++ks) {
+      const int chunk = 4 * ks + kq;  // x chunk == weight k-group of this lane
+      u32x4_t bf[kNB];
 #pragma unroll
-      for (int mb = 0; mb < S::kMB; ++mb) {
-        const int row = wm * S::kTM + mb * 32 + c32;
-        af[mb] = *reinterpret_cast<const u32x4_t*>(st + row * 128 + stage_slot<64>(row, chunk) * 16);
-      }
-#pragma unroll
-      for (int nb = 0; nb < S::kNB; ++nb) {
-        const int col = wn * S::kTN + nb * 32 + c32;
+      for (int nb = 0; nb < kNB; ++nb) {
+        const int col = wn * S::kTN + nb * 16 + c16;
         const uint32_t word = *reinterpret_cast<const uint32_t*>(st + S::kABytes + (chunk * BN + col) * 4);
         bf[nb] = dequant_int4x8(word, zro[nb], scl[nb]);
       }
 #pragma unroll
-      for (int mb = 0; mb < S::kMB; ++mb)
+      for (int mb = 0; mb < kMB; ++mb) {
+        const int row = wm * S::kTM + mb * 16 + c16;
+        const u32x4_t af = *reinterpret_cast<const u32x4_t*>(st + row * 128 + stage_slot<64>(row, chunk) * 16);
 #pragma unroll
-        for (int nb = 0; nb < S::kNB; ++nb) acc[mb][nb] = mfma_32x32x16(af[mb], bf[nb], acc[mb][nb]);
+        for (int nb = 0; nb < kNB; ++nb) acc[mb][nb] = mfma_16x16x32(af, bf[nb], acc[mb][nb]);
+      }
     }
   }
   barrier();  // every wave is done with the ring; the epilogue reuses the LDS
