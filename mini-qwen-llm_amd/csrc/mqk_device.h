@@ -218,38 +218,6 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
       : "memory");
 }
 
-// L2 -> LDS through the buffer (MUBUF) path: buffer_load_dwordx4 ... lds.  The
-// compiler sets M0 from the wave-uniform LDS address and counts the load in
-// vmcnt like any vector-memory load.  Measured on MI355X in the tile kernels'
-// main loop: 2-3 % less time than the same loads as global_load_lds_dwordx4
-// (the loads alone take the same time; beside the matrix cores they interfere
-// less), with the same bytes in LDS.
-typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
-__device__ void mqk_raw_buffer_load_lds(i32x4_t rsrc, __attribute__((address_space(3))) uint32_t* lds, int size,
-                                        int voffset, int soffset, int offset, int aux)
-    __asm("llvm.amdgcn.raw.buffer.load.lds");
-
-// Buffer resource for raw loads at `base`: stride 0, no range check
-// (num_records all ones), the gfx9 raw-buffer word 3.  Wave-uniform.
-__device__ __forceinline__ i32x4_t raw_buffer_rsrc(const void* base) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  i32x4_t r;
-  r.x = __builtin_amdgcn_readfirstlane(int32_t(uint32_t(a)));
-  r.y = __builtin_amdgcn_readfirstlane(int32_t(uint32_t(a >> 32) & 0xFFFFu));
-  r.z = -1;
-  r.w = 0x00020000;
-  return r;
-}
-
-// 16 bytes per lane from rsrc's base + voffset (this lane) + soffset (uniform) to
-// LDS byte lds_base + 16 * lane (lds_base wave-uniform).
-__device__ __forceinline__ void bdma16(i32x4_t rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds_base) {
-  mqk_raw_buffer_load_lds(rsrc,
-                          reinterpret_cast<__attribute__((address_space(3))) uint32_t*>(
-                              uintptr_t(__builtin_amdgcn_readfirstlane(lds_base))),
-                          16, int(voffset), int(soffset), 0, 0);
-}
-
 // L2 -> LDS, 4 bytes per lane: this lane's word at gptr goes to LDS byte
 // lds_base + 4 * lane (lds_base wave-uniform).
 __device__ __forceinline__ void dma4(const void* gptr, uint32_t lds_base) {

@@ -3,9 +3,8 @@
 //
 // A workgroup computes a BM x (NH*128) tile of  x[M,K] @ W^T  (NH whole heads;
 // the Q/K/V weight matrices are addressed directly).  K is consumed in SBK-wide
-// (32 or 64) stages held in an NS-deep LDS ring that is filled with direct loads
-// (buffer_load_dwordx4 ... lds in this kernel, global_load_lds_dwordx4 in the int4
-// and split-K kernels; L2 -> LDS without VGPRs): while stage k is multiplied, the loads of stages
+// (32 or 64) stages held in an NS-deep LDS ring that is filled with global_load_lds_dwordx4
+// (L2 -> LDS without VGPRs): while stage k is multiplied, the loads of stages
 // k+1 .. k+NS-1 are in flight, which hides the L2 latency that a single
 // register-staged prefetch could not.  One barrier per stage: after it, every
 // wave's loads for stage k have landed (each wave first waits for its own with
@@ -712,11 +711,10 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m, PairX 
 
   // ---- this lane's sources: load instruction i of a stage fills staged rows
   // [R*(wave + i*W), +R), R = rows per load; lane -> row +lane/chunks, slot lane%chunks.
-  // The loads go through buffer resources based at the tile's first x row and, per
-  // projection, at the tile's first weight row of it, so the per-lane offsets stay
-  // small (at most the tile's rows x K x 2 bytes); loads i < kALoads fill x rows,
-  // the others weight rows of one projection each (proj_of[i], wave-uniform).
-  // The tile's first head of each projection (its weight rows start there).
+  // Each load's source is a wave-uniform base (the tile's first x row, or the first
+  // weight row of the load's head) plus a small per-lane byte offset (at most the
+  // tile's rows x K x 2 bytes) plus the stage's k offset; loads i < kALoads fill x
+  // rows, the others weight rows of one head each.
   uint32_t voff[S::kLoadsPerWave];
   const uint16_t* lbase[S::kLoadsPerWave];  // the load's base (x: the tile's first row; weights: the head's)
   uint32_t dst_off[S::kLoadsPerWave];
@@ -748,10 +746,6 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m, PairX 
     }
     dst_off[i] = uint32_t(row0 * kRowBytes);
   }
-  // the loads' resources, built once (wave-uniform bases)
-  i32x4_t rsrc[S::kLoadsPerWave];
-#pragma unroll
-  for (int i = 0; i < S::kLoadsPerWave; ++i) rsrc[i] = raw_buffer_rsrc(lbase[i]);
   // input RMSNorm: scale of the x row and k offset of the chunk each of this
   // lane's x loads brings in (load i < kALoads, row0 + lane / chunks, slot lane % chunks)
   const bool in_norm = p.in_gamma != nullptr;
@@ -773,7 +767,8 @@ tile_dma_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, int group_m, PairX 
     const uint32_t base = lds0 + uint32_t((kt % NS) * S::kStageBytes);
     const uint32_t koff = uint32_t(kt) * (SBK * 2);
 #pragma unroll
-    for (int i = 0; i < S::kLoadsPerWave; ++i) bdma16(rsrc[i], voff[i], koff, base + dst_off[i]);
+    for (int i = 0; i < S::kLoadsPerWave; ++i)
+      dma16(reinterpret_cast<const char*>(lbase[i]) + voff[i] + koff, base + dst_off[i]);
   };
 
   // ---- main loop -------------------------------------------------------------------
