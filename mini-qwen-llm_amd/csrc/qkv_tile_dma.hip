@@ -79,7 +79,7 @@ struct DmaShape {
   static constexpr int kRingBytes = NS * kStageBytes;
   static constexpr int kEpiBytes = BM * kEpiPitch * 4;
   static constexpr int kLdsBytes = kRingBytes > kEpiBytes ? kRingBytes : kEpiBytes;
-  static_assert(kTM % 32 == 0 && kTN % 32 == 0, "wave tile");
+  static_assert(kTM % 16 == 0 && kTN % 16 == 0, "wave tile (16 x 16 accumulator blocks)");
   static_assert(kLoadsPerStage % kWaves == 0, "loads per wave");
   static constexpr int kALoads = BM / (kRowsPerLoad * kWaves);  // this wave's loads i < kALoads fill x rows
   static_assert(BM % (kRowsPerLoad * kWaves) == 0, "x rows are whole load rounds");
@@ -837,6 +837,7 @@ tile_dma_split_kernel(ProblemArgs p, WeightArgs w, EpilogueArgs e, TileSplit sp)
   using S = DmaShape<BM, NH, WM, WN, NS, SBK>;
   constexpr int kRowBytes = S::kRowBytes;
   constexpr int BN = S::kBN;
+  static_assert(S::kTM % 32 == 0 && S::kTN % 32 == 0, "wave tile (32 x 32 accumulator blocks)");
   __shared__ __attribute__((aligned(16))) unsigned char smem[S::kLdsBytes];
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
 
