@@ -2,7 +2,7 @@
 """Benchmark of the fused QKV + QK-Norm + RoPE op on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
-    python bench.py --only {c1f32,c2f32,d14b,c2,c3,c4,c5,mid,mid256,mid128,gemm,copy,stream} --steps K   # one workload, for profiler runs
+    python bench.py --only {c1f32,c2f32,d14b,c2,c3,c4,c5,mid,mid1024,mid1536,mid256,mid128,gemm,copy,stream} --steps K   # one workload, for profiler runs
 
 Headline (``value``): BASELINE config 2, Qwen3-8B prefill B=4 x S=512 (2048
 tokens, hidden 4096, 32 Q heads, 8 KV heads, head_dim 128, bf16), tokens/s of
@@ -22,7 +22,8 @@ profiles/ when present.  ``cpu_baseline`` times a torch fp32 restatement of the
 reference's unfused composition (3 projections -> per-head RMSNorm -> RoPE) on
 the host's cores for a bounded sample of the same workload.
 ``secondary`` reports the other BASELINE configurations (decode, long prefill,
-W4A16) with their own roofline fractions; every step rotates over several copies
+W4A16) with their own roofline fractions, and single-sequence Qwen3-8B prefills of
+512, 1024 and 1536 tokens (the mid token counts); every step rotates over several copies
 of its inputs (decode: 8 weight sets, 400 MB; prefill and W4A16: 6 sets of x and
 weights, 300-480 MB), more than the 256 MB Infinity Cache, so it reads HBM.
 Config 1 (the Qwen3-0.6B-shaped layer, B=1 x S=128, which the reference runs
