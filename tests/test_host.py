@@ -124,7 +124,9 @@ def test_head_tile_plan(lib):
     T = 1024 (8 x 48 = 384 single-head tiles, two rounds) one round of 128-row
     pair tiles takes the call (8 x 16 pairs of 2 x 128 x 192): the counters, then
     per pair 2 x 128 floats of row sums of squares and a 128 x 64 float hand-over
-    area.  With pair tiles off, the split-K launch keeps it."""
+    area.  With pair tiles off, the split-K launch keeps it.  Further up, nearly a
+    round of 192-row pairs takes T = 1536 (but not T = 1152, 7 workgroups per 8
+    CUs), and 128 x 320 pairs take hidden 2048 with 40 heads at T = 2048."""
     from mqk import _native
     if _native.get_option("device_cus") != 256:
         pytest.skip("the plan depends on the device's CU count (256 on MI355X)")
@@ -136,8 +138,17 @@ def test_head_tile_plan(lib):
         assert lib.mqk_fused_qkv_rope_workspace_size(512, 32, 8, 4096) == 0
         assert lib.mqk_fused_qkv_rope_workspace_size(768, 32, 4, 2048) == 0
         assert lib.mqk_fused_qkv_rope_workspace_size(1024, 32, 8, 4096) == C + 128 * (2 * 128 + 128 * 64) * 4
+        # T = 1536: 8 x 16 pairs of 192-row tiles (2 x 192 x 192 per 3 heads): per pair
+        # 2 x 192 floats of sums and a 192 x 64 float hand-over area
+        assert lib.mqk_fused_qkv_rope_workspace_size(1536, 32, 8, 4096) == C + 128 * (2 * 192 + 192 * 64) * 4
+        # T = 1152 (7 workgroups per 8 CUs as 192-row pairs): whole-head tiles, no workspace
+        assert lib.mqk_fused_qkv_rope_workspace_size(1152, 32, 8, 4096) == 0
+        # hidden 2048 with 40 heads at T = 2048: 16 x 8 pairs of 128 x 320 tiles (2 x 128 floats
+        # of sums and a 128 x 64 hand-over area each)
+        assert lib.mqk_fused_qkv_rope_workspace_size(2048, 32, 4, 2048) == C + 128 * (2 * 128 + 128 * 64) * 4
         _native.set_option("pair_tiles", 0)
         assert lib.mqk_fused_qkv_rope_workspace_size(1024, 32, 8, 4096) == C + 128 * 2 * part
+        assert lib.mqk_fused_qkv_rope_workspace_size(1536, 32, 8, 4096) == 0
     finally:
         _native.set_option("decode_blocks", 16)
         _native.set_option("pair_tiles", 1)
