@@ -44,7 +44,7 @@ enum mqk_status {
   MQK_OK = 0,
   MQK_ERR_NULL_POINTER = -1,     /* a required pointer is NULL */
   MQK_ERR_BAD_SHAPE = -2,        /* a size is negative, zero where it must not be, or inconsistent */
-  MQK_ERR_UNSUPPORTED = -3,      /* a valid shape this library does not implement (e.g. head_dim 256) */
+  MQK_ERR_UNSUPPORTED = -3,      /* a valid shape this library does not implement (e.g. head_dim 66) */
   MQK_ERR_MISALIGNED = -4,       /* a pointer is not 16-byte aligned */
   MQK_ERR_WORKSPACE = -5,        /* workspace NULL or smaller than mqk_*_workspace_size() */
   MQK_ERR_HIP = -6,              /* a HIP runtime call failed (launch, attribute query) */
@@ -93,6 +93,11 @@ const char* mqk_last_error_detail(void);
  * accumulation on MFMA, the norm and RoPE are applied to the fp32 accumulator
  * (the projection is not rounded to bf16 before the norm), one bf16 rounding
  * per output.
+ * Other head sizes that are a multiple of 8 up to 512 (e.g. 80, 96, 192, 256) run
+ * as the reference composes the op (fused_qkv_rope.py:166-190): three plain GEMM
+ * launches into q / k / v (the projection rounded to bf16), then one QK-Norm +
+ * RoPE launch in place on q and k; no workspace is used, and the paged-cache
+ * write and the input RMSNorm of the _ex entry point are not offered for them.
  */
 int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
                             const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,

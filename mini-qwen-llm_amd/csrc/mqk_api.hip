@@ -571,12 +571,83 @@ static int apply_ext(const mqk_fused_ext* ext, const int32_t* positions, int64_t
   return apply_paged(ext->kv, positions, S, T, varlen, e);
 }
 
+// Head sizes the fused kernels do not tile (a multiple of 8 up to 512, other than
+// 64 and 128): the three projections run as plain GEMMs on the tile kernels,
+// written straight into q, k and v, then launch_norm_rope_any normalises and
+// rotates q and k in place.  Like the reference's own composition (a vendor GEMM
+// into bf16 q / k, then its norm + RoPE kernel, fused_qkv_rope.py:166-190), the
+// projections are rounded to bf16 before the norm.  The paged-cache write and the
+// fused input RMSNorm are not offered on this path.
+static int fused_bf16_any_d(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
+                            const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                            const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                            int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                            int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                            const mqk_fused_ext* ext, void* stream) {
+  if (T < 0 || hidden <= 0 || Hq <= 0 || Hkv <= 0)
+    return fail(MQK_ERR_BAD_SHAPE, "need T >= 0, hidden > 0, Hq > 0, Hkv > 0");
+  if (D % 8 != 0 || D > 512)
+    return fail(MQK_ERR_UNSUPPORTED, "head_dim %d not supported (64, 128, or a multiple of 8 up to 512)", D);
+  if (ext && (ext->kv || ext->in_gamma))
+    return fail(MQK_ERR_UNSUPPORTED, "head_dim %d: the paged-cache write and the input RMSNorm need head_dim "
+                                     "64 or 128", D);
+  if (hidden % kBK != 0)
+    return fail(MQK_ERR_UNSUPPORTED, "hidden %lld must be a multiple of 64", (long long)hidden);
+  const int64_t n_max = int64_t(Hq > Hkv ? Hq : Hkv) * D;
+  if ((n_max + kHeadDim - 1) / kHeadDim > kMaxTiles)
+    return fail(MQK_ERR_UNSUPPORTED, "Hq * head_dim must be <= %d", kMaxTiles * kHeadDim);
+  if (T > (int64_t(1) << 31) / 2) return fail(MQK_ERR_UNSUPPORTED, "T too large");
+  if (T == 0) return ok();
+  if (!x || !q || !k || !v) return fail(MQK_ERR_NULL_POINTER, "x/q/k/v must be non-NULL");
+  if (!w_q || !w_k || !w_v) return fail(MQK_ERR_NULL_POINTER, "w_q/w_k/w_v must be non-NULL");
+  if (!aligned16(x) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(w_q) ||
+      !aligned16(w_k) || !aligned16(w_v))
+    return fail(MQK_ERR_MISALIGNED, "x/q/k/v and the weights must be 16-byte aligned");
+  const bool varlen = ext && ext->cu_seqlens;
+  int st = check_rope_args(q_gamma, k_gamma, cos, sin, S, cos_rows, positions, eps, varlen);
+  if (st != MQK_OK) return st;
+  EpilogueArgs er = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps, q, k, v, Hq, Hkv);
+  er.head_dim = D;
+  ProblemArgs pr{x, T, hidden, 0};
+  if ((st = apply_ext(ext, positions, S, T, pr, er)) != MQK_OK) return st;
+  const Topology topo = device_topology();
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  const mqk_bf16* wts[3] = {w_q, w_k, w_v};
+  mqk_bf16* outs[3] = {q, k, v};
+  const int heads[3] = {Hq, Hkv, Hkv};
+  for (int i = 0; i < 3; ++i) {
+    const int64_t N = int64_t(heads[i]) * D;  // N % 8 == 0: the tiles store whole 8-column runs below N
+    const int tiles = int((N + kHeadDim - 1) / kHeadDim);
+    ProblemArgs p{x, T, hidden, tiles};
+    p.cus = topo.cus;
+    p.xcds = topo.xcds;
+    WeightArgs w{};
+    w.w[0] = wts[i];
+    w.n_cols[0] = N;
+    EpilogueArgs e{};
+    e.qkv = 0;
+    e.Hq = tiles;
+    e.Hkv = 0;
+    e.out = outs[i];
+    e.N = N;
+    e.head_dim = kHeadDim;  // (plain output: the epilogue's 128-column blocks)
+    const TileVariant* v = choose_tile_variant(0, T, tiles, 0, topo.cus);
+    if (!v) v = choose_tile_variant(1, T, tiles, 0, topo.cus);
+    st = hip_status(launch_tile(*v, 0, p, w, e, int(g_group_m.load()), hs), "tile kernel launch (projection)");
+    if (st != MQK_OK) return st;
+  }
+  return hip_status(launch_norm_rope_any(er, T, hs), "norm + RoPE launch");
+}
+
 static int fused_bf16_impl(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
                            const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
                            const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
                            int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
                            int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
                            const mqk_fused_ext* ext, void* workspace, size_t ws_bytes, void* stream) {
+  if (D > 0 && D % 2 == 0 && D != kHeadDim && D != 64)
+    return fused_bf16_any_d(x, w_q, w_k, w_v, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D,
+                            cos_rows, eps, q, k, v, ext, stream);
   const bool varlen = ext && ext->cu_seqlens;
   int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v, ext && ext->kv);
   if (st != MQK_OK) return st;

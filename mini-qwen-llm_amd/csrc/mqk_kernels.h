@@ -202,6 +202,9 @@ hipError_t launch_read_probe(const void* src, size_t bytes, int blocks, uint32_t
 hipError_t launch_clock_probe(uint64_t* out, int spins, hipStream_t stream);
 
 // Standalone QK-norm + RoPE.
+// QK-Norm + RoPE in place on already-projected q [T, Hq, D] / k [T, Hkv, D] (e.q, e.k)
+// for a head_dim D that is a multiple of 8 up to 512 (e.head_dim).
+hipError_t launch_norm_rope_any(const EpilogueArgs& e, int64_t T, hipStream_t stream);
 hipError_t launch_norm_rope(const uint16_t* q_raw, const uint16_t* k_raw, const EpilogueArgs& e,
                             int64_t T, hipStream_t stream);
 

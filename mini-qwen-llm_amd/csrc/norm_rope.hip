@@ -54,7 +54,66 @@ norm_rope_kernel(const uint16_t* __restrict__ q_raw, const uint16_t* __restrict_
   dst[col + hd2] = f32_to_bf16(x2n * c2 + x1n * s2);
 }
 
+// Any head_dim D that is a multiple of 8 up to kAnyMaxD (the op's generic path for
+// head sizes its fused kernels do not tile: the projections run as plain GEMMs
+// into q / k / v, then this kernel normalises and rotates q and k in place).  One
+// wave per (token, head): lane l owns the RoPE pairs (d, d + D/2) for d = l + 64 i,
+// so the rotation is lane-local and the sum of squares is one 64-lane butterfly.
+constexpr int kAnyMaxD = 512;
+
+__global__ void __launch_bounds__(kNrWaves * 64)
+norm_rope_any_kernel(EpilogueArgs e, int64_t T) {
+  const int lane = threadIdx.x & 63;
+  const int heads = e.Hq + e.Hkv;
+  const int64_t item = int64_t(blockIdx.x) * kNrWaves + (threadIdx.x >> 6);
+  if (item >= T * heads) return;
+  const int64_t t = item / heads;
+  const int h = int(item - t * heads);
+  const bool is_q = h < e.Hq;
+  const int hh = is_q ? h : h - e.Hq;
+  const int H = is_q ? e.Hq : e.Hkv;
+  const int hd = e.head_dim, hd2 = hd / 2;
+  uint16_t* row = (is_q ? e.q : e.k) + (t * H + hh) * hd;
+  const uint16_t* gamma = is_q ? e.q_gamma : e.k_gamma;
+  constexpr int kPer = kAnyMaxD / 128;  // pairs per lane at most
+  float x1[kPer], x2[kPer];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int d = lane + 64 * i;
+    x1[i] = d < hd2 ? bf16_to_f32(row[d]) : 0.f;
+    x2[i] = d < hd2 ? bf16_to_f32(row[d + hd2]) : 0.f;
+    ss += x1[i] * x1[i] + x2[i] * x2[i];
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+  const float rms = rsqrtf(ss / float(hd) + e.eps);
+  const int64_t prow = rope_row(e, t) * hd;
+  // in place: every lane has read its inputs before the butterfly completes
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int d = lane + 64 * i;
+    if (d < hd2) {
+      const float x1n = x1[i] * rms * bf16_to_f32(gamma[d]);
+      const float x2n = x2[i] * rms * bf16_to_f32(gamma[d + hd2]);
+      const float c1 = bf16_to_f32(e.cos[prow + d]), c2 = bf16_to_f32(e.cos[prow + d + hd2]);
+      const float s1 = bf16_to_f32(e.sin[prow + d]), s2 = bf16_to_f32(e.sin[prow + d + hd2]);
+      row[d] = f32_to_bf16(x1n * c1 - x2n * s1);
+      row[d + hd2] = f32_to_bf16(x2n * c2 + x1n * s2);
+    }
+  }
+}
+
 }  // namespace
+
+hipError_t launch_norm_rope_any(const EpilogueArgs& e, int64_t T, hipStream_t stream) {
+  if (e.head_dim <= 0 || e.head_dim % 8 != 0 || e.head_dim > kAnyMaxD) return hipErrorInvalidValue;
+  const int64_t items = T * (e.Hq + e.Hkv);
+  const int64_t blocks = (items + kNrWaves - 1) / kNrWaves;
+  if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(norm_rope_any_kernel, dim3(unsigned(blocks)), dim3(kNrWaves * 64), 0, stream, e, T);
+  return hipGetLastError();
+}
 
 hipError_t launch_norm_rope(const uint16_t* q_raw, const uint16_t* k_raw, const EpilogueArgs& e,
                             int64_t T, hipStream_t stream) {

@@ -19,7 +19,10 @@ Shapes are inferred as the reference does (:155-158): ``D = q_norm_w.shape[0]``,
 fp32 norm + RoPE applied to the accumulators, one bf16 store per output.
 
 Differences from the reference, all deliberate:
-  * the norm reads the fp32 accumulator, not a bf16-rounded GEMM output;
+  * the norm reads the fp32 accumulator, not a bf16-rounded GEMM output (head
+    sizes other than 64 and 128 -- multiples of 8 up to 512 -- run the
+    reference's own composition instead: GEMMs into bf16 q / k / v, then norm +
+    RoPE; other head sizes raise);
   * ``v`` is our own MFMA projection (fp32 accumulate, one rounding), so it is
     not bit-identical to a vendor GEMM (test_fused_qkv_rope.py:165 demands
     bit-equality with torch's own GEMM, which no independent kernel can give);

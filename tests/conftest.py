@@ -113,7 +113,7 @@ def no_pair_tiles():
 # Short names of the library's kernels, by (demangled or mangled) kernel name.
 _KERNEL_NAMES = (("decode_multi_kernel", "decode_multi"), ("decode_long_kernel", "decode"), ("decode_kernel", "decode"),
                  ("tile_dma_w4_kernel", "tile_w4"), ("tile_dma_split_kernel", "tile_split"), ("tile_dma_kernel", "tile"), ("tile_kernel", "tile_reg"),
-                 ("row_scale_kernel", "row_scale"), ("norm_rope_kernel", "norm_rope"),
+                 ("row_scale_kernel", "row_scale"), ("norm_rope_any_kernel", "norm_rope_any"), ("norm_rope_kernel", "norm_rope"),
                  ("f32_qkv_kernel", "f32"), ("w4_gemv", "gemv"))
 
 
