@@ -214,7 +214,9 @@ int mqk_w4a16_gemm_ex(const mqk_bf16* x, const int32_t* qweight, const void* sca
  * Fused W4A16 front: three int4 projections (q, k, v; each in the
  * mqk_w4a16_gemm layout with N = Hq*D, Hkv*D, Hkv*D) + QK-Norm + RoPE,
  * with the same position rules, outputs and workspace as
- * mqk_fused_qkv_rope_bf16.  Replaces attention.py:102-109 / :136-148, where
+ * mqk_fused_qkv_rope_bf16 (head sizes other than 64 and 128, multiples of 8 up
+ * to 512, as there: three mqk_w4a16_gemm launches into q / k / v, then the
+ * in-place QK-Norm + RoPE).  Replaces attention.py:102-109 / :136-148, where
  * the reference runs w4a16_gemm x3 then an unfused RMSNorm and RoPE.
  */
 int mqk_fused_qkv_rope_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void* sc_q,

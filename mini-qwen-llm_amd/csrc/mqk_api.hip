@@ -578,12 +578,11 @@ static int apply_ext(const mqk_fused_ext* ext, const int32_t* positions, int64_t
 // into bf16 q / k, then its norm + RoPE kernel, fused_qkv_rope.py:166-190), the
 // projections are rounded to bf16 before the norm.  The paged-cache write and the
 // fused input RMSNorm are not offered on this path.
-static int fused_bf16_any_d(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
-                            const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
-                            const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
-                            int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
-                            int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
-                            const mqk_fused_ext* ext, void* stream) {
+// Validation and the norm / RoPE arguments of the generic head-size path (below).
+static int any_d_prepare(const mqk_bf16* x, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                         const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions, int64_t T,
+                         int64_t S, int64_t hidden, int Hq, int Hkv, int D, int64_t cos_rows, float eps,
+                         mqk_bf16* q, mqk_bf16* k, mqk_bf16* v, const mqk_fused_ext* ext, EpilogueArgs& er) {
   if (T < 0 || hidden <= 0 || Hq <= 0 || Hkv <= 0)
     return fail(MQK_ERR_BAD_SHAPE, "need T >= 0, hidden > 0, Hq > 0, Hkv > 0");
   if (D % 8 != 0 || D > 512)
@@ -597,19 +596,38 @@ static int fused_bf16_any_d(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
   if ((n_max + kHeadDim - 1) / kHeadDim > kMaxTiles)
     return fail(MQK_ERR_UNSUPPORTED, "Hq * head_dim must be <= %d", kMaxTiles * kHeadDim);
   if (T > (int64_t(1) << 31) / 2) return fail(MQK_ERR_UNSUPPORTED, "T too large");
-  if (T == 0) return ok();
+  if (T == 0) return MQK_OK;
   if (!x || !q || !k || !v) return fail(MQK_ERR_NULL_POINTER, "x/q/k/v must be non-NULL");
-  if (!w_q || !w_k || !w_v) return fail(MQK_ERR_NULL_POINTER, "w_q/w_k/w_v must be non-NULL");
-  if (!aligned16(x) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(w_q) ||
-      !aligned16(w_k) || !aligned16(w_v))
-    return fail(MQK_ERR_MISALIGNED, "x/q/k/v and the weights must be 16-byte aligned");
-  const bool varlen = ext && ext->cu_seqlens;
-  int st = check_rope_args(q_gamma, k_gamma, cos, sin, S, cos_rows, positions, eps, varlen);
+  if (!aligned16(x) || !aligned16(q) || !aligned16(k) || !aligned16(v))
+    return fail(MQK_ERR_MISALIGNED, "x/q/k/v must be 16-byte aligned");
+  int st = check_rope_args(q_gamma, k_gamma, cos, sin, S, cos_rows, positions, eps, ext && ext->cu_seqlens);
   if (st != MQK_OK) return st;
-  EpilogueArgs er = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps, q, k, v, Hq, Hkv);
+  er = make_qkv_epilogue(q_gamma, k_gamma, cos, sin, positions, S, cos_rows, eps, q, k, v, Hq, Hkv);
   er.head_dim = D;
   ProblemArgs pr{x, T, hidden, 0};
-  if ((st = apply_ext(ext, positions, S, T, pr, er)) != MQK_OK) return st;
+  return apply_ext(ext, positions, S, T, pr, er);
+}
+
+// Head sizes the fused kernels do not tile (a multiple of 8 up to 512, other than
+// 64 and 128): the three projections run as plain GEMMs on the tile kernels,
+// written straight into q, k and v, then launch_norm_rope_any normalises and
+// rotates q and k in place.  Like the reference's own composition (a vendor GEMM
+// into bf16 q / k, then its norm + RoPE kernel, fused_qkv_rope.py:166-190), the
+// projections are rounded to bf16 before the norm.  The paged-cache write and the
+// fused input RMSNorm are not offered on this path.
+static int fused_bf16_any_d(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
+                            const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
+                            const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
+                            int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
+                            int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
+                            const mqk_fused_ext* ext, void* stream) {
+  EpilogueArgs er{};
+  int st = any_d_prepare(x, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D, cos_rows, eps, q, k,
+                         v, ext, er);
+  if (st != MQK_OK || T == 0) return st == MQK_OK ? ok() : st;
+  if (!w_q || !w_k || !w_v) return fail(MQK_ERR_NULL_POINTER, "w_q/w_k/w_v must be non-NULL");
+  if (!aligned16(w_q) || !aligned16(w_k) || !aligned16(w_v))
+    return fail(MQK_ERR_MISALIGNED, "weights must be 16-byte aligned");
   const Topology topo = device_topology();
   const hipStream_t hs = static_cast<hipStream_t>(stream);
   const mqk_bf16* wts[3] = {w_q, w_k, w_v};
@@ -996,6 +1014,23 @@ static int fused_w4a16_impl(const mqk_bf16* x, const int32_t* qw_q, const void* 
                             int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
                             int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
                             const mqk_fused_ext* ext, void* workspace, size_t ws_bytes, void* stream) {
+  if (D > 0 && D % 2 == 0 && D != kHeadDim && D != 64) {
+    // the generic head-size path, as fused_bf16_any_d, with the W4A16 GEMMs
+    EpilogueArgs er{};
+    int st = any_d_prepare(x, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D, cos_rows, eps, q,
+                           k, v, ext, er);
+    if (st != MQK_OK || T == 0) return st == MQK_OK ? ok() : st;
+    const int32_t* qws[3] = {qw_q, qw_k, qw_v};
+    const void* scs[3] = {sc_q, sc_k, sc_v};
+    const int32_t* qzs[3] = {qz_q, qz_k, qz_v};
+    mqk_bf16* outs[3] = {q, k, v};
+    const int heads[3] = {Hq, Hkv, Hkv};
+    for (int i = 0; i < 3; ++i)
+      if ((st = mqk_w4a16_gemm(x, qws[i], scs[i], qzs[i], T, hidden, int64_t(heads[i]) * D, group, scale_type,
+                               outs[i], stream)) != MQK_OK)
+        return st;
+    return hip_status(launch_norm_rope_any(er, T, static_cast<hipStream_t>(stream)), "norm + RoPE launch");
+  }
   const bool varlen = ext && ext->cu_seqlens;
   int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v, ext && ext->kv);
   if (st != MQK_OK) return st;

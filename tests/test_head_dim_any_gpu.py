@@ -95,3 +95,33 @@ def test_any_head_dim_refusals(device):
     with pytest.raises(Exception):
         mqk.fused_qkv_rope_ex(x.view(8, 1024), wq, wk, wv, gq, gk, cos, sin, input_norm_w=in_w)
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("T,round_weight", [(8, False), (40, True)])
+def test_any_head_dim_w4a16(T, round_weight, device):
+    """The W4A16 front at head_dim 96: the three W4A16 GEMMs into q / k / v (the
+    column-parallel kernel at T <= 16, which keeps the dequantised weight exact;
+    the int4 tiles above, which round it to bf16), then the norm + RoPE launch,
+    against the oracle with the same weight and projection rounding."""
+    import mqk
+    D, Hq, Hkv, hidden = 96, 16, 4, 1024
+    pos = torch.randint(0, 2048, (T,), generator=torch.Generator().manual_seed(T), dtype=torch.int32)
+    case = Case(T, 1, hidden, Hq, Hkv, seed=9400 + T, head_dim=D, rows=2048, positions=pos)
+    args = case.args(device)
+    projs = [tuple(t.to(device) for t in mqk.per_group_minmax_quantize(w.float().T.contiguous(), 128, torch.bfloat16))
+             for w in (case.w_q, case.w_k, case.w_v)]
+    kernels = launched_kernels(lambda: mqk.fused_qkv_rope_w4a16(args[0], *projs, *args[4:]))
+    assert len(kernels) == 4 and kernels[-1] == "norm_rope_any", kernels
+    out = mqk.fused_qkv_rope_w4a16(args[0], *projs, *args[4:])
+    torch.cuda.synchronize()
+    x2 = f32(case.x).reshape(T, hidden)
+    raw = [orc.round_bf16(orc.w4a16_gemm(x2, p[0].cpu().numpy(), p[1].float().cpu().numpy(), p[2].cpu().numpy(),
+                                         128, np.float64, round_weight)) for p in projs]
+    rows = pos.numpy()
+    q = orc.qk_norm_rope(raw[0].reshape(T, Hq, D), f32(case.q_norm_w), f32(case.cos), f32(case.sin), 1, rows)
+    k = orc.qk_norm_rope(raw[1].reshape(T, Hkv, D), f32(case.k_norm_w), f32(case.cos), f32(case.sin), 1, rows)
+    for name, o, r in zip("qkv", out, (q, k, raw[2].reshape(T, Hkv, D))):
+        o = f32(o).reshape(r.shape)
+        assert np.isfinite(o).all(), name
+        assert orc.max_abs(o, r) <= MAX_ABS, f"{name} max-abs {orc.max_abs(o, r)}"
+        assert orc.rel_l2(o, r) <= REL_L2, f"{name} rel-L2 {orc.rel_l2(o, r)}"
