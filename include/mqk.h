@@ -96,8 +96,9 @@ const char* mqk_last_error_detail(void);
  * Other head sizes that are a multiple of 8 up to 512 (e.g. 80, 96, 192, 256) run
  * as the reference composes the op (fused_qkv_rope.py:166-190): three plain GEMM
  * launches into q / k / v (the projection rounded to bf16), then one QK-Norm +
- * RoPE launch in place on q and k; no workspace is used, and the paged-cache
- * write and the input RMSNorm of the _ex entry point are not offered for them.
+ * RoPE launch in place on q and k (which also writes the paged-cache rows); the
+ * workspace holds only the input RMSNorm's per-token scales, and k / v must be
+ * given even with a paged cache.
  */
 int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
                             const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
@@ -216,7 +217,7 @@ int mqk_w4a16_gemm_ex(const mqk_bf16* x, const int32_t* qweight, const void* sca
  * with the same position rules, outputs and workspace as
  * mqk_fused_qkv_rope_bf16 (head sizes other than 64 and 128, multiples of 8 up
  * to 512, as there: three mqk_w4a16_gemm launches into q / k / v, then the
- * in-place QK-Norm + RoPE).  Replaces attention.py:102-109 / :136-148, where
+ * in-place QK-Norm + RoPE; no input RMSNorm at those sizes).  Replaces attention.py:102-109 / :136-148, where
  * the reference runs w4a16_gemm x3 then an unfused RMSNorm and RoPE.
  */
 int mqk_fused_qkv_rope_w4a16(const mqk_bf16* x, const int32_t* qw_q, const void* sc_q,

@@ -587,9 +587,6 @@ static int any_d_prepare(const mqk_bf16* x, const mqk_bf16* q_gamma, const mqk_b
     return fail(MQK_ERR_BAD_SHAPE, "need T >= 0, hidden > 0, Hq > 0, Hkv > 0");
   if (D % 8 != 0 || D > 512)
     return fail(MQK_ERR_UNSUPPORTED, "head_dim %d not supported (64, 128, or a multiple of 8 up to 512)", D);
-  if (ext && (ext->kv || ext->in_gamma))
-    return fail(MQK_ERR_UNSUPPORTED, "head_dim %d: the paged-cache write and the input RMSNorm need head_dim "
-                                     "64 or 128", D);
   if (hidden % kBK != 0)
     return fail(MQK_ERR_UNSUPPORTED, "hidden %lld must be a multiple of 64", (long long)hidden);
   const int64_t n_max = int64_t(Hq > Hkv ? Hq : Hkv) * D;
@@ -597,6 +594,7 @@ static int any_d_prepare(const mqk_bf16* x, const mqk_bf16* q_gamma, const mqk_b
     return fail(MQK_ERR_UNSUPPORTED, "Hq * head_dim must be <= %d", kMaxTiles * kHeadDim);
   if (T > (int64_t(1) << 31) / 2) return fail(MQK_ERR_UNSUPPORTED, "T too large");
   if (T == 0) return MQK_OK;
+  // (k and v are written even with a paged cache: the cache rows are copied from them)
   if (!x || !q || !k || !v) return fail(MQK_ERR_NULL_POINTER, "x/q/k/v must be non-NULL");
   if (!aligned16(x) || !aligned16(q) || !aligned16(k) || !aligned16(v))
     return fail(MQK_ERR_MISALIGNED, "x/q/k/v must be 16-byte aligned");
@@ -613,14 +611,16 @@ static int any_d_prepare(const mqk_bf16* x, const mqk_bf16* q_gamma, const mqk_b
 // written straight into q, k and v, then launch_norm_rope_any normalises and
 // rotates q and k in place.  Like the reference's own composition (a vendor GEMM
 // into bf16 q / k, then its norm + RoPE kernel, fused_qkv_rope.py:166-190), the
-// projections are rounded to bf16 before the norm.  The paged-cache write and the
-// fused input RMSNorm are not offered on this path.
+// projections are rounded to bf16 before the norm.  The fused input RMSNorm runs in
+// the GEMMs as in the fused path (per-token scales from the pre-pass, in the
+// workspace after its arrival counters); the paged-cache rows are written by the
+// norm + RoPE launch.
 static int fused_bf16_any_d(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
                             const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
                             const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
                             int64_t T, int64_t S, int64_t hidden, int Hq, int Hkv, int D,
                             int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
-                            const mqk_fused_ext* ext, void* stream) {
+                            const mqk_fused_ext* ext, void* workspace, size_t ws_bytes, void* stream) {
   EpilogueArgs er{};
   int st = any_d_prepare(x, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D, cos_rows, eps, q, k,
                          v, ext, er);
@@ -630,6 +630,19 @@ static int fused_bf16_any_d(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
     return fail(MQK_ERR_MISALIGNED, "weights must be 16-byte aligned");
   const Topology topo = device_topology();
   const hipStream_t hs = static_cast<hipStream_t>(stream);
+  ProblemArgs pn{x, T, hidden, 0};
+  if (ext && ext->in_gamma) {
+    if ((st = apply_ext(ext, positions, S, T, pn, er)) != MQK_OK) return st;  // (in_gamma checks)
+    // the scales after the workspace's arrival counters, which other calls on it need at zero
+    const size_t off = align_up(decode_counter_bytes(), 256);
+    if (!workspace || ws_bytes < off + size_t(T) * sizeof(float))
+      return fail(MQK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given%s", off + size_t(T) * sizeof(float),
+                  ws_bytes, workspace ? "" : " (NULL)");
+    float* scale = reinterpret_cast<float*>(static_cast<char*>(workspace) + off);
+    st = hip_status(launch_row_scale(x, T, hidden, ext->in_eps, scale, hs), "input norm pre-pass launch");
+    if (st != MQK_OK) return st;
+    pn.in_scale = scale;
+  }
   const mqk_bf16* wts[3] = {w_q, w_k, w_v};
   mqk_bf16* outs[3] = {q, k, v};
   const int heads[3] = {Hq, Hkv, Hkv};
@@ -639,6 +652,8 @@ static int fused_bf16_any_d(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
     ProblemArgs p{x, T, hidden, tiles};
     p.cus = topo.cus;
     p.xcds = topo.xcds;
+    p.in_gamma = pn.in_gamma;
+    p.in_scale = pn.in_scale;
     WeightArgs w{};
     w.w[0] = wts[i];
     w.n_cols[0] = N;
@@ -650,7 +665,9 @@ static int fused_bf16_any_d(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
     e.N = N;
     e.head_dim = kHeadDim;  // (plain output: the epilogue's 128-column blocks)
     const TileVariant* v = choose_tile_variant(0, T, tiles, 0, topo.cus);
-    if (!v) v = choose_tile_variant(1, T, tiles, 0, topo.cus);
+    // (the pipelined tiles hold the input norm's gamma in LDS beside their ring)
+    if (!v || (p.in_gamma && tile_dma_lds_bytes(v->id) + hidden * 2 > 160 * 1024))
+      v = choose_tile_variant(1, T, tiles, 0, topo.cus);
     st = hip_status(launch_tile(*v, 0, p, w, e, int(g_group_m.load()), hs), "tile kernel launch (projection)");
     if (st != MQK_OK) return st;
   }
@@ -665,7 +682,7 @@ static int fused_bf16_impl(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf1
                            const mqk_fused_ext* ext, void* workspace, size_t ws_bytes, void* stream) {
   if (D > 0 && D % 2 == 0 && D != kHeadDim && D != 64)
     return fused_bf16_any_d(x, w_q, w_k, w_v, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D,
-                            cos_rows, eps, q, k, v, ext, stream);
+                            cos_rows, eps, q, k, v, ext, workspace, ws_bytes, stream);
   const bool varlen = ext && ext->cu_seqlens;
   int st = validate_fused_common(x, T, S, hidden, Hq, Hkv, D, q, k, v, ext && ext->kv);
   if (st != MQK_OK) return st;
@@ -1015,7 +1032,10 @@ static int fused_w4a16_impl(const mqk_bf16* x, const int32_t* qw_q, const void* 
                             int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
                             const mqk_fused_ext* ext, void* workspace, size_t ws_bytes, void* stream) {
   if (D > 0 && D % 2 == 0 && D != kHeadDim && D != 64) {
-    // the generic head-size path, as fused_bf16_any_d, with the W4A16 GEMMs
+    // the generic head-size path, as fused_bf16_any_d, with the W4A16 GEMMs (which
+    // take no input norm)
+    if (ext && ext->in_gamma)
+      return fail(MQK_ERR_UNSUPPORTED, "head_dim %d: the W4A16 front's input RMSNorm needs head_dim 64 or 128", D);
     EpilogueArgs er{};
     int st = any_d_prepare(x, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D, cos_rows, eps, q,
                            k, v, ext, er);

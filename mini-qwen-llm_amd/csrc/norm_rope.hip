@@ -56,25 +56,37 @@ norm_rope_kernel(const uint16_t* __restrict__ q_raw, const uint16_t* __restrict_
 
 // Any head_dim D that is a multiple of 8 up to kAnyMaxD (the op's generic path for
 // head sizes its fused kernels do not tile: the projections run as plain GEMMs
-// into q / k / v, then this kernel normalises and rotates q and k in place).  One
-// wave per (token, head): lane l owns the RoPE pairs (d, d + D/2) for d = l + 64 i,
-// so the rotation is lane-local and the sum of squares is one 64-lane butterfly.
+// into q / k / v, then this kernel normalises and rotates q and k in place and,
+// with a paged cache, writes the k and v rows into it).  One wave per (token,
+// head) over the Hq + 2 * Hkv heads: lane l owns the RoPE pairs (d, d + D/2) for
+// d = l + 64 i, so the rotation is lane-local and the sum of squares is one
+// 64-lane butterfly.  V heads only copy their row into the cache.
 constexpr int kAnyMaxD = 512;
 
 __global__ void __launch_bounds__(kNrWaves * 64)
 norm_rope_any_kernel(EpilogueArgs e, int64_t T) {
   const int lane = threadIdx.x & 63;
-  const int heads = e.Hq + e.Hkv;
+  const int heads = e.Hq + 2 * e.Hkv;
   const int64_t item = int64_t(blockIdx.x) * kNrWaves + (threadIdx.x >> 6);
   if (item >= T * heads) return;
   const int64_t t = item / heads;
   const int h = int(item - t * heads);
-  const bool is_q = h < e.Hq;
-  const int hh = is_q ? h : h - e.Hq;
-  const int H = is_q ? e.Hq : e.Hkv;
+  const int proj = h < e.Hq ? 0 : (h < e.Hq + e.Hkv ? 1 : 2);
+  const int hh = proj == 0 ? h : (proj == 1 ? h - e.Hq : h - e.Hq - e.Hkv);
+  const int H = proj == 0 ? e.Hq : e.Hkv;
   const int hd = e.head_dim, hd2 = hd / 2;
-  uint16_t* row = (is_q ? e.q : e.k) + (t * H + hh) * hd;
-  const uint16_t* gamma = is_q ? e.q_gamma : e.k_gamma;
+  const int64_t slot = proj != 0 ? paged_slot(e, t) : -1;
+  uint16_t* crow = nullptr;  // this head's row in the paged cache (k or v), if any
+  // (arithmetic selects of argument fields: a select of their addresses would copy
+  // the argument struct to scratch memory)
+  if (slot >= 0) crow = pick3<uint16_t>(proj, nullptr, e.k_cache, e.v_cache) + (slot * e.Hkv + hh) * hd;
+  uint16_t* row = pick3<uint16_t>(proj, e.q, e.k, e.v) + (t * H + hh) * hd;
+  if (proj == 2) {  // V: the projection as it is, into the cache
+    if (crow)
+      for (int d = lane; d < hd; d += 64) crow[d] = row[d];
+    return;
+  }
+  const uint16_t* gamma = pick3<const uint16_t>(proj, e.q_gamma, e.k_gamma, e.k_gamma);
   constexpr int kPer = kAnyMaxD / 128;  // pairs per lane at most
   float x1[kPer], x2[kPer];
   float ss = 0.f;
@@ -98,8 +110,13 @@ norm_rope_any_kernel(EpilogueArgs e, int64_t T) {
       const float x2n = x2[i] * rms * bf16_to_f32(gamma[d + hd2]);
       const float c1 = bf16_to_f32(e.cos[prow + d]), c2 = bf16_to_f32(e.cos[prow + d + hd2]);
       const float s1 = bf16_to_f32(e.sin[prow + d]), s2 = bf16_to_f32(e.sin[prow + d + hd2]);
-      row[d] = f32_to_bf16(x1n * c1 - x2n * s1);
-      row[d + hd2] = f32_to_bf16(x2n * c2 + x1n * s2);
+      const uint16_t o1 = f32_to_bf16(x1n * c1 - x2n * s1), o2 = f32_to_bf16(x2n * c2 + x1n * s2);
+      row[d] = o1;
+      row[d + hd2] = o2;
+      if (crow) {
+        crow[d] = o1;
+        crow[d + hd2] = o2;
+      }
     }
   }
 }
@@ -108,7 +125,7 @@ norm_rope_any_kernel(EpilogueArgs e, int64_t T) {
 
 hipError_t launch_norm_rope_any(const EpilogueArgs& e, int64_t T, hipStream_t stream) {
   if (e.head_dim <= 0 || e.head_dim % 8 != 0 || e.head_dim > kAnyMaxD) return hipErrorInvalidValue;
-  const int64_t items = T * (e.Hq + e.Hkv);
+  const int64_t items = T * (e.Hq + 2 * e.Hkv);
   const int64_t blocks = (items + kNrWaves - 1) / kNrWaves;
   if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
   hipLaunchKernelGGL(norm_rope_any_kernel, dim3(unsigned(blocks)), dim3(kNrWaves * 64), 0, stream, e, T);

@@ -10,7 +10,8 @@ RoPE), so the outputs are held to the oracle with the same bf16 rounding of the
 projection (``round_projection=True``) at the acceptance bar (max-abs 2e-2, rel-L2
 1e-2); against the exact projection the rel-L2 bar holds too (the projection's
 rounding moves single elements of |q| ~ 2 by up to ~2.1e-2), in prefill, positions
-and varlen modes.  Head sizes it cannot take raise.
+and varlen modes, with the paged-cache write and with the fused input RMSNorm.
+Head sizes it cannot take raise.
 """
 from __future__ import annotations
 
@@ -81,20 +82,13 @@ def test_any_head_dim_varlen(device):
 
 
 def test_any_head_dim_refusals(device):
-    """Head sizes outside the generic path, and the features it does not offer, raise."""
+    """Head sizes outside the generic path raise (odd multiples of 2, above 512)."""
     import mqk
     for D in (66, 1024):
         case = Case(1, 8, 1024, 4, 2, seed=9200 + D, head_dim=D)
-        with pytest.raises(Exception):
+        with pytest.raises(mqk.MqkNativeError, match=f"head_dim {D} not supported"):
             mqk.fused_qkv_rope(*case.args(device))
             torch.cuda.synchronize()
-    D, Hkv = 256, 2
-    case = Case(1, 8, 1024, 4, Hkv, seed=9300, head_dim=D)
-    x, wq, wk, wv, gq, gk, cos, sin, _ = case.args(device)
-    in_w = torch.ones(1024, dtype=torch.bfloat16, device=device)
-    with pytest.raises(Exception):
-        mqk.fused_qkv_rope_ex(x.view(8, 1024), wq, wk, wv, gq, gk, cos, sin, input_norm_w=in_w)
-        torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("T,round_weight", [(8, False), (40, True)])
@@ -125,3 +119,50 @@ def test_any_head_dim_w4a16(T, round_weight, device):
         assert np.isfinite(o).all(), name
         assert orc.max_abs(o, r) <= MAX_ABS, f"{name} max-abs {orc.max_abs(o, r)}"
         assert orc.rel_l2(o, r) <= REL_L2, f"{name} rel-L2 {orc.rel_l2(o, r)}"
+
+
+def test_any_head_dim_paged_cache(device):
+    """The paged-cache write at head_dim 256 (prefill, two sequences): every cache
+    slot the block table maps holds the returned K / V row bit for bit; the rest
+    of the (sentinel-filled) caches stays untouched."""
+    import mqk
+    D, Hq, Hkv, hidden, B, S, bs = 256, 8, 2, 1024, 2, 40, 16
+    SENTINEL = -7
+    nb = 12
+    g = torch.Generator().manual_seed(9500)
+    bt = torch.randperm(nb, generator=g)[: B * 3].view(B, 3).to(torch.int32)
+    case = Case(B, S, hidden, Hq, Hkv, seed=9501, head_dim=D)
+    x, wq, wk, wv, gq, gk, cos, sin, _ = case.args(device)
+    kc = torch.full((nb, bs, Hkv, D), SENTINEL, dtype=torch.int16, device=device).view(torch.bfloat16)
+    vc = kc.clone()
+    q, k, v = mqk.fused_qkv_rope_ex(x, wq, wk, wv, gq, gk, cos, sin, k_cache=kc, v_cache=vc,
+                                    block_table=bt.to(device))
+    torch.cuda.synchronize()
+    T = B * S
+    seq = np.repeat(np.arange(B), S)
+    pos = np.tile(np.arange(S), B)
+    slots = torch.as_tensor(orc.paged_slot(bt.numpy(), seq, pos, bs, nb), dtype=torch.int64)
+    for name, cache, rows in (("k", kc, k), ("v", vc, v)):
+        flat = cache.view(torch.int16).reshape(-1, Hkv, D).cpu()
+        want = rows.view(torch.int16).reshape(T, Hkv, D).cpu()
+        assert torch.equal(flat[slots], want), f"{name} cache rows differ from the returned rows"
+        mask = torch.ones(flat.shape[0], dtype=torch.bool)
+        mask[slots] = False
+        assert bool((flat[mask] == SENTINEL).all()), f"{name}: a slot outside the table was written"
+    _check((q, k, v), case, np.arange(T), "paged D=256")
+
+
+def test_any_head_dim_input_norm(device):
+    """The fused input RMSNorm at head_dim 96: the op on x equals the op on the
+    oracle-normalised activations, within the acceptance bar."""
+    import mqk
+    D, Hq, Hkv, hidden, T = 96, 16, 4, 2048, 150
+    case = Case(1, T, hidden, Hq, Hkv, seed=9600, head_dim=D, x_std=3.0)
+    x, wq, wk, wv, gq, gk, cos, sin, _ = case.args(device)
+    gam = (1 + 0.3 * torch.randn(hidden, generator=torch.Generator().manual_seed(96))).bfloat16()
+    out = mqk.fused_qkv_rope_ex(x, wq, wk, wv, gq, gk, cos, sin, input_norm_w=gam.to(device))
+    torch.cuda.synchronize()
+    xn = orc.rms_norm_hf(f32(case.x).reshape(T, hidden), f32(gam), 1e-6, round_out=True)
+    normed = Case(1, T, hidden, Hq, Hkv, seed=9600, head_dim=D, x_std=3.0)
+    normed.x = torch.from_numpy(xn.astype(np.float32)).reshape(1, T, hidden).bfloat16()
+    _check([o.reshape(1, T, -1, D) for o in out], normed, np.arange(0, T, 7), "input norm D=96")
