@@ -268,16 +268,18 @@ w4_gemv_lds_kernel(const uint16_t* __restrict__ x, const int32_t* __restrict__ q
       const int64_t i = i0 + lane;
       if (i < groups * 2) dma16(sc + (i / 2) * N + col0 + 8 * (i % 2), lds0 + uint32_t(lay.sc_off + i0 * 16));
     }
+    for (int64_t i0 = int64_t(wave) * 64; i0 < int64_t(M) * K / 8; i0 += kMfmaWaves * 64) {
+      const int64_t i = i0 + lane;
+      if (i < int64_t(M) * K / 8) dma16(x + i * 8, lds0 + uint32_t(lay.x_off + i0 * 16));
+    }
+    // zeros: two words (16 columns) per group, one 8-byte piece per lane, through
+    // VGPRs (their LDS store waits for the load); issued after every direct load of
+    // the workgroup, so that this wave's one round trip overlaps theirs
     if (wave == kMfmaWaves - 1) {
-      // zeros: two words (16 columns) per group; one 8-byte piece per lane, as words
       for (int64_t g = lane; g < groups; g += 64) {
         const u32x2_t zw = *reinterpret_cast<const u32x2_t*>(qz + g * (N / 8) + col0 / 8);
         *reinterpret_cast<u32x2_t*>(g_gemv_x + lay.qz_off + g * 8) = zw;
       }
-    }
-    for (int64_t i0 = int64_t(wave) * 64; i0 < int64_t(M) * K / 8; i0 += kMfmaWaves * 64) {
-      const int64_t i = i0 + lane;
-      if (i < int64_t(M) * K / 8) dma16(x + i * 8, lds0 + uint32_t(lay.x_off + i0 * 16));
     }
     wait_vm<0>();
     __syncthreads();
