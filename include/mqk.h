@@ -147,6 +147,19 @@ int mqk_fused_qkv_rope_f16(const mqk_f16* x, const mqk_f16* w_q, const mqk_f16* 
  * same holds for mqk_fused_qkv_rope_ex_workspace_size. */
 size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden);
 
+/* Workspace bytes for any supported head_dim, with Hq and Hkv the head counts.
+ * For head_dim 128 and 64 it equals mqk_fused_qkv_rope_workspace_size over
+ * 128-column blocks.  Other head sizes run each projection as its own planned
+ * GEMM (decode kernel, decode blocks, split-K or single-head tiles) when the
+ * workspace holds what that plan needs, and on the tile kernels otherwise; this
+ * returns the most any of the three plans needs, for either weight format.  Like
+ * the reference's op, which infers D from the norm weight
+ * (mini_qwen/kernels/fused_qkv_rope.py:155-160), the entry points take any head
+ * size; the reference sizes no workspace, so this query has no counterpart
+ * there.  For the _ex entry points take the larger of this and
+ * mqk_fused_qkv_rope_ex_workspace_size. */
+size_t mqk_fused_qkv_rope_workspace_size_hd(int64_t T, int Hq, int Hkv, int64_t hidden, int head_dim);
+
 /*
  * mqk_fused_qkv_rope_bf16 without a workspace argument: allocates nothing, for
  * callers that cannot call hipMalloc (code under HIP-graph capture, tight

@@ -464,6 +464,18 @@ const char* mqk_error_string(int status) {
 
 const char* mqk_last_error_detail(void) { return g_detail; }
 
+// Workspace bytes run_fused needs for a plain GEMM (bf16 or int4 weights) of
+// `tiles` 128-column blocks (no input norm), as planned for it.
+static size_t plain_plan_bytes(int int4, int64_t M, int64_t K, int tiles, const Topology& topo) {
+  if (tiles > kMaxTiles) return ~size_t(0);
+  if (int4 && M <= g_gemv_max_m.load()) return 0;  // the column-parallel kernel needs none
+  const Plan pl = plan_fused(int4, M, K, tiles, true, topo, true, false, true, false);
+  size_t n = 0;
+  if (pl.splits > 0) n = std::max(n, decode_workspace_bytes(tiles, pl.splits, pl.passes));
+  if (pl.ksplit > 0) n = std::max(n, kDecodeCounterBytes + tile_split_part_bytes(pl.v->id, M, tiles, pl.ksplit));
+  return n;
+}
+
 size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden) {
   if (T <= 0 || Hq <= 0 || Hkv <= 0 || hidden <= 0 || hidden % kBK != 0) return 0;
   const int tiles = Hq + 2 * Hkv;
@@ -474,6 +486,24 @@ size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hid
     if (pl.v && is_pair_variant(pl.v->id)) n = std::max(n, pair_tile_workspace_bytes(pl.v->id, T - pl.tail, tiles));
     if (pl.ksplit > 0) n = std::max(n, kDecodeCounterBytes + tile_split_part_bytes(pl.v->id, T, tiles, pl.ksplit));
   }
+  return n;
+}
+
+size_t mqk_fused_qkv_rope_workspace_size_hd(int64_t T, int Hq, int Hkv, int64_t hidden, int head_dim) {
+  if (T <= 0 || Hq <= 0 || Hkv <= 0 || hidden <= 0 || hidden % kBK != 0 || head_dim <= 0) return 0;
+  if (head_dim == kHeadDim || head_dim == 64)
+    return mqk_fused_qkv_rope_workspace_size(T, int(int64_t(Hq) * head_dim / kHeadDim),
+                                             int(int64_t(Hkv) * head_dim / kHeadDim), hidden);
+  // other head sizes plan each projection of whole 128-column blocks on its own
+  // (either weight format)
+  const Topology topo = device_topology();
+  size_t n = 0;
+  for (int int4 = 0; int4 < 2; ++int4)
+    for (int h : {Hq, Hkv}) {
+      const int64_t N = int64_t(h) * head_dim;
+      if (N % kHeadDim != 0 || N / kHeadDim > kMaxTiles) continue;
+      n = std::max(n, plain_plan_bytes(int4, T, hidden, int(N / kHeadDim), topo));
+    }
   return n;
 }
 
@@ -571,13 +601,6 @@ static int apply_ext(const mqk_fused_ext* ext, const int32_t* positions, int64_t
   return apply_paged(ext->kv, positions, S, T, varlen, e);
 }
 
-// Head sizes the fused kernels do not tile (a multiple of 8 up to 512, other than
-// 64 and 128): the three projections run as plain GEMMs on the tile kernels,
-// written straight into q, k and v, then launch_norm_rope_any normalises and
-// rotates q and k in place.  Like the reference's own composition (a vendor GEMM
-// into bf16 q / k, then its norm + RoPE kernel, fused_qkv_rope.py:166-190), the
-// projections are rounded to bf16 before the norm.  The paged-cache write and the
-// fused input RMSNorm are not offered on this path.
 // Validation and the norm / RoPE arguments of the generic head-size path (below).
 static int any_d_prepare(const mqk_bf16* x, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
                          const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions, int64_t T,
@@ -607,14 +630,17 @@ static int any_d_prepare(const mqk_bf16* x, const mqk_bf16* q_gamma, const mqk_b
 }
 
 // Head sizes the fused kernels do not tile (a multiple of 8 up to 512, other than
-// 64 and 128): the three projections run as plain GEMMs on the tile kernels,
-// written straight into q, k and v, then launch_norm_rope_any normalises and
-// rotates q and k in place.  Like the reference's own composition (a vendor GEMM
-// into bf16 q / k, then its norm + RoPE kernel, fused_qkv_rope.py:166-190), the
-// projections are rounded to bf16 before the norm.  The fused input RMSNorm runs in
-// the GEMMs as in the fused path (per-token scales from the pre-pass, in the
-// workspace after its arrival counters); the paged-cache rows are written by the
-// norm + RoPE launch.
+// 64 and 128): the three projections run as plain GEMMs, written straight into q,
+// k and v, then launch_norm_rope_any normalises and rotates q and k in place.  A
+// projection of whole 128-column blocks goes through the planner (run_fused: the
+// decode kernel, decode blocks, split-K or single-head tiles, as for the fused
+// op) when the workspace holds what its plan needs; otherwise, and with the fused
+// input RMSNorm, it runs on the tile kernels.  Like the reference's own
+// composition (a vendor GEMM into bf16 q / k, then its norm + RoPE kernel,
+// fused_qkv_rope.py:166-190), the projections are rounded to bf16 before the
+// norm.  The fused input RMSNorm runs in the GEMMs as in the fused path (per-token
+// scales from the pre-pass, in the workspace after its arrival counters); the
+// paged-cache rows are written by the norm + RoPE launch.
 static int fused_bf16_any_d(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
                             const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
                             const mqk_bf16* cos, const mqk_bf16* sin, const int32_t* positions,
@@ -649,6 +675,24 @@ static int fused_bf16_any_d(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
   for (int i = 0; i < 3; ++i) {
     const int64_t N = int64_t(heads[i]) * D;  // N % 8 == 0: the tiles store whole 8-column runs below N
     const int tiles = int((N + kHeadDim - 1) / kHeadDim);
+    if (!pn.in_gamma && N % kHeadDim == 0 && aligned16(outs[i]) &&
+        plain_plan_bytes(0, T, hidden, tiles, topo) <= (workspace ? ws_bytes : 0)) {
+      // whole 128-column blocks: the planner's launches for this projection
+      // (decode blocks, split-K or single-head tiles where they are faster)
+      ProblemArgs pp{x, T, hidden, tiles};
+      WeightArgs w{};
+      w.w[0] = wts[i];
+      w.n_cols[0] = N;
+      EpilogueArgs e{};
+      e.qkv = 0;
+      e.Hq = tiles;
+      e.Hkv = 0;
+      e.out = outs[i];
+      e.N = N;
+      e.head_dim = kHeadDim;
+      if ((st = run_fused(0, pp, w, e, 0.f, workspace, ws_bytes, hs)) != MQK_OK) return st;
+      continue;
+    }
     ProblemArgs p{x, T, hidden, tiles};
     p.cus = topo.cus;
     p.xcds = topo.xcds;
@@ -1045,10 +1089,19 @@ static int fused_w4a16_impl(const mqk_bf16* x, const int32_t* qw_q, const void* 
     const int32_t* qzs[3] = {qz_q, qz_k, qz_v};
     mqk_bf16* outs[3] = {q, k, v};
     const int heads[3] = {Hq, Hkv, Hkv};
-    for (int i = 0; i < 3; ++i)
-      if ((st = mqk_w4a16_gemm(x, qws[i], scs[i], qzs[i], T, hidden, int64_t(heads[i]) * D, group, scale_type,
-                               outs[i], stream)) != MQK_OK)
-        return st;
+    const Topology topo = device_topology();
+    for (int i = 0; i < 3; ++i) {
+      // whole 128-column blocks with the workspace their plan needs: the planned
+      // launches (mqk_w4a16_gemm_ex: decode kernel, decode blocks, tiles); else the
+      // column-parallel kernel (M <= 16) or the tile kernels
+      const int64_t N = int64_t(heads[i]) * D;
+      const bool planned = N % kHeadDim == 0 &&
+                           plain_plan_bytes(1, T, hidden, int(N / kHeadDim), topo) <= (workspace ? ws_bytes : 0);
+      st = planned ? mqk_w4a16_gemm_ex(x, qws[i], scs[i], qzs[i], T, hidden, N, group, scale_type, outs[i],
+                                       workspace, ws_bytes, stream)
+                   : mqk_w4a16_gemm(x, qws[i], scs[i], qzs[i], T, hidden, N, group, scale_type, outs[i], stream);
+      if (st != MQK_OK) return st;
+    }
     return hip_status(launch_norm_rope_any(er, T, static_cast<hipStream_t>(stream)), "norm + RoPE launch");
   }
   const bool varlen = ext && ext->cu_seqlens;

@@ -83,6 +83,7 @@ SIGNATURES = {
          _I64, _F, _P, _P, _P, _P],              # cos_rows eps q k v stream
     ),
     "mqk_fused_qkv_rope_workspace_size": (_SZ, [_I64, _I, _I, _I64]),
+    "mqk_fused_qkv_rope_workspace_size_hd": (_SZ, [_I64, _I, _I, _I64, _I]),
     "mqk_fused_qkv_rope_bf16_noalloc": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P,     # x w_q w_k w_v q_gamma k_gamma cos sin positions
@@ -340,6 +341,21 @@ def blocks(heads: int, head_dim: int) -> int:
     """Heads -> the kernels' 128-column blocks (two heads per block at head_dim 64):
     the head counts the workspace-size queries take."""
     return heads * head_dim // 128
+
+
+def fused_workspace_bytes(T: int, H_Q: int, H_KV: int, hidden: int, D: int, ext=None) -> int:
+    """Workspace bytes of one fused call: the fused plan's over 128-column blocks
+    (with ``ext``: the _ex query, which adds the input-norm scales), and for head
+    sizes other than 64 and 128 at least what each projection's own plan needs."""
+    lib = library()
+    if ext is None:
+        n = int(lib.mqk_fused_qkv_rope_workspace_size(T, blocks(H_Q, D), blocks(H_KV, D), hidden))
+    else:
+        n = int(lib.mqk_fused_qkv_rope_ex_workspace_size(T, blocks(H_Q, D), blocks(H_KV, D), hidden,
+                                                         ctypes.byref(ext)))
+    if D not in (64, 128):
+        n = max(n, int(lib.mqk_fused_qkv_rope_workspace_size_hd(T, H_Q, H_KV, hidden, D)))
+    return n
 
 
 def ptr(t) -> int | None:

@@ -149,7 +149,7 @@ def fused_qkv_rope(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), stream)
         _native.check(status, entry)
         return q, k, v
-    nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, _native.blocks(H_Q, D), _native.blocks(H_KV, D), H))
+    nbytes = _native.fused_workspace_bytes(T, H_Q, H_KV, H, D)
     ws = _native.workspace(device, stream, nbytes)
     status = _native.call(
         device, lib.mqk_fused_qkv_rope_bf16,
@@ -248,7 +248,7 @@ def fused_qkv_rope_paged(
         return q, k, v
     lib = _native.library()
     stream = _native.stream_handle(device)
-    nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, _native.blocks(H_Q, D), _native.blocks(H_KV, D), H))
+    nbytes = _native.fused_workspace_bytes(T, H_Q, H_KV, H, D)
     ws = _native.workspace(device, stream, nbytes)
     status = _native.call(device, lib.mqk_fused_qkv_rope_paged_bf16,
         x.data_ptr(), w_q.data_ptr(), w_k.data_ptr(), w_v.data_ptr(),
@@ -385,7 +385,7 @@ def fused_qkv_rope_ex(
         return q, k, v
     lib = _native.library()
     stream = _native.stream_handle(device)
-    nbytes = int(lib.mqk_fused_qkv_rope_ex_workspace_size(T, _native.blocks(H_Q, D), _native.blocks(H_KV, D), H, ctypes.byref(ext)))
+    nbytes = _native.fused_workspace_bytes(T, H_Q, H_KV, H, D, ext)
     ws = _native.workspace(device, stream, nbytes)
     status = _native.call(device, lib.mqk_fused_qkv_rope_ex_bf16,
         x.data_ptr(), w_q.data_ptr(), w_k.data_ptr(), w_v.data_ptr(),

@@ -59,11 +59,34 @@ def test_any_head_dim_matches_oracle(D, Hq, Hkv, hidden, B, S, positions, device
     case = Case(B, S, hidden, Hq, Hkv, seed=9000 + D, head_dim=D, rows=4096 if positions else None, positions=pos)
     args = case.args(device)
     kernels = launched_kernels(lambda: mqk.fused_qkv_rope(*args))
-    assert len(kernels) == 4 and kernels[-1] == "norm_rope_any", kernels
+    # (each projection: the launches its plan takes, e.g. a tile launch and a tail)
+    assert len(kernels) >= 4 and kernels[-1] == "norm_rope_any" and "norm_rope_any" not in kernels[:-1], kernels
     out = mqk.fused_qkv_rope(*args)
     torch.cuda.synchronize()
     idx = np.unique(np.concatenate([[0, T - 1], np.random.default_rng(D).choice(T, min(T, 24), replace=False)]))
     _check(out, case, idx, f"D={D} Hq={Hq} Hkv={Hkv} T={T}")
+
+
+@pytest.mark.parametrize("T,expect", [(8, "decode"), (48, "decode"), (600, None)])
+def test_any_head_dim_planned_projections(T, expect, device):
+    """Projections of whole 128-column blocks take the planner's launches: at
+    decode sizes the split-K decode kernel streams each projection's weights over
+    every CU (a tile launch would give the few tiles one CU each).  Held to the
+    oracle as above; the bf16 decode and tile plans of one projection agree with
+    each other only to rounding, so only the oracle decides."""
+    import mqk
+    D, Hq, Hkv, hidden = 256, 16, 4, 4096
+    pos = torch.randint(0, 4096, (T,), generator=torch.Generator().manual_seed(T), dtype=torch.int32)
+    case = Case(T, 1, hidden, Hq, Hkv, seed=9050 + T, head_dim=D, rows=4096, positions=pos)
+    args = case.args(device)
+    kernels = launched_kernels(lambda: mqk.fused_qkv_rope(*args))
+    assert kernels[-1] == "norm_rope_any" and "norm_rope_any" not in kernels[:-1], kernels
+    if expect:
+        assert kernels[:-1] == [expect] * 3, kernels
+    out = mqk.fused_qkv_rope(*args)
+    torch.cuda.synchronize()
+    idx = np.unique(np.concatenate([[0, T - 1], np.random.default_rng(T).choice(T, min(T, 24), replace=False)]))
+    _check(out, case, idx, f"planned D=256 T={T}")
 
 
 def test_any_head_dim_varlen(device):
@@ -108,7 +131,7 @@ def test_any_head_dim_w4a16(T, round_weight, device):
     projs = [tuple(t.to(device) for t in mqk.per_group_minmax_quantize(w.float().T.contiguous(), 128, torch.bfloat16))
              for w in (case.w_q, case.w_k, case.w_v)]
     kernels = launched_kernels(lambda: mqk.fused_qkv_rope_w4a16(args[0], *projs, *args[4:]))
-    assert len(kernels) == 4 and kernels[-1] == "norm_rope_any", kernels
+    assert len(kernels) >= 4 and kernels[-1] == "norm_rope_any" and "norm_rope_any" not in kernels[:-1], kernels
     out = mqk.fused_qkv_rope_w4a16(args[0], *projs, *args[4:])
     torch.cuda.synchronize()
     x2 = f32(case.x).reshape(T, hidden)

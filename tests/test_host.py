@@ -586,3 +586,27 @@ def test_f16_validation(lib):
     assert f(hidden=48) == -3
     assert f(x=None) == -1
     assert f(T=0) == 0
+
+
+def test_workspace_size_any_head_dim(lib):
+    """mqk_fused_qkv_rope_workspace_size_hd: at head_dim 128 and 64 the fused
+    plan's bytes over 128-column blocks; at other head sizes what the three
+    projections' own plans need (the decode kernel's counters and partials at
+    decode sizes, none where single-head tiles take every projection)."""
+    from mqk import _native
+    for T in (1, 8, 256, 2048):
+        assert lib.mqk_fused_qkv_rope_workspace_size_hd(T, 32, 8, 4096, 128) == \
+            lib.mqk_fused_qkv_rope_workspace_size(T, 32, 8, 4096)
+        assert lib.mqk_fused_qkv_rope_workspace_size_hd(T, 32, 8, 4096, 64) == \
+            lib.mqk_fused_qkv_rope_workspace_size(T, 16, 4, 4096)
+    assert lib.mqk_fused_qkv_rope_workspace_size_hd(0, 16, 4, 4096, 256) == 0
+    assert lib.mqk_fused_qkv_rope_workspace_size_hd(8, 16, 4, 4000, 256) == 0  # hidden % 64 != 0
+    if _native.get_option("device_cus") != 256:
+        pytest.skip("the plan depends on the device's CU count (256 on MI355X)")
+    # T = 8, head_dim 256: each projection runs on the split-K decode kernel, whose
+    # counters and partials the workspace holds
+    n = lib.mqk_fused_qkv_rope_workspace_size_hd(8, 16, 4, 4096, 256)
+    assert n >= 4096 + 256 + 512 * 128
+    # the Python front takes the larger of the fused and the per-projection sizes
+    assert _native.fused_workspace_bytes(8, 16, 4, 4096, 256) >= n
+    assert _native.fused_workspace_bytes(8, 32, 8, 4096, 128) == lib.mqk_fused_qkv_rope_workspace_size(8, 32, 8, 4096)
