@@ -149,10 +149,15 @@ size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hid
 
 /* Workspace bytes for any supported head_dim, with Hq and Hkv the head counts.
  * For head_dim 128 and 64 it equals mqk_fused_qkv_rope_workspace_size over
- * 128-column blocks.  Other head sizes run each projection as its own planned
- * GEMM (decode kernel, decode blocks, split-K or single-head tiles) when the
- * workspace holds what that plan needs, and on the tile kernels otherwise; this
- * returns the most any of the three plans needs, for either weight format.  Like
+ * 128-column blocks.  Other head sizes with bf16 weights whose q and k / v
+ * widths (Hq * head_dim, Hkv * head_dim) are whole 128-column blocks run the
+ * three projections as one launch of the fused op's plan over those blocks
+ * (decode kernel, decode blocks, split-K, single-head or pair tiles), q and k
+ * stored as projected, then the norm + RoPE launch; otherwise each projection
+ * of whole blocks is planned on its own (W4A16 always), and the rest run on the
+ * tile kernels.  Each runs its planned form when the workspace holds what that
+ * plan needs, and the tile kernels otherwise; this returns the most they need,
+ * for either weight format.  Like
  * the reference's op, which infers D from the norm weight
  * (mini_qwen/kernels/fused_qkv_rope.py:155-160), the entry points take any head
  * size; the reference sizes no workspace, so this query has no counterpart

@@ -464,16 +464,23 @@ const char* mqk_error_string(int status) {
 
 const char* mqk_last_error_detail(void) { return g_detail; }
 
-// Workspace bytes run_fused needs for a plain GEMM (bf16 or int4 weights) of
-// `tiles` 128-column blocks (no input norm), as planned for it.
-static size_t plain_plan_bytes(int int4, int64_t M, int64_t K, int tiles, const Topology& topo) {
+// Workspace bytes run_fused's plan of `tiles` 128-column blocks needs (before
+// any input-norm scales): a plain GEMM (bf16 or int4 weights, no pair tiles), or
+// with allow_pair the q/k/v launch of the generic head sizes.
+static size_t plan_bytes(int int4, int64_t M, int64_t K, int tiles, const Topology& topo, bool in_norm,
+                         bool allow_pair) {
   if (tiles > kMaxTiles) return ~size_t(0);
-  if (int4 && M <= g_gemv_max_m.load()) return 0;  // the column-parallel kernel needs none
-  const Plan pl = plan_fused(int4, M, K, tiles, true, topo, true, false, true, false);
+  const Plan pl = plan_fused(int4, M, K, tiles, true, topo, true, in_norm, true, allow_pair);
   size_t n = 0;
   if (pl.splits > 0) n = std::max(n, decode_workspace_bytes(tiles, pl.splits, pl.passes));
   if (pl.ksplit > 0) n = std::max(n, kDecodeCounterBytes + tile_split_part_bytes(pl.v->id, M, tiles, pl.ksplit));
+  if (pl.v && is_pair_variant(pl.v->id)) n = std::max(n, pair_tile_workspace_bytes(pl.v->id, M - pl.tail, tiles));
   return n;
+}
+
+static size_t plain_plan_bytes(int int4, int64_t M, int64_t K, int tiles, const Topology& topo) {
+  if (int4 && M <= g_gemv_max_m.load()) return 0;  // the column-parallel kernel needs none
+  return plan_bytes(int4, M, K, tiles, topo, false, false);
 }
 
 size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hidden) {
@@ -494,10 +501,14 @@ size_t mqk_fused_qkv_rope_workspace_size_hd(int64_t T, int Hq, int Hkv, int64_t 
   if (head_dim == kHeadDim || head_dim == 64)
     return mqk_fused_qkv_rope_workspace_size(T, int(int64_t(Hq) * head_dim / kHeadDim),
                                              int(int64_t(Hkv) * head_dim / kHeadDim), hidden);
-  // other head sizes plan each projection of whole 128-column blocks on its own
-  // (either weight format)
+  // other head sizes: bf16 weights whose q and k/v widths are whole 128-column
+  // blocks run all three projections in one launch of the fused kernels' plan;
+  // otherwise (and W4A16) each projection of whole blocks is planned on its own
   const Topology topo = device_topology();
   size_t n = 0;
+  if ((int64_t(Hq) * head_dim) % kHeadDim == 0 && (int64_t(Hkv) * head_dim) % kHeadDim == 0)
+    n = plan_bytes(0, T, hidden, int((int64_t(Hq) + 2 * Hkv) * head_dim / kHeadDim), topo, false, true);
+  if (n == ~size_t(0)) n = 0;
   for (int int4 = 0; int4 < 2; ++int4)
     for (int h : {Hq, Hkv}) {
       const int64_t N = int64_t(h) * head_dim;
@@ -630,12 +641,14 @@ static int any_d_prepare(const mqk_bf16* x, const mqk_bf16* q_gamma, const mqk_b
 }
 
 // Head sizes the fused kernels do not tile (a multiple of 8 up to 512, other than
-// 64 and 128): the three projections run as plain GEMMs, written straight into q,
-// k and v, then launch_norm_rope_any normalises and rotates q and k in place.  A
-// projection of whole 128-column blocks goes through the planner (run_fused: the
-// decode kernel, decode blocks, split-K or single-head tiles, as for the fused
-// op) when the workspace holds what its plan needs; otherwise, and with the fused
-// input RMSNorm, it runs on the tile kernels.  Like the reference's own
+// 64 and 128): the three projections are written straight into q, k and v, then
+// launch_norm_rope_any normalises and rotates q and k in place.  When the q and
+// k / v widths are whole 128-column blocks they run as one launch of the fused
+// op's plan over those blocks (run_fused with qkv 2: q and k stored as
+// projected); otherwise a projection of whole blocks goes through the planner on
+// its own (run_fused, plain epilogue), and the others, and the fused input RMSNorm
+// of that route, run on the tile kernels.  A planned form runs only when the
+// workspace holds what its plan needs.  Like the reference's own
 // composition (a vendor GEMM into bf16 q / k, then its norm + RoPE kernel,
 // fused_qkv_rope.py:166-190), the projections are rounded to bf16 before the
 // norm.  The fused input RMSNorm runs in the GEMMs as in the fused path (per-token
@@ -656,6 +669,39 @@ static int fused_bf16_any_d(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf
     return fail(MQK_ERR_MISALIGNED, "weights must be 16-byte aligned");
   const Topology topo = device_topology();
   const hipStream_t hs = static_cast<hipStream_t>(stream);
+  const int64_t nq = int64_t(Hq) * D, nkv = int64_t(Hkv) * D;
+  if (nq % kHeadDim == 0 && nkv % kHeadDim == 0) {
+    // q and k/v widths of whole 128-column blocks: one launch of the fused
+    // kernels' plan for all three projections over those blocks, q and k stored
+    // as projected (qkv 2), when the workspace holds what that plan needs
+    const bool in_norm = ext && ext->in_gamma;
+    const int tiles = int((nq + 2 * nkv) / kHeadDim);
+    const size_t need = plan_bytes(0, T, hidden, tiles, topo, in_norm, true);
+    const size_t scales = in_norm ? align_up(size_t(T) * sizeof(float), 256) : 0;
+    const bool fits = need != ~size_t(0) &&
+                      ((need == 0 && !in_norm) ||
+                       (workspace && align_up(need > 0 ? need : decode_counter_bytes(), 256) + scales <= ws_bytes));
+    if (fits) {
+      ProblemArgs pr{x, T, hidden, tiles};
+      pr.in_gamma = in_norm ? ext->in_gamma : nullptr;
+      WeightArgs w{};
+      w.w[0] = w_q;
+      w.w[1] = w_k;
+      w.w[2] = w_v;
+      w.n_cols[0] = nq;
+      w.n_cols[1] = nkv;
+      w.n_cols[2] = nkv;
+      EpilogueArgs e = er;
+      e.qkv = 2;
+      e.Hq = int(nq / kHeadDim);
+      e.Hkv = int(nkv / kHeadDim);
+      e.head_dim = kHeadDim;
+      e.k_cache = nullptr;  // (the paged rows are written by the norm + RoPE launch)
+      e.v_cache = nullptr;
+      if ((st = run_fused(0, pr, w, e, in_norm ? ext->in_eps : 0.f, workspace, ws_bytes, hs)) != MQK_OK) return st;
+      return hip_status(launch_norm_rope_any(er, T, hs), "norm + RoPE launch");
+    }
+  }
   ProblemArgs pn{x, T, hidden, 0};
   if (ext && ext->in_gamma) {
     if ((st = apply_ext(ext, positions, S, T, pn, er)) != MQK_OK) return st;  // (in_gamma checks)

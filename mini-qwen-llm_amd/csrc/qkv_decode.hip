@@ -366,7 +366,7 @@ __device__ __forceinline__ void finish_block(const ProblemArgs& p, const WeightA
   const int hd = e.head_dim;
   const PairRuns pr = pair_runs(c, hd);  // (head_dim 64: two heads per block, see pair_runs)
   const int rr = blk * kDecRows + r;  // this thread's row of the launch
-  const bool qk = e.qkv && d.proj != 2;
+  const bool qk = e.qkv == 1 && d.proj != 2;  // (qkv 2: q and k stored as projected)
   f32x4_t sum[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) sum[mb] = f32x4_t{};
@@ -642,7 +642,7 @@ __device__ __forceinline__ uint32_t arrive(uint32_t* counter, const DecWork& d) 
 __device__ __forceinline__ void block_rows(const EpilogueArgs& e, const DecWork& d, int M, int b, int64_t& prow,
                                            int64_t& cslot) {
   const int rr = b * kDecRows + (threadIdx.x >> 3);
-  prow = (e.qkv && d.proj != 2 && rr < M) ? rope_row(e, rr) * e.head_dim : 0;
+  prow = (e.qkv == 1 && d.proj != 2 && rr < M) ? rope_row(e, rr) * e.head_dim : 0;
   cslot = (e.qkv && d.proj != 0 && rr < M) ? paged_slot(e, rr) : -1;
 }
 

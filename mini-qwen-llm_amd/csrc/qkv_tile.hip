@@ -75,7 +75,7 @@ __device__ __forceinline__ void store_block(const f32x16_t (&acc)[4], int64_t ro
   const int H = proj == 0 ? e.Hq : e.Hkv;
   uint16_t* __restrict__ dst = pick3(proj, e.q, e.k, e.v);
 
-  if (proj == 2) {  // V: plain projection (fused_qkv_rope.py:169, :194)
+  if (proj == 2 || e.qkv == 2) {  // V (fused_qkv_rope.py:169, :194), or any head with qkv 2: as projected
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int64_t t = row_base + 8 * (i >> 2) + 4 * half + (i & 3);

@@ -255,7 +255,7 @@ __device__ __forceinline__ void tile_epilogue(const AV (&acc)[MB][NB], const Row
         lo[4 * v] = a.x; lo[4 * v + 1] = a.y; lo[4 * v + 2] = a.z; lo[4 * v + 3] = a.w;
         hi[4 * v] = b.x; hi[4 * v + 1] = b.y; hi[4 * v + 2] = b.z; hi[4 * v + 3] = b.w;
       }
-      if (e.qkv && proj != 2) {
+      if (e.qkv == 1 && proj != 2) {  // (qkv 2: q and k stored as projected)
         // RMSNorm over the head (fused_qkv_rope.py:98-100), then rotate-half RoPE (:102-118)
         const float ss = head_sum(run_sumsq(lo, hi), hd);
         const float rms = head_rms(ss, e.eps, hd);
@@ -343,7 +343,7 @@ __device__ __forceinline__ void finish_unit_rows(const float* tile, int pitch, i
       hi[4 * v] = b.x; hi[4 * v + 1] = b.y; hi[4 * v + 2] = b.z; hi[4 * v + 3] = b.w;
     }
     const bool valid = t < p.M;
-    if (e.qkv && proj != 2) {
+    if (e.qkv == 1 && proj != 2) {
       const float ss = head_sum(run_sumsq(lo, hi), hd);
       const float rms = head_rms(ss, e.eps, hd);
       const int64_t base = (valid ? rope_row(e, t) : 0) * hd;
@@ -453,7 +453,7 @@ __device__ __forceinline__ void pair_epilogue(const AV (&acc)[MB][NB], RowV prow
   __shared__ uint32_t xword;
   int proj, hh;
   split_head(h_pair + NH, e.Hq, e.Hkv, proj, hh);
-  const bool qk = e.qkv && proj != 2;
+  const bool qk = e.qkv == 1 && proj != 2;
   const int head0 = h_pair + side * (NH + 1);
   // RoPE table rows and paged-KV-cache slots of the whole-head epilogue's rows
   // (tid / 8 + q * THREADS / 8)
