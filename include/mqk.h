@@ -94,11 +94,13 @@ const char* mqk_last_error_detail(void);
  * (the projection is not rounded to bf16 before the norm), one bf16 rounding
  * per output.
  * Other head sizes that are a multiple of 8 up to 512 (e.g. 80, 96, 192, 256) run
- * as the reference composes the op (fused_qkv_rope.py:166-190): three plain GEMM
- * launches into q / k / v (the projection rounded to bf16), then one QK-Norm +
- * RoPE launch in place on q and k (which also writes the paged-cache rows); the
- * workspace holds only the input RMSNorm's per-token scales, and k / v must be
- * given even with a paged cache.
+ * as the reference composes the op (fused_qkv_rope.py:166-190): the projections
+ * into q / k / v (rounded to bf16; one launch of the fused plan with q and k
+ * stored as projected where Hq * D and Hkv * D are whole 128-column blocks, else
+ * one or more launches per projection), then one QK-Norm + RoPE launch in place
+ * on q and k (which also writes the paged-cache rows).  Size the workspace with
+ * mqk_fused_qkv_rope_workspace_size_hd (a smaller one runs the tile kernels);
+ * k / v must be given even with a paged cache.
  */
 int mqk_fused_qkv_rope_bf16(const mqk_bf16* x, const mqk_bf16* w_q, const mqk_bf16* w_k,
                             const mqk_bf16* w_v, const mqk_bf16* q_gamma, const mqk_bf16* k_gamma,
@@ -149,16 +151,16 @@ size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hid
 
 /* Workspace bytes for any supported head_dim, with Hq and Hkv the head counts.
  * For head_dim 128 and 64 it equals mqk_fused_qkv_rope_workspace_size over
- * 128-column blocks.  Other head sizes with bf16 weights whose q and k / v
- * widths (Hq * head_dim, Hkv * head_dim) are whole 128-column blocks run the
- * three projections as one launch of the fused op's plan over those blocks
- * (decode kernel, decode blocks, split-K, single-head or pair tiles), q and k
- * stored as projected, then the norm + RoPE launch; otherwise each projection
- * of whole blocks is planned on its own (W4A16 always), and the rest run on the
- * tile kernels.  Each runs its planned form when the workspace holds what that
- * plan needs, and the tile kernels otherwise; this returns the most they need,
- * for either weight format.  Like
- * the reference's op, which infers D from the norm weight
+ * 128-column blocks.  Other head sizes whose q and k / v widths (Hq * head_dim,
+ * Hkv * head_dim) are whole 128-column blocks run the three projections as one
+ * launch of the fused op's plan over those blocks (decode kernel, decode
+ * blocks, split-K, single-head or pair tiles), q and k stored as projected,
+ * then the norm + RoPE launch; otherwise each projection of whole blocks is
+ * planned on its own, and the rest run on the tile kernels (W4A16 up to 16
+ * rows: the column-parallel kernel).  Each runs its planned form when the
+ * workspace holds what that plan needs, and the tile kernels otherwise; this
+ * returns the most they need, for either weight format.  Like the reference's
+ * op, which infers D from the norm weight
  * (mini_qwen/kernels/fused_qkv_rope.py:155-160), the entry points take any head
  * size; the reference sizes no workspace, so this query has no counterpart
  * there.  For the _ex entry points take the larger of this and

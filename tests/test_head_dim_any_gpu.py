@@ -128,21 +128,25 @@ def test_any_head_dim_refusals(device):
             torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("T,round_weight", [(8, False), (40, True)])
-def test_any_head_dim_w4a16(T, round_weight, device):
-    """The W4A16 front at head_dim 96: the three W4A16 GEMMs into q / k / v (the
-    column-parallel kernel at T <= 16, which keeps the dequantised weight exact;
-    the int4 tiles above, which round it to bf16), then the norm + RoPE launch,
-    against the oracle with the same weight and projection rounding."""
+@pytest.mark.parametrize("T,Hkv,round_weight,expect", [(8, 4, True, ["decode"]), (40, 4, True, ["decode"]),
+                                                       (8, 2, False, ["gemv"] * 3)])
+def test_any_head_dim_w4a16(T, Hkv, round_weight, expect, device):
+    """The W4A16 front at head_dim 96: the projections into q / k / v, then the
+    norm + RoPE launch, against the oracle with the same weight and projection
+    rounding.  With 4 KV heads (q 1536, k / v 384 columns: whole 128-column
+    blocks) one launch of the fused int4 plan, which rounds the dequantised
+    weight to bf16, with q and k stored as projected; with 2 (k / v 192 columns)
+    at T = 8, three column-parallel GEMMs, which keep it exact."""
     import mqk
-    D, Hq, Hkv, hidden = 96, 16, 4, 1024
+    D, Hq, hidden = 96, 16, 1024
     pos = torch.randint(0, 2048, (T,), generator=torch.Generator().manual_seed(T), dtype=torch.int32)
-    case = Case(T, 1, hidden, Hq, Hkv, seed=9400 + T, head_dim=D, rows=2048, positions=pos)
+    case = Case(T, 1, hidden, Hq, Hkv, seed=9400 + T + Hkv, head_dim=D, rows=2048, positions=pos)
     args = case.args(device)
     projs = [tuple(t.to(device) for t in mqk.per_group_minmax_quantize(w.float().T.contiguous(), 128, torch.bfloat16))
              for w in (case.w_q, case.w_k, case.w_v)]
     kernels = launched_kernels(lambda: mqk.fused_qkv_rope_w4a16(args[0], *projs, *args[4:]))
-    assert len(kernels) >= 4 and kernels[-1] == "norm_rope_any" and "norm_rope_any" not in kernels[:-1], kernels
+    assert kernels[-1] == "norm_rope_any" and "norm_rope_any" not in kernels[:-1], kernels
+    assert kernels[:-1] == expect, kernels
     out = mqk.fused_qkv_rope_w4a16(args[0], *projs, *args[4:])
     torch.cuda.synchronize()
     x2 = f32(case.x).reshape(T, hidden)
