@@ -159,7 +159,9 @@ size_t mqk_fused_qkv_rope_workspace_size(int64_t T, int Hq, int Hkv, int64_t hid
  * planned on its own, and the rest run on the tile kernels (W4A16 up to 16
  * rows: the column-parallel kernel).  Each runs its planned form when the
  * workspace holds what that plan needs, and the tile kernels otherwise; this
- * returns the most they need, for either weight format.  Like the reference's
+ * returns the most they need, for either weight format, with or without the
+ * fused input RMSNorm (which, for W4A16 weights at these head sizes, needs the
+ * one-launch form: whole 128-column widths).  Like the reference's
  * op, which infers D from the norm weight
  * (mini_qwen/kernels/fused_qkv_rope.py:155-160), the entry points take any head
  * size; the reference sizes no workspace, so this query has no counterpart

@@ -508,9 +508,13 @@ size_t mqk_fused_qkv_rope_workspace_size_hd(int64_t T, int Hq, int Hkv, int64_t 
   size_t n = 0;
   if ((int64_t(Hq) * head_dim) % kHeadDim == 0 && (int64_t(Hkv) * head_dim) % kHeadDim == 0)
     for (int int4 = 0; int4 < 2; ++int4) {
-      const size_t m = plan_bytes(int4, T, hidden, int((int64_t(Hq) + 2 * Hkv) * head_dim / kHeadDim), topo, false,
-                                  true);
+      const int tiles = int((int64_t(Hq) + 2 * Hkv) * head_dim / kHeadDim);
+      const size_t m = plan_bytes(int4, T, hidden, tiles, topo, false, true);
       if (m != ~size_t(0)) n = std::max(n, m);
+      // (with the fused input RMSNorm: that plan, then the per-token scales)
+      const size_t mn = plan_bytes(int4, T, hidden, tiles, topo, true, true);
+      if (mn != ~size_t(0))
+        n = std::max(n, align_up(mn > 0 ? mn : decode_counter_bytes(), 256) + align_up(size_t(T) * sizeof(float), 256));
     }
   for (int int4 = 0; int4 < 2; ++int4)
     for (int h : {Hq, Hkv}) {
@@ -1125,10 +1129,8 @@ static int fused_w4a16_impl(const mqk_bf16* x, const int32_t* qw_q, const void* 
                             int64_t cos_rows, float eps, mqk_bf16* q, mqk_bf16* k, mqk_bf16* v,
                             const mqk_fused_ext* ext, void* workspace, size_t ws_bytes, void* stream) {
   if (D > 0 && D % 2 == 0 && D != kHeadDim && D != 64) {
-    // the generic head-size path, as fused_bf16_any_d, with the W4A16 GEMMs (which
-    // take no input norm)
-    if (ext && ext->in_gamma)
-      return fail(MQK_ERR_UNSUPPORTED, "head_dim %d: the W4A16 front's input RMSNorm needs head_dim 64 or 128", D);
+    // the generic head-size path, as fused_bf16_any_d, with int4 weights
+    const bool in_norm = ext && ext->in_gamma;
     EpilogueArgs er{};
     int st = any_d_prepare(x, q_gamma, k_gamma, cos, sin, positions, T, S, hidden, Hq, Hkv, D, cos_rows, eps, q,
                            k, v, ext, er);
@@ -1151,9 +1153,13 @@ static int fused_w4a16_impl(const mqk_bf16* x, const int32_t* qw_q, const void* 
             MQK_OK)
           return st;
       const int tiles = int((nq + 2 * nkv) / kHeadDim);
-      const size_t need = plan_bytes(1, T, hidden, tiles, topo, false, true);
-      if (need != ~size_t(0) && (need == 0 || (workspace && align_up(need, 256) <= ws_bytes))) {
+      const size_t need = plan_bytes(1, T, hidden, tiles, topo, in_norm, true);
+      const size_t scales = in_norm ? align_up(size_t(T) * sizeof(float), 256) : 0;
+      if (need != ~size_t(0) &&
+          ((need == 0 && !in_norm) ||
+           (workspace && align_up(need > 0 ? need : decode_counter_bytes(), 256) + scales <= ws_bytes))) {
         ProblemArgs pr{x, T, hidden, tiles};
+        pr.in_gamma = in_norm ? ext->in_gamma : nullptr;
         WeightArgs w{};
         for (int i = 0; i < 3; ++i) {
           w.qw[i] = qws[i];
@@ -1172,10 +1178,16 @@ static int fused_w4a16_impl(const mqk_bf16* x, const int32_t* qw_q, const void* 
         e.k_cache = nullptr;  // (the paged rows are written by the norm + RoPE launch)
         e.v_cache = nullptr;
         const hipStream_t hs = static_cast<hipStream_t>(stream);
-        if ((st = run_fused(1, pr, w, e, 0.f, workspace, ws_bytes, hs)) != MQK_OK) return st;
+        if ((st = run_fused(1, pr, w, e, in_norm ? ext->in_eps : 0.f, workspace, ws_bytes, hs)) != MQK_OK) return st;
         return hip_status(launch_norm_rope_any(er, T, hs), "norm + RoPE launch");
       }
     }
+    // (the per-projection W4A16 GEMMs take no input norm)
+    if (in_norm)
+      return fail(MQK_ERR_UNSUPPORTED,
+                  "head_dim %d: the W4A16 front's input RMSNorm needs Hq * head_dim and Hkv * head_dim to be "
+                  "multiples of 128 and a workspace of mqk_fused_qkv_rope_ex_workspace_size bytes",
+                  D);
     for (int i = 0; i < 3; ++i) {
       // whole 128-column blocks with the workspace their plan needs: the planned
       // launches (mqk_w4a16_gemm_ex: decode kernel, decode blocks, tiles); else the

@@ -276,9 +276,9 @@ def _fused_w4a16(x, q_proj, k_proj, v_proj, q_norm_w, k_norm_w, cos, sin, positi
     lib = _native.library()
     stream = _native.stream_handle(device)
     if ext is not None:
-        nbytes = int(lib.mqk_fused_qkv_rope_ex_workspace_size(T, _native.blocks(H_Q, D), _native.blocks(H_KV, D), H, ctypes.byref(ext)))
+        nbytes = _native.fused_workspace_bytes(T, H_Q, H_KV, H, D, ext)
     else:
-        nbytes = int(lib.mqk_fused_qkv_rope_workspace_size(T, _native.blocks(H_Q, D), _native.blocks(H_KV, D), H))
+        nbytes = _native.fused_workspace_bytes(T, H_Q, H_KV, H, D)
     ws = _native.workspace(device, stream, nbytes)
     flat = [t.data_ptr() for trio in parts for t in trio]
     head = (x.data_ptr(), *flat, group_size, sts[0],

@@ -207,3 +207,43 @@ def test_any_head_dim_input_norm(device):
     normed = Case(1, T, hidden, Hq, Hkv, seed=9600, head_dim=D, x_std=3.0)
     normed.x = torch.from_numpy(xn.astype(np.float32)).reshape(1, T, hidden).bfloat16()
     _check([o.reshape(1, T, -1, D) for o in out], normed, np.arange(0, T, 7), "input norm D=96")
+
+
+@pytest.mark.parametrize("T", [8, 150])
+def test_any_head_dim_w4a16_input_norm(T, device):
+    """The W4A16 front's fused input RMSNorm at head_dim 96 (q 1536 and k / v 384
+    columns: one launch of the fused int4 plan, its per-token scales from the
+    pre-pass): against the oracle on the normalised activations, the weight
+    dequantised and rounded to bf16 as the int4 kernels do, the projection
+    rounded to bf16.  With k / v widths that are not whole 128-column blocks it
+    raises."""
+    import mqk
+    D, Hq, Hkv, hidden = 96, 16, 4, 1024
+    pos = torch.randint(0, 2048, (T,), generator=torch.Generator().manual_seed(T), dtype=torch.int32)
+    case = Case(T, 1, hidden, Hq, Hkv, seed=9700 + T, head_dim=D, rows=2048, positions=pos, x_std=3.0)
+    args = case.args(device)
+    projs = [tuple(t.to(device) for t in mqk.per_group_minmax_quantize(w.float().T.contiguous(), 128, torch.bfloat16))
+             for w in (case.w_q, case.w_k, case.w_v)]
+    gam = (1 + 0.3 * torch.randn(hidden, generator=torch.Generator().manual_seed(97))).bfloat16()
+    out = mqk.fused_qkv_rope_w4a16_ex(args[0], *projs, *args[4:8], positions=args[8], input_norm_w=gam.to(device))
+    torch.cuda.synchronize()
+    xn = orc.rms_norm_hf(f32(case.x).reshape(T, hidden), f32(gam), 1e-6, round_out=True)
+    raw = [orc.round_bf16(orc.w4a16_gemm(xn, p[0].cpu().numpy(), p[1].float().cpu().numpy(), p[2].cpu().numpy(),
+                                         128, np.float64, True)) for p in projs]
+    rows = pos.numpy()
+    q = orc.qk_norm_rope(raw[0].reshape(T, Hq, D), f32(case.q_norm_w), f32(case.cos), f32(case.sin), 1, rows)
+    k = orc.qk_norm_rope(raw[1].reshape(T, Hkv, D), f32(case.k_norm_w), f32(case.cos), f32(case.sin), 1, rows)
+    for name, o, r in zip("qkv", out, (q, k, raw[2].reshape(T, Hkv, D))):
+        o = f32(o).reshape(r.shape)
+        assert np.isfinite(o).all(), name
+        assert orc.max_abs(o, r) <= MAX_ABS, f"{name} max-abs {orc.max_abs(o, r)}"
+        assert orc.rel_l2(o, r) <= REL_L2, f"{name} rel-L2 {orc.rel_l2(o, r)}"
+    # k / v of 2 heads x 96 = 192 columns: the per-projection GEMMs take no input norm
+    case2 = Case(T, 1, hidden, Hq, 2, seed=9800 + T, head_dim=D, rows=2048, positions=pos)
+    a2 = case2.args(device)
+    p2 = [tuple(t.to(device) for t in mqk.per_group_minmax_quantize(w.float().T.contiguous(), 128, torch.bfloat16))
+          for w in (case2.w_q, case2.w_k, case2.w_v)]
+    with pytest.raises(mqk.MqkNativeError, match="input RMSNorm needs"):
+        mqk.fused_qkv_rope_w4a16_ex(a2[0], *p2, *a2[4:8], positions=a2[8],
+                                    input_norm_w=gam.to(device))
+        torch.cuda.synchronize()
